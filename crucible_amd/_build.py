@@ -1,0 +1,79 @@
+"""Build the gfx950 shared library and the host-only paging test binary.
+
+``build_library()`` compiles every source under ``csrc/`` with hipcc for gfx950 into
+``crucible_amd/libcrucible_attn.so`` (objects under ``crucible_amd/_build/``).
+``build_paging_kat()`` builds ``_build/paging_kat`` with g++ (no HIP), the C++ port of
+the reference's paging unit tests.
+"""
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+BUILD = os.path.join(HERE, "_build")
+LIB_PATH = os.path.join(HERE, "libcrucible_attn.so")
+KAT_PATH = os.path.join(BUILD, "paging_kat")
+
+ARCH = "gfx950"
+DEVICE_SOURCES = ["kv_append.hip", "attn_decode.hip", "attn_prefill.hip", "abi_common.cpp",
+                  "paging.cpp"]
+# Packed-FP32 instructions stay off: hipcc would otherwise form v_pk_* f32 ops on its own.
+HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+               "-Wall", "-Wno-unused-function"]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found: the crucible_amd library needs ROCm's hipcc")
+
+
+def _run(cmd):
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n"
+                           f"{proc.stdout}\n{proc.stderr}")
+    return proc
+
+
+def build_library(jobs: int = 8) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    hipcc = _hipcc()
+    objs = []
+    cmds = []
+    for src in DEVICE_SOURCES:
+        obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+        objs.append(obj)
+        lang = ["-x", "hip"] if src.endswith(".cpp") else []
+        cmds.append([hipcc, *HIPCC_FLAGS, *lang, "-c", os.path.join(CSRC, src), "-o", obj])
+    with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        list(ex.map(_run, cmds))
+    tmp = LIB_PATH + ".tmp"
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+def build_paging_kat() -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    cxx = os.environ.get("CXX", "g++")
+    _run([cxx, "-O2", "-std=c++17", "-Wall", "-Wextra",
+          os.path.join(CSRC, "paging_kat.cpp"), os.path.join(CSRC, "paging.cpp"),
+          "-o", KAT_PATH])
+    return KAT_PATH
+
+
+def build_all() -> None:
+    build_library()
+    build_paging_kat()
+
+
+if __name__ == "__main__":
+    build_all()
+    print(LIB_PATH)

@@ -1,0 +1,523 @@
+// Causal prefill attention for gfx950: flash-style tiles on MFMA (fp16 in, fp32 acc).
+//
+// Reference semantics (engine/kernels/kernels.cu:1844-1948 reference prefill, and
+// 2100-2276 for the segment-descriptor form): query row r at absolute position pos_r
+// attends to keys [0, pos_r] of its own sequence through that sequence's page table;
+// head h reads kv head h / (n_head / n_kv_head); scores are scaled by 1/sqrt(64).
+//
+// One kernel serves every reference prefill entry point; they differ only in how a
+// query row finds its (table, position):
+//   SEGMENTS  {packed_start, chunk_len, absolute_start, table_index} per request
+//             (attention_prefill_tiled, gpu.rs:1606-1751)
+//   OWNERS    owners[r], positions[r] per row (attention_prefill_packed, gpu.rs:1551-1604)
+//   PARAMS    one table, position params[5] + r (attention_prefill_paged, gpu.rs:1502-1549)
+//   CONTIG    contiguous cache, position pos_offset + r (attention_prefill, gpu.rs:1886-1934)
+//
+// Workgroup = 4 waves = (4 / HPW) row slices x HPW query heads of one GQA group, so the
+// HPW heads that share a kv head share every K/V tile staged in LDS. A wave owns QB
+// blocks of 16 query rows for one head. Per 64-key tile and 16-row block:
+//   S^T[64 key x 16 q] = K[64 x 64] . Q^T        8x mfma_f32_16x16x32_f16
+//   online softmax per query column (base 2), causal mask by absolute position
+//   O^T[64 dim x 16 q] += V^T[64 x 64 key] . P^T 8x mfma_f32_16x16x32_f16
+// The transposed V pages are copied into LDS as-is (no transpose on the way), and the
+// P^T operand is exactly the register layout the S^T product leaves behind.
+// Tiles are double-buffered in LDS; a wave skips tiles that lie wholly above the
+// causal diagonal of its rows (the workgroup still loads up to its last row).
+//
+// Rows of a workgroup are processed in runs of one owner (table). SEGMENTS, PARAMS and
+// CONTIG tiles are always a single run; an OWNERS tile that straddles two requests
+// makes two passes, each masking the rows of the other request.
+#include "common.hpp"
+
+#include <cmath>
+#include <cstdlib>
+
+namespace crucible {
+namespace {
+
+enum RowMode { kSegments = 0, kOwners = 1, kParams = 2, kContig = 3 };
+
+constexpr int kKeyTile = 64;
+constexpr int kLdsPad = 8;                   // halfs of padding per LDS row
+constexpr int kLdsRow = kKeyTile + kLdsPad;  // 72 halfs = 144 bytes
+
+struct PrefillArgs {
+    const void* q;
+    const half_t* k_pool;
+    const half_t* v_pool;
+    void* out;
+    const int32_t* tables;     // nullptr in CONTIG mode
+    const int32_t* segments;   // SEGMENTS
+    const int32_t* owners;     // OWNERS
+    const int32_t* positions;  // OWNERS
+    const int32_t* params;     // PARAMS
+    PoolAddr addr;
+    int64_t table_stride;
+    int64_t pos_offset;        // CONTIG
+    int64_t rows;              // OWNERS / PARAMS / CONTIG
+    int mode;
+    int n_head;
+    int n_kv_head;
+    int n_rep;
+    int max_seq;
+    int out_f16;
+    float scale_log2;
+};
+
+template <int HPW, int QB, bool QF32>
+__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
+    constexpr int RS = 4 / HPW;          // row slices per workgroup
+    constexpr int WROWS = 16 * QB;       // rows per wave
+    constexpr int R = RS * WROWS;        // rows per workgroup
+
+    __shared__ half_t s_k[2][kKeyTile][kLdsRow];  // [buf][key][dim]
+    __shared__ half_t s_v[2][64][kLdsRow];        // [buf][dim][key]
+    __shared__ int s_owner[R];
+    __shared__ int s_pos[R];
+    __shared__ int s_row[R];
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int col = lane & 15;
+    const int grp = lane >> 4;
+    const int rs = wave / HPW;
+    const int hi = wave % HPW;
+
+    const int groups_per_kv = a.n_rep / HPW;
+    const int g = blockIdx.x / groups_per_kv;
+    const int h = g * a.n_rep + (blockIdx.x % groups_per_kv) * HPW + hi;
+
+    // ---- rows of this tile: (packed row, owner, absolute position); -1 = none
+    if (tid < R) {
+        int row = -1, owner = 0, pos = 0;
+        const int64_t local = (int64_t)blockIdx.y * R + tid;
+        if (a.mode == kSegments) {
+            const int32_t* seg = a.segments + 4 * (int64_t)blockIdx.z;
+            if (local < seg[1]) {
+                row = (int)(seg[0] + local);
+                pos = (int)(seg[2] + local);
+                owner = seg[3];
+            }
+        } else if (local < a.rows) {
+            row = (int)local;
+            if (a.mode == kOwners) {
+                owner = a.owners[local];
+                pos = a.positions[local];
+            } else if (a.mode == kParams) {
+                pos = (int)(a.params[kParamPrefillPos] + local);
+            } else {
+                pos = (int)(a.pos_offset + local);
+            }
+        }
+        if (pos < 0 || pos >= a.max_seq) row = -1;  // outside the table: never read
+        s_row[tid] = row;
+        s_owner[tid] = owner;
+        s_pos[tid] = pos;
+    }
+    __syncthreads();
+    if (s_row[0] < 0 && a.mode != kOwners) return;  // uniform: tile past the chunk end
+
+    // ---- per-lane query state for each 16-row block
+    const int64_t ld_q = (int64_t)a.n_head * kHeadDim;
+    half8_t qh[QB][2], ql[QB][2];
+    float m[QB], l[QB];
+    float4_t acc[QB][4];
+    int my_row[QB], my_pos[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const int ri = rs * WROWS + qb * 16 + col;
+        my_row[qb] = s_row[ri];
+        my_pos[qb] = s_pos[ri];
+        m[qb] = -INFINITY;
+        l[qb] = 0.0f;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) acc[qb][db] = float4_t{0.f, 0.f, 0.f, 0.f};
+        qh[qb][0] = qh[qb][1] = ql[qb][0] = ql[qb][1] = half8_t{};
+        if (my_row[qb] >= 0) {
+            const int64_t off = (int64_t)my_row[qb] * ld_q + (int64_t)h * kHeadDim + 8 * grp;
+            if constexpr (QF32) {
+                const float* qp = static_cast<const float*>(a.q) + off;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float x0 = qp[j], x1 = qp[32 + j];
+                    qh[qb][0][j] = (half_t)x0;
+                    qh[qb][1][j] = (half_t)x1;
+                    ql[qb][0][j] = (half_t)(x0 - (float)qh[qb][0][j]);
+                    ql[qb][1][j] = (half_t)(x1 - (float)qh[qb][1][j]);
+                }
+            } else {
+                const half_t* qp = static_cast<const half_t*>(a.q) + off;
+                qh[qb][0] = *reinterpret_cast<const half8_t*>(qp);
+                qh[qb][1] = *reinterpret_cast<const half8_t*>(qp + 32);
+            }
+        }
+    }
+
+    const int kv_dim = a.addr.kv_dim;
+    // Cooperative tile loader: K as [key][dim] (thread: key t/4, dims 16*(t%4)..+15),
+    // V^T as [dim][key] (thread: page t/64 of the tile, channel t%64, 16 slots).
+    const int lk_key = tid >> 2, lk_c = (tid & 3) * 16;
+    const int lv_pg = tid >> 6, lv_d = tid & 63;
+
+    // ---- runs of one owner
+    int r0 = 0;
+    while (r0 < R) {
+        // next run start: first valid row at or after r0
+        while (r0 < R && s_row[r0] < 0) ++r0;
+        if (r0 >= R) break;
+        const int owner = s_owner[r0];
+        int r1 = r0 + 1;
+        while (r1 < R && s_row[r1] >= 0 && s_owner[r1] == owner) ++r1;
+        int hist_end = 0;
+        for (int r = r0; r < r1; ++r) hist_end = max(hist_end, s_pos[r] + 1);
+        // this wave's last visible key within the run
+        int wave_last = -1;
+        for (int r = max(r0, rs * WROWS); r < min(r1, rs * WROWS + WROWS); ++r)
+            wave_last = max(wave_last, s_pos[r]);
+
+        const int32_t* table = a.tables ? a.tables + (int64_t)owner * a.table_stride : nullptr;
+        const int n_tiles = (hist_end + kKeyTile - 1) / kKeyTile;
+
+        half8_t rk[2];
+        half8_t rv[2];
+        auto load_tile = [&](int kt) {
+            const int key = kt * kKeyTile + lk_key;
+            if (key < hist_end) {
+                const int64_t page = table ? (int64_t)table[key >> kPageShift] : (int64_t)(key >> kPageShift);
+                const half_t* kp = a.k_pool + block_base(a.addr, page) +
+                                   (int64_t)(key & kPageMask) * kv_dim + g * kHeadDim + lk_c;
+                rk[0] = *reinterpret_cast<const half8_t*>(kp);
+                rk[1] = *reinterpret_cast<const half8_t*>(kp + 8);
+            } else {
+                rk[0] = rk[1] = half8_t{};
+            }
+            const int key0 = kt * kKeyTile + lv_pg * kPageTokens;
+            if (key0 < hist_end) {
+                const int64_t page = table ? (int64_t)table[key0 >> kPageShift] : (int64_t)(key0 >> kPageShift);
+                const half_t* vp = a.v_pool + block_base(a.addr, page) +
+                                   (int64_t)(g * kHeadDim + lv_d) * kPageTokens;
+                rv[0] = *reinterpret_cast<const half8_t*>(vp);
+                rv[1] = *reinterpret_cast<const half8_t*>(vp + 8);
+                const int valid = hist_end - key0;  // slots >= valid hold no data
+                if (valid < kPageTokens) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        if (j >= valid) rv[0][j] = (half_t)0.0f;
+                        if (8 + j >= valid) rv[1][j] = (half_t)0.0f;
+                    }
+                }
+            } else {
+                rv[0] = rv[1] = half8_t{};
+            }
+        };
+        auto store_tile = [&](int buf) {
+            *reinterpret_cast<half8_t*>(&s_k[buf][lk_key][lk_c]) = rk[0];
+            *reinterpret_cast<half8_t*>(&s_k[buf][lk_key][lk_c + 8]) = rk[1];
+            *reinterpret_cast<half8_t*>(&s_v[buf][lv_d][lv_pg * kPageTokens]) = rv[0];
+            *reinterpret_cast<half8_t*>(&s_v[buf][lv_d][lv_pg * kPageTokens + 8]) = rv[1];
+        };
+
+        bool in_run[QB];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            const int ri = rs * WROWS + qb * 16 + col;
+            in_run[qb] = my_row[qb] >= 0 && ri >= r0 && ri < r1;
+        }
+
+        load_tile(0);
+        store_tile(0);
+        __syncthreads();
+        for (int kt = 0; kt < n_tiles; ++kt) {
+            const int buf = kt & 1;
+            if (kt + 1 < n_tiles) load_tile(kt + 1);
+            const int kbase = kt * kKeyTile;
+            if (wave_last >= kbase) {
+                // S^T blocks: st[qb][kb][r] = S^T[kbase + 16*kb + 4*grp + r][q = col]
+                float sv[QB][4][4];
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+                    const half8_t a0 = *reinterpret_cast<const half8_t*>(&s_k[buf][16 * kb + col][8 * grp]);
+                    const half8_t a1 = *reinterpret_cast<const half8_t*>(&s_k[buf][16 * kb + col][32 + 8 * grp]);
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb) {
+                        float4_t st = {0.f, 0.f, 0.f, 0.f};
+                        st = mfma_16x16x32(a0, qh[qb][0], st);
+                        st = mfma_16x16x32(a1, qh[qb][1], st);
+                        if constexpr (QF32) {
+                            st = mfma_16x16x32(a0, ql[qb][0], st);
+                            st = mfma_16x16x32(a1, ql[qb][1], st);
+                        }
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int key = kbase + 16 * kb + 4 * grp + r;
+                            sv[qb][kb][r] = (in_run[qb] && key <= my_pos[qb]) ? st[r] * a.scale_log2 : -INFINITY;
+                        }
+                    }
+                }
+                half8_t pb[QB][2];
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    float tm = -INFINITY;
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) tm = fmaxf(tm, sv[qb][kb][r]);
+                    tm = fmaxf(tm, __shfl_xor(tm, 16));
+                    tm = fmaxf(tm, __shfl_xor(tm, 32));
+                    const float mn = fmaxf(m[qb], tm);
+                    const float mu = (mn == -INFINITY) ? 0.0f : mn;
+                    const float alpha = fast_exp2(m[qb] - mu);
+                    float ps = 0.0f;
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const half_t p = (half_t)fast_exp2(sv[qb][kb][r] - mu);
+                            pb[qb][kb >> 1][(kb & 1) * 4 + r] = p;
+                            ps += (float)p;
+                        }
+                    l[qb] = l[qb] * alpha + ps;
+                    m[qb] = mn;
+#pragma unroll
+                    for (int db = 0; db < 4; ++db) acc[qb][db] = acc[qb][db] * alpha;
+                }
+                // O^T[dim][q] += V^T[dim][32 keys] . P^T[32 keys][q], key pairs (kb 0,1), (2,3)
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const half_t* vrow = &s_v[buf][16 * db + col][0];
+                        const half4_t v0 = *reinterpret_cast<const half4_t*>(vrow + 32 * ks + 4 * grp);
+                        const half4_t v1 = *reinterpret_cast<const half4_t*>(vrow + 32 * ks + 16 + 4 * grp);
+                        const half8_t va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+#pragma unroll
+                        for (int qb = 0; qb < QB; ++qb) acc[qb][db] = mfma_16x16x32(va, pb[qb][ks], acc[qb][db]);
+                    }
+                }
+            }
+            if (kt + 1 < n_tiles) store_tile(buf ^ 1);
+            __syncthreads();
+        }
+        r0 = r1;
+    }
+
+    // ---- normalise and write: lane (q = col, grp) holds dims 16*db + 4*grp .. +3
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        float lt = l[qb];
+        lt += __shfl_xor(lt, 16);
+        lt += __shfl_xor(lt, 32);
+        if (my_row[qb] < 0) continue;
+        const float inv = 1.0f / lt;
+        const int64_t off = (int64_t)my_row[qb] * ld_q + (int64_t)h * kHeadDim + 4 * grp;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const float4_t o = acc[qb][db] * inv;
+            if (a.out_f16) {
+                const half4_t hv = {(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
+                *reinterpret_cast<half4_t*>(static_cast<half_t*>(a.out) + off + 16 * db) = hv;
+            } else {
+                *reinterpret_cast<float4_t*>(static_cast<float*>(a.out) + off + 16 * db) = o;
+            }
+        }
+    }
+}
+
+int heads_per_wg(int n_rep) { return (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1; }
+
+template <int HPW, int QB>
+void launch_hq(const PrefillArgs& a, bool q_f32, dim3 grid, hipStream_t stream) {
+    if (q_f32) hipLaunchKernelGGL((prefill_kernel<HPW, QB, true>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((prefill_kernel<HPW, QB, false>), grid, dim3(256), 0, stream, a);
+}
+
+// tile_rows_total: rows spanned by grid.y (max_chunk or rows); z: requests.
+int launch_prefill(const PrefillArgs& a, int64_t tile_rows_total, int64_t z, bool q_f32,
+                   hipStream_t stream, const char* what) {
+    const int hpw = heads_per_wg(a.n_rep);
+    const int64_t gx = (int64_t)a.n_kv_head * (a.n_rep / hpw);
+    const int rs = 4 / hpw;
+    auto tiles = [&](int qb) { return (tile_rows_total + rs * 16 * qb - 1) / (rs * 16 * qb); };
+    int qb = (gx * tiles(2) * z * 4 >= 2048) ? 2 : 1;
+    if (const char* env = std::getenv("CRUCIBLE_PREFILL_QB")) {
+        const int v = std::atoi(env);
+        if (v == 1 || v == 2) qb = v;
+    }
+    const int64_t gy = tiles(qb);
+    CRUCIBLE_CHECK(gx <= INT32_MAX && gy <= 65535 && z <= 65535, CRUCIBLE_ERR_INVALID,
+                   "%s: grid (%lld, %lld, %lld) too large", what, (long long)gx, (long long)gy,
+                   (long long)z);
+    const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)z);
+    if (hpw == 4) {
+        if (qb == 2) launch_hq<4, 2>(a, q_f32, grid, stream);
+        else launch_hq<4, 1>(a, q_f32, grid, stream);
+    } else if (hpw == 2) {
+        if (qb == 2) launch_hq<2, 2>(a, q_f32, grid, stream);
+        else launch_hq<2, 1>(a, q_f32, grid, stream);
+    } else {
+        if (qb == 2) launch_hq<1, 2>(a, q_f32, grid, stream);
+        else launch_hq<1, 1>(a, q_f32, grid, stream);
+    }
+    return fail_launch(what);
+}
+
+int check_prefill(const char* what, int q_dtype, int out_dtype, int64_t n_head,
+                  int64_t n_kv_head, int64_t head_dim, int64_t kv_dim) {
+    CRUCIBLE_CHECK(dtype_ok(q_dtype) && dtype_ok(out_dtype), CRUCIBLE_ERR_INVALID,
+                   "%s: bad dtype", what);
+    CRUCIBLE_CHECK(n_head > 0 && n_kv_head > 0 && n_head % n_kv_head == 0, CRUCIBLE_ERR_INVALID,
+                   "%s: n_head %lld must be a positive multiple of n_kv_head %lld", what,
+                   (long long)n_head, (long long)n_kv_head);
+    CRUCIBLE_CHECK(head_dim == kHeadDim, CRUCIBLE_ERR_UNSUPPORTED,
+                   "%s: head_dim %lld unsupported (this build implements 64)", what,
+                   (long long)head_dim);
+    CRUCIBLE_CHECK(kv_dim == n_kv_head * head_dim, CRUCIBLE_ERR_INVALID,
+                   "%s: kv_dim %lld != n_kv_head * head_dim", what, (long long)kv_dim);
+    CRUCIBLE_CHECK(n_head <= (1 << 20), CRUCIBLE_ERR_INVALID, "%s: n_head too large", what);
+    return CRUCIBLE_OK;
+}
+
+PrefillArgs base_args(const void* q, const void* k_pool, const void* v_pool, void* out,
+                      int out_dtype, int64_t n_head, int64_t n_kv_head, int64_t kv_dim,
+                      int64_t max_seq) {
+    PrefillArgs a{};
+    a.q = q;
+    a.k_pool = static_cast<const half_t*>(k_pool);
+    a.v_pool = static_cast<const half_t*>(v_pool);
+    a.out = out;
+    a.addr.kv_dim = (int32_t)kv_dim;
+    a.n_head = (int)n_head;
+    a.n_kv_head = (int)n_kv_head;
+    a.n_rep = (int)(n_head / n_kv_head);
+    a.max_seq = (int)max_seq;
+    a.out_f16 = out_dtype == CRUCIBLE_F16;
+    a.scale_log2 = 0.125f * kLog2e;
+    return a;
+}
+
+}  // namespace
+}  // namespace crucible
+
+using namespace crucible;
+
+extern "C" int crucible_attention_prefill_paged(const void* q, int q_dtype, const void* k_pool,
+                                                const void* v_pool, void* out, int out_dtype,
+                                                const int32_t* page_table, int64_t rows,
+                                                int64_t n_head, int64_t n_kv_head,
+                                                int64_t head_dim, int64_t n_layer, int64_t layer,
+                                                int64_t kv_dim, int64_t max_seq,
+                                                const int32_t* params, crucible_stream_t stream) {
+    const char* what = "attention_prefill_paged";
+    if (int rc = check_prefill(what, q_dtype, out_dtype, n_head, n_kv_head, head_dim, kv_dim))
+        return rc;
+    CRUCIBLE_CHECK(rows >= 0 && rows <= INT32_MAX, CRUCIBLE_ERR_INVALID, "%s: rows", what);
+    if (rows == 0) return CRUCIBLE_OK;
+    CRUCIBLE_CHECK(q && k_pool && v_pool && out && page_table && params, CRUCIBLE_ERR_INVALID,
+                   "%s: null buffer", what);
+    CRUCIBLE_CHECK(n_layer > 0 && layer >= 0 && layer < n_layer, CRUCIBLE_ERR_INVALID,
+                   "%s: layer %lld outside n_layer %lld", what, (long long)layer,
+                   (long long)n_layer);
+    CRUCIBLE_CHECK(max_seq > 0 && max_seq <= INT32_MAX, CRUCIBLE_ERR_INVALID, "%s: max_seq",
+                   what);
+    PrefillArgs a = base_args(q, k_pool, v_pool, out, out_dtype, n_head, n_kv_head, kv_dim, max_seq);
+    a.mode = kParams;
+    a.tables = page_table;
+    a.params = params;
+    a.rows = rows;
+    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
+    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    return launch_prefill(a, rows, 1, q_dtype == CRUCIBLE_F32, stream, what);
+}
+
+extern "C" int crucible_attention_prefill_packed(
+    const void* q, int q_dtype, const void* k_pool, const void* v_pool, void* out, int out_dtype,
+    const int32_t* tables, const int32_t* owners, const int32_t* positions, int64_t rows,
+    int64_t table_stride, int64_t n_head, int64_t n_kv_head, int64_t head_dim, int64_t n_layer,
+    int64_t layer, int64_t kv_dim, int64_t max_seq, crucible_stream_t stream) {
+    const char* what = "attention_prefill_packed";
+    if (int rc = check_prefill(what, q_dtype, out_dtype, n_head, n_kv_head, head_dim, kv_dim))
+        return rc;
+    CRUCIBLE_CHECK(rows >= 0 && rows <= INT32_MAX, CRUCIBLE_ERR_INVALID, "%s: rows", what);
+    if (rows == 0) return CRUCIBLE_OK;
+    CRUCIBLE_CHECK(q && k_pool && v_pool && out && tables && owners && positions,
+                   CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
+    CRUCIBLE_CHECK(n_layer > 0 && layer >= 0 && layer < n_layer, CRUCIBLE_ERR_INVALID,
+                   "%s: layer %lld outside n_layer %lld", what, (long long)layer,
+                   (long long)n_layer);
+    CRUCIBLE_CHECK(table_stride > 0 && max_seq > 0 && max_seq <= table_stride * kPageTokens &&
+                       max_seq <= INT32_MAX,
+                   CRUCIBLE_ERR_INVALID, "%s: max_seq %lld must be in 1..table_stride*16", what,
+                   (long long)max_seq);
+    PrefillArgs a = base_args(q, k_pool, v_pool, out, out_dtype, n_head, n_kv_head, kv_dim, max_seq);
+    a.mode = kOwners;
+    a.tables = tables;
+    a.owners = owners;
+    a.positions = positions;
+    a.rows = rows;
+    a.table_stride = table_stride;
+    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
+    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    return launch_prefill(a, rows, 1, q_dtype == CRUCIBLE_F32, stream, what);
+}
+
+extern "C" int crucible_attention_prefill_tiled(
+    const void* q, int q_dtype, const void* k_pool, const void* v_pool, const void* current_k,
+    const void* current_v, void* out, int out_dtype, const int32_t* tables,
+    const int32_t* segments, int64_t requests, int64_t max_chunk, int64_t table_stride,
+    int64_t n_head, int64_t n_kv_head, int64_t head_dim, int64_t n_layer, int64_t layer,
+    int64_t kv_dim, int hybrid, int64_t score_capacity, crucible_stream_t stream) {
+    (void)current_k;
+    (void)current_v;
+    const char* what = "attention_prefill_tiled";
+    if (int rc = check_prefill(what, q_dtype, out_dtype, n_head, n_kv_head, head_dim, kv_dim))
+        return rc;
+    CRUCIBLE_CHECK(!hybrid, CRUCIBLE_ERR_UNSUPPORTED,
+                   "%s: hybrid (current-chunk K/V from scratch) is not implemented; append "
+                   "the chunk to the pool first",
+                   what);
+    // Launch checks of gpu.rs:1680-1719.
+    CRUCIBLE_CHECK(requests > 0 && max_chunk > 0 && table_stride > 0 && n_layer > 0 &&
+                       layer >= 0 && layer < n_layer && requests <= 65535,
+                   CRUCIBLE_ERR_INVALID, "%s: invalid launch dimensions", what);
+    CRUCIBLE_CHECK(q && k_pool && v_pool && out && tables && segments, CRUCIBLE_ERR_INVALID,
+                   "%s: null buffer", what);
+    CRUCIBLE_CHECK(score_capacity >= 0 && score_capacity <= table_stride * kPageTokens,
+                   CRUCIBLE_ERR_INVALID, "%s: score capacity exceeds the page table", what);
+    const int64_t max_seq = table_stride * kPageTokens;
+    CRUCIBLE_CHECK(max_seq <= INT32_MAX, CRUCIBLE_ERR_INVALID, "%s: table too large", what);
+    PrefillArgs a = base_args(q, k_pool, v_pool, out, out_dtype, n_head, n_kv_head, kv_dim, max_seq);
+    a.mode = kSegments;
+    a.tables = tables;
+    a.segments = segments;
+    a.table_stride = table_stride;
+    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
+    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    return launch_prefill(a, max_chunk, requests, q_dtype == CRUCIBLE_F32, stream, what);
+}
+
+extern "C" int crucible_attention_prefill(const void* q, int q_dtype, const void* k_cache,
+                                          const void* v_cache, void* out, int out_dtype,
+                                          int64_t rows, int64_t n_head, int64_t n_kv_head,
+                                          int64_t head_dim, int64_t max_seq,
+                                          int64_t cache_stride, int64_t layer_base,
+                                          int64_t pos_offset, crucible_stream_t stream) {
+    const char* what = "attention_prefill";
+    if (int rc = check_prefill(what, q_dtype, out_dtype, n_head, n_kv_head, head_dim,
+                               cache_stride))
+        return rc;
+    CRUCIBLE_CHECK(rows >= 0 && rows <= INT32_MAX, CRUCIBLE_ERR_INVALID, "%s: rows", what);
+    if (rows == 0) return CRUCIBLE_OK;
+    CRUCIBLE_CHECK(q && k_cache && v_cache && out, CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
+    CRUCIBLE_CHECK(max_seq > 0 && max_seq <= INT32_MAX && layer_base >= 0 && pos_offset >= 0 &&
+                       pos_offset + rows <= max_seq,
+                   CRUCIBLE_ERR_INVALID, "%s: rows past max_seq", what);
+    PrefillArgs a = base_args(q, k_cache, v_cache, out, out_dtype, n_head, n_kv_head,
+                              cache_stride, max_seq);
+    a.mode = kContig;
+    a.rows = rows;
+    a.pos_offset = pos_offset;
+    a.addr.page_stride = kPageTokens * cache_stride;
+    a.addr.layer_off = layer_base;
+    return launch_prefill(a, rows, 1, q_dtype == CRUCIBLE_F32, stream, what);
+}

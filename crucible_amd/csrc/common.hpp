@@ -1,0 +1,82 @@
+// Shared definitions for the gfx950 attention kernels and their C-ABI wrappers.
+//
+// Page geometry follows the reference engine exactly (engine/kernels/kernels.cu:1630-1638,
+// engine/src/paged.rs:12-21): 16-token pages, page = table[pos >> 4], slot = pos & 15,
+// block(page, layer) = ((page * n_layer + layer) * 16) * kv_dim elements. All offsets are
+// formed in 64-bit. Inside a block, K keeps the reference order [16][kv_dim] and V is
+// stored transposed, [kv_dim][16], so a V page slice is already the A operand of the PV
+// matrix product.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/crucible_attn.h"
+
+namespace crucible {
+
+constexpr int kPageTokens = 16;
+constexpr int kPageShift = 4;
+constexpr int kPageMask = 15;
+constexpr int kHeadDim = 64;
+constexpr int kParamPrefillPos = CRUCIBLE_PARAM_PREFILL_POS;
+constexpr int kParamSeq = CRUCIBLE_PARAM_SEQ;
+
+typedef _Float16 half_t;
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- addressing
+
+// How a kernel finds the fp16 rows of position `pos` for layer `layer`:
+//   paged:      block = table[pos >> 4] * page_stride + layer_off
+//   contiguous: block = (pos >> 4) * page_stride + layer_off   (table == nullptr)
+// page_stride = n_layer * 16 * kv_dim (paged) or 16 * kv_dim (contiguous);
+// layer_off = layer * 16 * kv_dim (paged) or layer_base (contiguous).
+struct PoolAddr {
+    int64_t page_stride;
+    int64_t layer_off;
+    int32_t kv_dim;
+};
+
+__device__ __forceinline__ int64_t block_base(const PoolAddr& a, int64_t page) {
+    return page * a.page_stride + a.layer_off;
+}
+
+// ---------------------------------------------------------------- math
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float4_t mfma_16x16x32(half8_t a, half8_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float4_t mfma_16x16x16(half4_t a, half4_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// log2(e): softmax is evaluated as 2^(s * scale * log2e - m) with m in the same units.
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------- host side
+
+void set_error(int status, const char* fmt, ...);
+int fail_launch(const char* what);
+inline bool dtype_ok(int d) { return d == CRUCIBLE_F32 || d == CRUCIBLE_F16; }
+inline bool kind_ok(int k) { return k == CRUCIBLE_POOL_K || k == CRUCIBLE_POOL_V; }
+
+}  // namespace crucible
+
+#define CRUCIBLE_CHECK(cond, status, ...)                 \
+    do {                                                  \
+        if (!(cond)) {                                    \
+            ::crucible::set_error((status), __VA_ARGS__); \
+            return (status);                              \
+        }                                                 \
+    } while (0)

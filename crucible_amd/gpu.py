@@ -1,0 +1,228 @@
+"""Host-side mirror of the reference engine's attention launch API.
+
+``Gpu`` has the attention and KV-append methods of ``impl Gpu`` in the reference
+(engine/src/gpu.rs), with the same names, argument order and meaning, over torch
+device tensors. Each method checks its tensors (device, dtype, contiguity, capacity,
+as the reference checks slice lengths), calls the C ABI, and raises ``CrucibleError``
+on any non-zero status. Everything runs on the caller's current HIP stream, nothing
+synchronises, and nothing here computes attention itself: the HIP library is the only
+implementation and loading fails if it is missing.
+
+Differences from the reference, all from the allowed page-layout change:
+  * pools are fp16 (reference: f32) and V pools store each (page, layer) block
+    transposed, so the append methods take ``kind="k"`` or ``kind="v"``;
+  * split-K decode needs a workspace; pass one (graph capture) or let the Gpu keep
+    a cached one per (batch, n_head, max_seq).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import CrucibleError, F16, F32, POOL_K, POOL_V, PAGE_TOKENS
+
+_DTYPES = {torch.float32: F32, torch.float16: F16}
+_KINDS = {"k": POOL_K, "v": POOL_V, POOL_K: POOL_K, POOL_V: POOL_V}
+
+
+def _ptr(t):
+    return None if t is None else ctypes_ptr(t)
+
+
+def ctypes_ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def _dtype(t: torch.Tensor, what: str) -> int:
+    if t.dtype not in _DTYPES:
+        raise CrucibleError(_lib.ERR_INVALID, f"{what}: dtype {t.dtype} (need float32/float16)")
+    return _DTYPES[t.dtype]
+
+
+def _need(t, what, *, dtype=None, numel=None):
+    if t is None:
+        raise CrucibleError(_lib.ERR_INVALID, f"{what} is required")
+    if not t.is_cuda:
+        raise CrucibleError(_lib.ERR_INVALID, f"{what} must be a device tensor")
+    if not t.is_contiguous():
+        raise CrucibleError(_lib.ERR_INVALID, f"{what} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise CrucibleError(_lib.ERR_INVALID, f"{what}: dtype {t.dtype}, expected {dtype}")
+    if numel is not None and t.numel() < numel:
+        raise CrucibleError(_lib.ERR_INVALID, f"{what}: {t.numel()} elements, need {numel}")
+    return t
+
+
+def pool_elems(n_pages: int, n_layer: int, kv_dim: int) -> int:
+    """Elements of one fp16 pool: [n_pages][n_layer][16][kv_dim] (paged.rs:14-21)."""
+    return n_pages * n_layer * PAGE_TOKENS * kv_dim
+
+
+class Gpu:
+    """The attention/append subset of the reference ``Gpu`` (engine/src/gpu.rs:327-2157)."""
+
+    def __init__(self, device: int | torch.device = 0):
+        self.lib = _lib.load()
+        self.device = torch.device("cuda", device) if isinstance(device, int) else device
+        self._workspaces: dict[tuple, torch.Tensor] = {}
+
+    # ------------------------------------------------------------- plumbing
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def workspace(self, batch: int, n_head: int, max_seq: int) -> torch.Tensor:
+        """Split-K scratch for decode, allocated once per shape (never inside a call)."""
+        key = (batch, n_head, max_seq)
+        ws = self._workspaces.get(key)
+        if ws is None:
+            nbytes = self.lib.crucible_attention_decode_workspace_bytes(batch, n_head, max_seq)
+            ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=self.device)
+            self._workspaces[key] = ws
+        return ws
+
+    @staticmethod
+    def version() -> str:
+        return _lib.load().crucible_attn_version().decode()
+
+    # ------------------------------------------------------------- KV append
+    def cache_store(self, src, cache, rows, kv_dim, layer_base, pos_offset, *, kind):
+        """gpu.rs:1259-1279: contiguous cache, position pos_offset + row."""
+        _need(src, "src", numel=rows * kv_dim)
+        _need(cache, "cache", dtype=torch.float16)
+        _lib.check(self.lib.crucible_cache_store(
+            _ptr(src), _dtype(src, "src"), _ptr(cache), _KINDS[kind], rows, kv_dim, layer_base,
+            pos_offset, self._stream()))
+
+    def cache_store_paged(self, src, pool, page_table, rows, kv_dim, n_layer, layer, params, *,
+                          kind):
+        """gpu.rs:1281-1307: one table, position params[5] + row."""
+        _need(src, "src", numel=rows * kv_dim)
+        _need(pool, "pool", dtype=torch.float16)
+        _need(page_table, "page_table", dtype=torch.int32)
+        _need(params, "params", dtype=torch.int32, numel=6)
+        _lib.check(self.lib.crucible_cache_store_paged(
+            _ptr(src), _dtype(src, "src"), _ptr(pool), _KINDS[kind], _ptr(page_table), rows,
+            kv_dim, n_layer, layer, _ptr(params), self._stream()))
+
+    def cache_store_rows_paged(self, src, pool, page_tables, positions, rows, kv_dim,
+                               table_stride, n_layer, layer, *, kind):
+        """gpu.rs:1405-1439: row r at positions[r] through its own table row."""
+        _need(src, "src", numel=rows * kv_dim)
+        _need(pool, "pool", dtype=torch.float16)
+        _need(page_tables, "page_tables", dtype=torch.int32, numel=rows * table_stride)
+        _need(positions, "positions", dtype=torch.int32, numel=rows)
+        _lib.check(self.lib.crucible_cache_store_rows_paged(
+            _ptr(src), _dtype(src, "src"), _ptr(pool), _KINDS[kind], _ptr(page_tables),
+            _ptr(positions), rows, kv_dim, table_stride, n_layer, layer, self._stream()))
+
+    def cache_store_packed_paged(self, src, pool, tables, owners, positions, rows, kv_dim,
+                                 table_stride, n_layer, layer, *, kind):
+        """gpu.rs:1800-1835: row r at positions[r] through tables[owners[r]]."""
+        _need(src, "src", numel=rows * kv_dim)
+        _need(pool, "pool", dtype=torch.float16)
+        _need(tables, "tables", dtype=torch.int32)
+        _need(owners, "owners", dtype=torch.int32, numel=rows)
+        _need(positions, "positions", dtype=torch.int32, numel=rows)
+        _lib.check(self.lib.crucible_cache_store_packed_paged(
+            _ptr(src), _dtype(src, "src"), _ptr(pool), _KINDS[kind], _ptr(tables), _ptr(owners),
+            _ptr(positions), rows, kv_dim, table_stride, n_layer, layer, self._stream()))
+
+    # ------------------------------------------------------------- decode
+    def attention_decode_paged(self, q, k_pool, v_pool, out, page_tables, seq_lens, batch,
+                               n_head, n_kv_head, head_dim, table_stride, n_layer, layer,
+                               kv_dim, max_seq, workspace=None):
+        """gpu.rs:1441-1500. seq_lens[b] <= 0: request b inactive, out untouched."""
+        _need(q, "q", numel=batch * n_head * head_dim)
+        _need(out, "out", numel=batch * n_head * head_dim)
+        _need(k_pool, "k_pool", dtype=torch.float16)
+        _need(v_pool, "v_pool", dtype=torch.float16)
+        _need(page_tables, "page_tables", dtype=torch.int32, numel=batch * table_stride)
+        _need(seq_lens, "seq_lens", dtype=torch.int32, numel=batch)
+        ws = workspace if workspace is not None else self.workspace(batch, n_head, max_seq)
+        _need(ws, "workspace")
+        _lib.check(self.lib.crucible_attention_decode_paged(
+            _ptr(q), _dtype(q, "q"), _ptr(k_pool), _ptr(v_pool), _ptr(out), _dtype(out, "out"),
+            _ptr(page_tables), _ptr(seq_lens), batch, n_head, n_kv_head, head_dim, table_stride,
+            n_layer, layer, kv_dim, max_seq, _ptr(ws), ws.numel() * ws.element_size(),
+            self._stream()))
+
+    def attention_decode(self, q, k_cache, v_cache, out, n_head, n_kv_head, head_dim, params,
+                         max_seq, cache_stride, layer_base, workspace=None):
+        """gpu.rs:762-817: contiguous cache, length params[3]."""
+        _need(q, "q", numel=n_head * head_dim)
+        _need(out, "out", numel=n_head * head_dim)
+        _need(k_cache, "k_cache", dtype=torch.float16)
+        _need(v_cache, "v_cache", dtype=torch.float16)
+        _need(params, "params", dtype=torch.int32, numel=6)
+        ws = workspace if workspace is not None else self.workspace(1, n_head, max_seq)
+        _lib.check(self.lib.crucible_attention_decode(
+            _ptr(q), _dtype(q, "q"), _ptr(k_cache), _ptr(v_cache), _ptr(out), _dtype(out, "out"),
+            n_head, n_kv_head, head_dim, _ptr(params), max_seq, cache_stride, layer_base,
+            _ptr(ws), ws.numel() * ws.element_size(), self._stream()))
+
+    def attention_split(self, q, k_cache, v_cache, partial_o, partial_m, partial_l, out, n_head,
+                        n_kv_head, head_dim, params, capacity, cache_stride, layer_base):
+        """gpu.rs:1936-2014: flash-decoding with caller-owned partials (128-token chunks)."""
+        n_chunks = -(-capacity // 128)
+        _need(q, "q", numel=n_head * head_dim)
+        _need(out, "out", numel=n_head * head_dim)
+        _need(partial_o, "partial_o", dtype=torch.float32, numel=n_head * n_chunks * head_dim)
+        _need(partial_m, "partial_m", dtype=torch.float32, numel=n_head * n_chunks)
+        _need(partial_l, "partial_l", dtype=torch.float32, numel=n_head * n_chunks)
+        _need(params, "params", dtype=torch.int32, numel=6)
+        _lib.check(self.lib.crucible_attention_split(
+            _ptr(q), _dtype(q, "q"), _ptr(k_cache), _ptr(v_cache), _ptr(partial_o),
+            _ptr(partial_m), _ptr(partial_l), _ptr(out), _dtype(out, "out"), n_head, n_kv_head,
+            head_dim, _ptr(params), capacity, cache_stride, layer_base, self._stream()))
+
+    # ------------------------------------------------------------- prefill
+    def attention_prefill_paged(self, q, k_pool, v_pool, out, page_table, rows, n_head,
+                                n_kv_head, head_dim, n_layer, layer, kv_dim, max_seq, params):
+        """gpu.rs:1502-1549: one sequence, row r at position params[5] + r."""
+        _need(q, "q", numel=rows * n_head * head_dim)
+        _need(out, "out", numel=rows * n_head * head_dim)
+        _need(page_table, "page_table", dtype=torch.int32)
+        _need(params, "params", dtype=torch.int32, numel=6)
+        _lib.check(self.lib.crucible_attention_prefill_paged(
+            _ptr(q), _dtype(q, "q"), _ptr(k_pool), _ptr(v_pool), _ptr(out), _dtype(out, "out"),
+            _ptr(page_table), rows, n_head, n_kv_head, head_dim, n_layer, layer, kv_dim, max_seq,
+            _ptr(params), self._stream()))
+
+    def attention_prefill_packed(self, q, k_pool, v_pool, out, tables, owners, positions, rows,
+                                 table_stride, n_head, n_kv_head, head_dim, n_layer, layer,
+                                 kv_dim, max_seq):
+        """gpu.rs:1551-1604: row r of request owners[r] at position positions[r]."""
+        _need(q, "q", numel=rows * n_head * head_dim)
+        _need(out, "out", numel=rows * n_head * head_dim)
+        _need(tables, "tables", dtype=torch.int32)
+        _need(owners, "owners", dtype=torch.int32, numel=rows)
+        _need(positions, "positions", dtype=torch.int32, numel=rows)
+        _lib.check(self.lib.crucible_attention_prefill_packed(
+            _ptr(q), _dtype(q, "q"), _ptr(k_pool), _ptr(v_pool), _ptr(out), _dtype(out, "out"),
+            _ptr(tables), _ptr(owners), _ptr(positions), rows, table_stride, n_head, n_kv_head,
+            head_dim, n_layer, layer, kv_dim, max_seq, self._stream()))
+
+    def attention_prefill_tiled(self, q, k_pool, v_pool, current_k, current_v, out, tables,
+                                segments, requests, max_chunk, table_stride, n_head, n_kv_head,
+                                head_dim, n_layer, layer, kv_dim, hybrid=False,
+                                score_capacity=0):
+        """gpu.rs:1606-1751: segments {packed_start, chunk_len, absolute_start, table_index}."""
+        _need(segments, "segments", dtype=torch.int32, numel=4 * requests)
+        _need(tables, "tables", dtype=torch.int32, numel=requests * table_stride)
+        _need(q, "q", numel=max_chunk * n_head * head_dim)
+        _need(out, "out", numel=max_chunk * n_head * head_dim)
+        _lib.check(self.lib.crucible_attention_prefill_tiled(
+            _ptr(q), _dtype(q, "q"), _ptr(k_pool), _ptr(v_pool), _ptr(current_k),
+            _ptr(current_v), _ptr(out), _dtype(out, "out"), _ptr(tables), _ptr(segments),
+            requests, max_chunk, table_stride, n_head, n_kv_head, head_dim, n_layer, layer,
+            kv_dim, int(bool(hybrid)), score_capacity, self._stream()))
+
+    def attention_prefill(self, q, k_cache, v_cache, out, rows, n_head, n_kv_head, head_dim,
+                          max_seq, cache_stride, layer_base, pos_offset):
+        """gpu.rs:1886-1934: contiguous cache, row r at position pos_offset + r."""
+        _need(q, "q", numel=rows * n_head * head_dim)
+        _need(out, "out", numel=rows * n_head * head_dim)
+        _lib.check(self.lib.crucible_attention_prefill(
+            _ptr(q), _dtype(q, "q"), _ptr(k_cache), _ptr(v_cache), _ptr(out), _dtype(out, "out"),
+            rows, n_head, n_kv_head, head_dim, max_seq, cache_stride, layer_base, pos_offset,
+            self._stream()))

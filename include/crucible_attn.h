@@ -1,0 +1,241 @@
+/*
+ * crucible_attn.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Drop-in boundary for the attention and KV-append methods of the reference
+ * engine's GPU backend (Onwcan/crucible, engine/src/gpu.rs, `impl Gpu`). Each
+ * entry point below names the method it replaces. Argument order and meaning
+ * follow the reference; sizes are int64_t where the reference takes usize.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer unless stated otherwise. The caller owns
+ *     every buffer; no entry point allocates device memory, synchronises, or
+ *     copies host<->device. Every entry point enqueues on `stream` and returns.
+ *   - Per-step values (positions, lengths, page tables, params) are read from
+ *     device memory, never passed by value, so hipGraph capture of a step stays
+ *     valid across replays (kernels.cu:17-35 in the reference).
+ *   - Return value: CRUCIBLE_OK (0) or an error code. Argument validation
+ *     happens before any launch; on error nothing is enqueued. The message of
+ *     the last error on the calling thread is available from
+ *     crucible_attn_last_error().
+ *   - Page geometry is the reference's: 16-token pages, page = table[pos >> 4],
+ *     slot = pos & 15, and a page holds every layer. Element offsets of the
+ *     (page, layer) block are ((page * n_layer + layer) * 16) * kv_dim.
+ *   - Page layout (the one change the north star allows): K pools keep the
+ *     reference element order inside a block, [16][kv_dim]. V pools store each
+ *     block transposed, [kv_dim][16]; element (slot, c) is at block + c*16 + slot.
+ *     KV pools hold IEEE fp16. Pool sizes are unchanged.
+ *   - Contiguous caches (the reference's non-paged oracle path) use the same
+ *     element order with pages numbered pos >> 4 inside a layer region:
+ *     K [layer][cap][kv_dim], V [layer][cap/16][kv_dim][16]; `layer_base` is
+ *     layer * cap * kv_dim as in the reference.
+ */
+#ifndef CRUCIBLE_ATTN_H
+#define CRUCIBLE_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same type as HIP's hipStream_t; NULL is the default stream. */
+typedef struct ihipStream_t* crucible_stream_t;
+
+enum crucible_status {
+    CRUCIBLE_OK = 0,
+    CRUCIBLE_ERR_INVALID = 1,     /* argument failed validation; nothing launched */
+    CRUCIBLE_ERR_UNSUPPORTED = 2, /* geometry this build does not implement */
+    CRUCIBLE_ERR_WORKSPACE = 3,   /* workspace missing or smaller than required */
+    CRUCIBLE_ERR_LAUNCH = 4       /* the HIP runtime rejected a launch */
+};
+
+enum crucible_dtype { CRUCIBLE_F32 = 0, CRUCIBLE_F16 = 1 };
+enum crucible_pool_kind { CRUCIBLE_POOL_K = 0, CRUCIBLE_POOL_V = 1 };
+
+/* Index of the prefill position offset in the device params buffer
+ * (gpu.rs:78 PARAM_PREFILL_POS, kernels.cu:43). */
+#define CRUCIBLE_PARAM_PREFILL_POS 5
+/* Index of the visible length in the params buffer (gpu.rs:70 PARAM_SEQ). */
+#define CRUCIBLE_PARAM_SEQ 3
+#define CRUCIBLE_PAGE_TOKENS 16
+
+/* ------------------------------------------------------------------ library */
+
+/* Version string of this library (static storage). */
+const char* crucible_attn_version(void);
+
+/* Copy the calling thread's last error message into buf (NUL-terminated,
+ * truncated to n). Returns the status of that error (CRUCIBLE_OK if none). */
+int crucible_attn_last_error(char* buf, size_t n);
+
+/* ------------------------------------------------------------------ KV append
+ * src is [rows][kv_dim] in src_dtype; f32 values are rounded to fp16 (RNE).
+ * `kind` says which pool layout `pool` has (K or V).
+ */
+
+/* Replaces Gpu::cache_store (gpu.rs:1259-1279; kernel kernels.cu:1079-1092):
+ * contiguous cache, position pos_offset + row, layer region at layer_base. */
+int crucible_cache_store(const void* src, int src_dtype, void* cache, int kind,
+                         int64_t rows, int64_t kv_dim, int64_t layer_base,
+                         int64_t pos_offset, crucible_stream_t stream);
+
+/* Replaces Gpu::cache_store_paged (gpu.rs:1281-1307; kernels.cu:1646-1669):
+ * one sequence's table, position params[5] + row. */
+int crucible_cache_store_paged(const void* src, int src_dtype, void* pool, int kind,
+                               const int32_t* page_table, int64_t rows, int64_t kv_dim,
+                               int64_t n_layer, int64_t layer, const int32_t* params,
+                               crucible_stream_t stream);
+
+/* Replaces Gpu::cache_store_rows_paged (gpu.rs:1405-1439; kernels.cu:1713-1731):
+ * row r at positions[r] through page_tables[r * table_stride + ...]. */
+int crucible_cache_store_rows_paged(const void* src, int src_dtype, void* pool, int kind,
+                                    const int32_t* page_tables, const int32_t* positions,
+                                    int64_t rows, int64_t kv_dim, int64_t table_stride,
+                                    int64_t n_layer, int64_t layer, crucible_stream_t stream);
+
+/* Replaces Gpu::cache_store_packed_paged (gpu.rs:1800-1835; kernels.cu:2280-2292):
+ * row r at positions[r] through tables[owners[r] * table_stride + ...]. */
+int crucible_cache_store_packed_paged(const void* src, int src_dtype, void* pool, int kind,
+                                      const int32_t* tables, const int32_t* owners,
+                                      const int32_t* positions, int64_t rows, int64_t kv_dim,
+                                      int64_t table_stride, int64_t n_layer, int64_t layer,
+                                      crucible_stream_t stream);
+
+/* ------------------------------------------------------------------ decode
+ * q is [batch][n_head * head_dim] (q_dtype), out is [batch][n_head * head_dim]
+ * (out_dtype). head_dim must be 64 and n_head a multiple of n_kv_head with
+ * n_head / n_kv_head <= 16. Query head h reads KV head h / (n_head / n_kv_head).
+ * The split-K partials live in a caller-provided workspace of at least
+ * crucible_attention_decode_workspace_bytes(...) bytes (no allocation here).
+ */
+
+size_t crucible_attention_decode_workspace_bytes(int64_t batch, int64_t n_head,
+                                                 int64_t max_seq);
+
+/* Replaces Gpu::attention_decode_paged (gpu.rs:1441-1500; kernels.cu:1741-1839).
+ * seq_lens[b] <= 0 marks an inactive request: its output is left untouched. */
+int crucible_attention_decode_paged(const void* q, int q_dtype, const void* k_pool,
+                                    const void* v_pool, void* out, int out_dtype,
+                                    const int32_t* page_tables, const int32_t* seq_lens,
+                                    int64_t batch, int64_t n_head, int64_t n_kv_head,
+                                    int64_t head_dim, int64_t table_stride, int64_t n_layer,
+                                    int64_t layer, int64_t kv_dim, int64_t max_seq,
+                                    void* workspace, size_t workspace_bytes,
+                                    crucible_stream_t stream);
+
+/* Replaces Gpu::attention_decode (gpu.rs:762-817; kernels.cu:288-389): one
+ * sequence in a contiguous cache, visible length params[CRUCIBLE_PARAM_SEQ]. */
+int crucible_attention_decode(const void* q, int q_dtype, const void* k_cache,
+                              const void* v_cache, void* out, int out_dtype, int64_t n_head,
+                              int64_t n_kv_head, int64_t head_dim, const int32_t* params,
+                              int64_t max_seq, int64_t cache_stride, int64_t layer_base,
+                              void* workspace, size_t workspace_bytes,
+                              crucible_stream_t stream);
+
+/* Replaces Gpu::attention_split (gpu.rs:1936-2014; kernels.cu:692-850): the
+ * flash-decoding form of attention_decode with caller-owned partials, laid out
+ * as in the reference: partial_o [n_head][n_chunks][head_dim], partial_m and
+ * partial_l [n_head][n_chunks], n_chunks = ceil(capacity / 128). The partial
+ * values are internal to the combine; only `out` is part of the contract. */
+int crucible_attention_split(const void* q, int q_dtype, const void* k_cache,
+                             const void* v_cache, float* partial_o, float* partial_m,
+                             float* partial_l, void* out, int out_dtype, int64_t n_head,
+                             int64_t n_kv_head, int64_t head_dim, const int32_t* params,
+                             int64_t capacity, int64_t cache_stride, int64_t layer_base,
+                             crucible_stream_t stream);
+
+/* ------------------------------------------------------------------ prefill
+ * Causal attention for query rows whose keys are already in the pool. q is
+ * [rows][n_head * head_dim], out likewise. Row r sees keys [0, pos_r].
+ */
+
+/* Replaces Gpu::attention_prefill_paged (gpu.rs:1502-1549; kernels.cu:1927-1936):
+ * one sequence, row r at position params[5] + r. */
+int crucible_attention_prefill_paged(const void* q, int q_dtype, const void* k_pool,
+                                     const void* v_pool, void* out, int out_dtype,
+                                     const int32_t* page_table, int64_t rows, int64_t n_head,
+                                     int64_t n_kv_head, int64_t head_dim, int64_t n_layer,
+                                     int64_t layer, int64_t kv_dim, int64_t max_seq,
+                                     const int32_t* params, crucible_stream_t stream);
+
+/* Replaces Gpu::attention_prefill_packed (gpu.rs:1551-1604; kernels.cu:1938-1948):
+ * row r belongs to request owners[r] at position positions[r]. Rows of one
+ * request need not be adjacent; adjacent rows of one request share K/V tiles. */
+int crucible_attention_prefill_packed(const void* q, int q_dtype, const void* k_pool,
+                                      const void* v_pool, void* out, int out_dtype,
+                                      const int32_t* tables, const int32_t* owners,
+                                      const int32_t* positions, int64_t rows,
+                                      int64_t table_stride, int64_t n_head, int64_t n_kv_head,
+                                      int64_t head_dim, int64_t n_layer, int64_t layer,
+                                      int64_t kv_dim, int64_t max_seq, crucible_stream_t stream);
+
+/* Replaces Gpu::attention_prefill_tiled (gpu.rs:1606-1751; kernels.cu:1950-2276):
+ * segments[4*i .. 4*i+3] = {packed_start, chunk_len, absolute_start, table_index}.
+ * Query row packed_start + j is at position absolute_start + j. `hybrid` must be
+ * 0 (current_k/current_v are accepted for signature parity and not read);
+ * score_capacity is validated as in the reference but not needed here. */
+int crucible_attention_prefill_tiled(const void* q, int q_dtype, const void* k_pool,
+                                     const void* v_pool, const void* current_k,
+                                     const void* current_v, void* out, int out_dtype,
+                                     const int32_t* tables, const int32_t* segments,
+                                     int64_t requests, int64_t max_chunk, int64_t table_stride,
+                                     int64_t n_head, int64_t n_kv_head, int64_t head_dim,
+                                     int64_t n_layer, int64_t layer, int64_t kv_dim,
+                                     int hybrid, int64_t score_capacity,
+                                     crucible_stream_t stream);
+
+/* Replaces Gpu::attention_prefill (gpu.rs:1886-1934; kernels.cu:1099-1172):
+ * contiguous cache, row r at position pos_offset + r. */
+int crucible_attention_prefill(const void* q, int q_dtype, const void* k_cache,
+                               const void* v_cache, void* out, int out_dtype, int64_t rows,
+                               int64_t n_head, int64_t n_kv_head, int64_t head_dim,
+                               int64_t max_seq, int64_t cache_stride, int64_t layer_base,
+                               int64_t pos_offset, crucible_stream_t stream);
+
+/* ------------------------------------------------------------------ host helpers */
+
+/* Build prefill segments from cumulative sequence offsets (host memory):
+ * cu_seqlens[0..n] with cu_seqlens[0] = 0; absolute_starts[i] (NULL = all 0);
+ * table i for sequence i. Writes 4*n int32 to segments_out and returns the
+ * largest chunk length, or -1 if the offsets are not non-decreasing. */
+int64_t crucible_segments_from_cu_seqlens(const int32_t* cu_seqlens, int64_t n,
+                                          const int32_t* absolute_starts,
+                                          int32_t* segments_out);
+
+/* ------------------------------------------------------------------ paging (host)
+ * The reference allocator (engine/src/paged.rs:64-242) restated in C++ for a
+ * C/C++ caller: a stack free list (first alloc is page 0), per-sequence tables
+ * with all-or-nothing growth, zero-padded device tables. Handles are opaque.
+ */
+typedef struct crucible_page_pool crucible_page_pool;
+typedef struct crucible_seq_pages crucible_seq_pages;
+
+crucible_page_pool* crucible_page_pool_new(int64_t n_pages, int64_t n_layer, int64_t kv_dim);
+void crucible_page_pool_free(crucible_page_pool* pool);
+int64_t crucible_page_pool_free_pages(const crucible_page_pool* pool);
+int64_t crucible_page_pool_used_pages(const crucible_page_pool* pool);
+/* Returns the page id, or -1 when exhausted (error message set). */
+int64_t crucible_page_pool_alloc(crucible_page_pool* pool);
+int crucible_page_pool_release(crucible_page_pool* pool, int64_t page);
+
+crucible_seq_pages* crucible_seq_pages_new(void);
+void crucible_seq_pages_free(crucible_seq_pages* seq);
+int64_t crucible_seq_pages_len(const crucible_seq_pages* seq);
+int64_t crucible_seq_pages_n_pages(const crucible_seq_pages* seq);
+int crucible_seq_pages_grow(crucible_seq_pages* seq, crucible_page_pool* pool, int64_t extra);
+int crucible_seq_pages_release(crucible_seq_pages* seq, crucible_page_pool* pool);
+/* (page, slot) of position pos; returns CRUCIBLE_ERR_INVALID past the end. */
+int crucible_seq_pages_translate(const crucible_seq_pages* seq, int64_t pos, int64_t* page,
+                                 int64_t* slot);
+/* Write the table padded with zeros to `stride` entries (host memory). */
+int crucible_seq_pages_table_padded(const crucible_seq_pages* seq, int64_t stride,
+                                    int32_t* out);
+/* prefill.rs:160-172: ceil((prompt + generated - 1) / 16), or -1 if invalid. */
+int64_t crucible_request_page_reservation(int64_t prompt, int64_t generated, int64_t context);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CRUCIBLE_ATTN_H */

@@ -1,0 +1,82 @@
+"""The C-ABI library loads, exports every symbol include/crucible_attn.h declares, and
+rejects invalid arguments before launching anything (no GPU needed for these calls)."""
+import ctypes
+import re
+
+import pytest
+
+from crucible_amd import _lib
+
+
+def _declared():
+    text = open(_lib.HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(crucible_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declarations_are_all_bound_and_exported():
+    names = _declared()
+    assert len(names) >= 28
+    lib = _lib.load()
+    for name in names:
+        assert hasattr(lib, name), f"library does not export {name}"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_version():
+    assert _lib.load().crucible_attn_version().decode().startswith("crucible_attn")
+
+
+def test_header_compiles_as_c(tmp_path):
+    import subprocess
+    src = tmp_path / "t.c"
+    src.write_text('#include "crucible_attn.h"\nint main(void){return CRUCIBLE_OK;}\n')
+    inc = _lib.HEADER.rsplit("/", 1)[0]
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", inc, str(src), "-o",
+                    str(tmp_path / "t")], check=True)
+
+
+def _status_and_msg(rc):
+    status, msg = _lib.last_error()
+    return rc, status, msg
+
+
+def test_invalid_arguments_are_rejected_before_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    # head_dim 128 is outside this build
+    rc = lib.crucible_attention_decode_paged(fake, 1, fake, fake, fake, 0, fake, fake, 1, 12, 3,
+                                             128, 64, 12, 0, 384, 1024, fake, 1 << 20, None)
+    assert rc == _lib.ERR_UNSUPPORTED
+    assert "head_dim" in _lib.last_error()[1]
+    # layer outside n_layer
+    rc = lib.crucible_attention_decode_paged(fake, 1, fake, fake, fake, 0, fake, fake, 1, 12, 3,
+                                             64, 64, 12, 12, 192, 1024, fake, 1 << 20, None)
+    assert rc == _lib.ERR_INVALID and "layer" in _lib.last_error()[1]
+    # n_head not a multiple of n_kv_head
+    rc = lib.crucible_attention_prefill_paged(fake, 1, fake, fake, fake, 0, fake, 10, 12, 5, 64,
+                                              12, 0, 320, 1024, fake, None)
+    assert rc == _lib.ERR_INVALID
+    # workspace too small for split-K
+    rc = lib.crucible_attention_decode_paged(fake, 1, fake, fake, fake, 0, fake, fake, 16, 12, 3,
+                                             64, 128, 12, 0, 192, 2048, fake, 16, None)
+    assert rc == _lib.ERR_WORKSPACE
+    # bad dtype / pool kind for the append
+    rc = lib.crucible_cache_store_rows_paged(fake, 7, fake, 0, fake, fake, 1, 192, 8, 12, 0, None)
+    assert rc == _lib.ERR_INVALID
+    rc = lib.crucible_cache_store_rows_paged(fake, 0, fake, 9, fake, fake, 1, 192, 8, 12, 0, None)
+    assert rc == _lib.ERR_INVALID
+    # hybrid prefill is not implemented
+    rc = lib.crucible_attention_prefill_tiled(fake, 1, fake, fake, None, None, fake, 0, fake, fake,
+                                              1, 16, 4, 12, 3, 64, 12, 0, 192, 1, 256, None)
+    assert rc == _lib.ERR_UNSUPPORTED
+    # empty batches are a no-op, not an error
+    assert lib.crucible_attention_decode_paged(None, 1, None, None, None, 0, None, None, 0, 12, 3,
+                                               64, 64, 12, 0, 192, 1024, None, 0, None) == 0
+
+
+def test_workspace_size_formula():
+    lib = _lib.load()
+    # worst case one page per wave: ceil(ceil(2048/16)/4) = 32 splits, 66 floats per (b, h, split)
+    assert lib.crucible_attention_decode_workspace_bytes(16, 12, 2048) == 16 * 12 * 32 * 66 * 4
+    assert lib.crucible_attention_decode_workspace_bytes(0, 12, 2048) == 0

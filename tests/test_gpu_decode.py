@@ -1,0 +1,231 @@
+"""Paged decode parity against the f64 oracle (max-abs <= 2e-3, the stated bar), plus the
+reference's structural contracts: inactive requests untouched, future slots never read,
+paged == contiguous bit for bit, page remapping and batch order invariant."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from attn_cases import disjoint_tables, random_pools
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3  # max-abs 2e-3 against the fp32 reference
+SENTINEL = -12345.25
+
+
+def _dev(a, dev):
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.float16).copy()).to(dev)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _run_decode(gpu, dev, q, k_pool, v_pool, tables, lens, n_head, n_kv, n_layer, layer,
+                max_seq, q_dtype=torch.float16, out_dtype=torch.float32):
+    batch, stride = tables.shape
+    kv = n_kv * 64
+    d_q = torch.from_numpy(q).to(dev).to(q_dtype)
+    out = torch.full((batch, n_head * 64), SENTINEL, dtype=out_dtype, device=dev)
+    gpu.attention_decode_paged(d_q, _dev(k_pool, dev), _dev(v_pool, dev), out, _dev(tables, dev),
+                               _dev(np.asarray(lens, np.int32), dev), batch, n_head, n_kv, 64,
+                               stride, n_layer, layer, kv, max_seq)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def _case(seed, lens, n_head, n_kv, n_layer=3, stride=None, q_f16=True):
+    rng = np.random.default_rng(seed)
+    stride = stride or max(1, -(-max(max(lens), 1) // 16))
+    n_pages = sum(-(-max(n, 1) // 16) for n in lens) + 4
+    k_pool, v_pool = random_pools(rng, n_pages, n_layer, n_kv * 64)
+    tables = disjoint_tables(rng, n_pages, [max(n, 1) for n in lens], stride)
+    q = rng.standard_normal((len(lens), n_head * 64)).astype(np.float32)
+    if q_f16:
+        q = q.astype(np.float16).astype(np.float32)
+    return q, k_pool, v_pool, tables, stride
+
+
+def _oracle(q, k_pool, v_pool, tables, lens, n_head, n_kv, n_layer, layer):
+    lens = np.asarray(lens, np.int32)
+    return oracle.attention_paged_rows(q, k_pool, v_pool, tables, lens, n_head=n_head,
+                                       n_kv_head=n_kv, head_dim=64,
+                                       table_stride=tables.shape[1], n_layer=n_layer, layer=layer)
+
+
+EDGE_LENS = [1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 511, 512, 1023, 1024, 2048]
+
+
+@pytest.mark.parametrize("n_head,n_kv", [(12, 3), (12, 12), (16, 4), (12, 6), (12, 1), (16, 16)])
+def test_decode_matches_oracle_across_page_boundaries(gpu, dev, n_head, n_kv):
+    lens = EDGE_LENS
+    q, kp, vp, tables, stride = _case(n_head * 31 + n_kv, lens, n_head, n_kv)
+    got = _run_decode(gpu, dev, q, kp, vp, tables, lens, n_head, n_kv, 3, 1, stride * 16)
+    want = _oracle(q, kp, vp, tables, lens, n_head, n_kv, 3, 1)
+    err = np.abs(got - want).max()
+    print(f"decode {n_head}/{n_kv}: max-abs {err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("q_dtype,out_dtype", [(torch.float32, torch.float32),
+                                               (torch.float16, torch.float16),
+                                               (torch.float32, torch.float16)])
+def test_decode_dtypes(gpu, dev, q_dtype, out_dtype):
+    lens = [7, 300, 1000]
+    q, kp, vp, tables, stride = _case(3, lens, 12, 3, q_f16=False)
+    got = _run_decode(gpu, dev, q, kp, vp, tables, lens, 12, 3, 3, 1, stride * 16,
+                      q_dtype=q_dtype, out_dtype=out_dtype)
+    qq = q if q_dtype == torch.float32 else q.astype(np.float16).astype(np.float32)
+    want = _oracle(qq, kp, vp, tables, lens, 12, 3, 3, 1)
+    err = np.abs(got - want).max()
+    # an fp16 output adds its own rounding (<= 2^-11 relative of |out| < 4)
+    bound = TOL if out_dtype == torch.float32 else TOL + 2e-3
+    assert err <= bound, err
+    if q_dtype == torch.float32 and out_dtype == torch.float32:
+        assert err <= 1e-4  # f32 query is carried as hi + lo fp16 halves
+
+
+def test_inactive_requests_are_untouched(gpu, dev):
+    lens = [0, 50, 0, -3, 200]
+    q, kp, vp, tables, stride = _case(4, lens, 12, 3)
+    got = _run_decode(gpu, dev, q, kp, vp, tables, lens, 12, 3, 3, 1, stride * 16)
+    for b in (0, 2, 3):
+        assert np.all(got[b] == SENTINEL)
+    want = _oracle(q, kp, vp, tables, lens, 12, 3, 3, 1)
+    assert np.abs(got[[1, 4]] - want[[1, 4]]).max() <= TOL
+
+
+def test_future_slots_are_never_read(gpu, dev):
+    """NaN in every slot at or past seq_len (same page and later pages) changes nothing."""
+    lens = [37, 16, 129]
+    n_layer, layer, kv = 3, 1, 192
+    q, kp, vp, tables, stride = _case(5, lens, 12, 3, stride=16)
+    clean = _run_decode(gpu, dev, q, kp, vp, tables, lens, 12, 3, n_layer, layer, stride * 16)
+    kp2, vp2 = kp.copy(), vp.copy()
+    for b, n in enumerate(lens):
+        for pos in range(n, -(-n // 16) * 16):
+            page = tables[b, pos >> 4]
+            for c in range(kv):
+                kp2[oracle.pool_index(0, page, pos & 15, c, n_layer, layer, kv)] = 0x7E00
+                vp2[oracle.pool_index(1, page, pos & 15, c, n_layer, layer, kv)] = 0x7E00
+    # pages after the last one in the table: point them at a NaN-filled page
+    poisoned = _run_decode(gpu, dev, q, kp2, vp2, tables, lens, 12, 3, n_layer, layer, stride * 16)
+    assert np.array_equal(clean.view(np.uint32), poisoned.view(np.uint32))
+
+
+def test_page_remap_and_batch_order_invariance(gpu, dev):
+    lens = [100, 1, 700, 33]
+    n_layer, layer, kv = 2, 0, 192
+    q, kp, vp, tables, stride = _case(6, lens, 12, 3, n_layer=n_layer)
+    base = _run_decode(gpu, dev, q, kp, vp, tables, lens, 12, 3, n_layer, layer, stride * 16)
+    # move every used page to a new physical id (same contents)
+    rng = np.random.default_rng(60)
+    n_pages = kp.size // (n_layer * 16 * kv)
+    perm = rng.permutation(n_pages)
+    blk = n_layer * 16 * kv
+    kp2 = np.empty_like(kp)
+    vp2 = np.empty_like(vp)
+    for old in range(n_pages):
+        kp2[perm[old] * blk:(perm[old] + 1) * blk] = kp[old * blk:(old + 1) * blk]
+        vp2[perm[old] * blk:(perm[old] + 1) * blk] = vp[old * blk:(old + 1) * blk]
+    tables2 = perm[tables].astype(np.int32)
+    remapped = _run_decode(gpu, dev, q, kp2, vp2, tables2, lens, 12, 3, n_layer, layer, stride * 16)
+    assert np.array_equal(base.view(np.uint32), remapped.view(np.uint32))
+    order = [2, 0, 3, 1]
+    shuffled = _run_decode(gpu, dev, q[order], kp, vp, tables[order], [lens[i] for i in order],
+                           12, 3, n_layer, layer, stride * 16)
+    assert np.array_equal(base[order].view(np.uint32), shuffled.view(np.uint32))
+
+
+def test_paged_equals_contiguous_bit_for_bit(gpu, dev):
+    """The reference's gpu-paged contract (main.rs:1253-1257) for decode."""
+    rng = np.random.default_rng(7)
+    n_head, n_kv, hd, kv, cap, n_layer, layer = 12, 3, 64, 192, 1024, 3, 2
+    for length in [1, 7, 15, 16, 17, 31, 32, 33, 64, 127, 128, 129, 256, 511, 512, 1023]:
+        # contiguous cache [layer][cap][kv] (V: [layer][cap/16][kv][16]) ...
+        k_c, v_c = random_pools(rng, cap // 16, n_layer, kv)  # same element count
+        # ... equals a pool whose page p (one layer) is block p of the layer region
+        q = rng.standard_normal((1, n_head * hd)).astype(np.float16)
+        params = np.array([0, 0, length - 1, length, 0, 0], np.int32)
+        out_c = torch.zeros((1, n_head * hd), dtype=torch.float32, device=dev)
+        gpu.attention_decode(_dev(q, dev), _dev(k_c, dev), _dev(v_c, dev), out_c, n_head, n_kv,
+                             hd, _dev(params, dev), cap, kv, layer * cap * kv)
+        region = slice(layer * cap * kv, (layer + 1) * cap * kv)
+        k_p, v_p = k_c[region].copy(), v_c[region].copy()
+        table = rng.permutation(cap // 16).astype(np.int32)
+        k_perm, v_perm = np.empty_like(k_p), np.empty_like(v_p)
+        blk = 16 * kv
+        for logical in range(cap // 16):
+            phys = table[logical]
+            k_perm[phys * blk:(phys + 1) * blk] = k_p[logical * blk:(logical + 1) * blk]
+            v_perm[phys * blk:(phys + 1) * blk] = v_p[logical * blk:(logical + 1) * blk]
+        out_p = torch.zeros_like(out_c)
+        gpu.attention_decode_paged(_dev(q, dev), _dev(k_perm, dev), _dev(v_perm, dev), out_p,
+                                   _dev(table[None], dev), _dev(np.array([length], np.int32), dev),
+                                   1, n_head, n_kv, hd, cap // 16, 1, 0, kv, cap)
+        torch.cuda.synchronize()
+        assert torch.equal(out_c, out_p), length
+
+
+def test_split_form_matches_oracle(gpu, dev):
+    """attention_split (caller-owned partials, 128-token chunks) on a contiguous cache."""
+    rng = np.random.default_rng(8)
+    n_head, n_kv, hd, kv, cap = 12, 3, 64, 192, 1024
+    k_c, v_c = random_pools(rng, cap // 16, 1, kv)
+    for length in [1, 128, 129, 777, 1024]:
+        q = rng.standard_normal((1, n_head * hd)).astype(np.float32)
+        params = np.array([0, 0, length - 1, length, 0, 0], np.int32)
+        n_chunks = cap // 128
+        po = torch.zeros(n_head * n_chunks * hd, device=dev)
+        pm = torch.zeros(n_head * n_chunks, device=dev)
+        pl = torch.zeros(n_head * n_chunks, device=dev)
+        out = torch.zeros((1, n_head * hd), device=dev)
+        gpu.attention_split(_dev(q, dev), _dev(k_c, dev), _dev(v_c, dev), po, pm, pl, out, n_head,
+                            n_kv, hd, _dev(params, dev), cap, kv, 0)
+        torch.cuda.synchronize()
+        want = _oracle(q, k_c, v_c, np.arange(cap // 16, dtype=np.int32)[None], [length], n_head,
+                       n_kv, 1, 0)
+        assert np.abs(out.cpu().numpy() - want).max() <= TOL
+
+
+def test_config2_decode_b1_ctx1024(gpu, dev):
+    from crucible_amd.workloads import config2_decode_b1
+    for n_kv in (3, 12):
+        cfg = config2_decode_b1(n_kv_head=n_kv)
+        rng = np.random.default_rng(cfg.seed)
+        kp, vp = random_pools(rng, cfg.n_pages, cfg.n_layer, cfg.kv_dim)
+        q = rng.standard_normal((1, 12 * 64)).astype(np.float16).astype(np.float32)
+        got = _run_decode(gpu, dev, q, kp, vp, cfg.tables, cfg.lens, 12, n_kv, cfg.n_layer, 0,
+                          cfg.max_seq)
+        want = _oracle(q, kp, vp, cfg.tables, cfg.lens, 12, n_kv, cfg.n_layer, 0)
+        assert np.abs(got - want).max() <= TOL
+
+
+def test_config3_decode_b16_all_layers(gpu, dev):
+    """BASELINE config 3 at full size (8192-page pool, 12 layers, ctx 65..2048), GQA-3."""
+    from crucible_amd.workloads import config3_decode_b16, make_pools
+    cfg = config3_decode_b16()
+    rng = np.random.default_rng(cfg.seed)
+    tables = disjoint_tables(rng, cfg.n_pages, cfg.lens, cfg.table_stride)
+    kp, vp = make_pools(cfg.n_pages, cfg.n_layer, cfg.kv_dim, cfg.seed, dev)
+    # compact copy of the used pages for the oracle
+    used = np.unique(np.concatenate([tables[b, :-(-int(n) // 16)] for b, n in enumerate(cfg.lens)]))
+    remap = np.zeros(cfg.n_pages, np.int32)
+    remap[used] = np.arange(used.size, dtype=np.int32)
+    blk = cfg.n_layer * 16 * cfg.kv_dim
+    idx = torch.from_numpy(used).long().to(dev)
+    kc = kp.view(cfg.n_pages, blk)[idx].cpu().numpy().view(np.uint16).reshape(-1)
+    vc = vp.view(cfg.n_pages, blk)[idx].cpu().numpy().view(np.uint16).reshape(-1)
+    ctables = remap[tables]
+    q_all = torch.randn(cfg.n_layer, 16, 12 * 64, device=dev).to(torch.float16)
+    out = torch.zeros(16, 12 * 64, device=dev)
+    d_tab, d_len = _dev(tables, dev), _dev(cfg.lens, dev)
+    worst = 0.0
+    for layer in range(cfg.n_layer):
+        gpu.attention_decode_paged(q_all[layer], kp, vp, out, d_tab, d_len, 16, 12, 3, 64,
+                                   cfg.table_stride, cfg.n_layer, layer, cfg.kv_dim, cfg.max_seq)
+        torch.cuda.synchronize()
+        want = _oracle(q_all[layer].float().cpu().numpy(), kc, vc, ctables, cfg.lens, 12, 3,
+                       cfg.n_layer, layer)
+        worst = max(worst, float(np.abs(out.cpu().numpy() - want).max()))
+    print(f"config3 all layers: max-abs {worst:.3e}")
+    assert worst <= TOL

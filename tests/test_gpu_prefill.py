@@ -1,0 +1,224 @@
+"""Causal and packed prefill parity.
+
+The reference's attention corpus (gpu_attention_validation.rs:431-509: page boundaries,
+offsets, singles up to 1024, packed 16x16..2x512, ragged rows at four Q-scale profiles) runs
+through every prefill entry point (segments, owners/positions, params, contiguous) and is
+compared with the f64 oracle on every element (bar: max-abs 2e-3). Structural contracts are
+exact: future-page poison leaves outputs bit-identical (:597-632), descriptor composition,
+order and page reuse leave each request's bits unchanged (:639-682), and output rows outside
+the written range keep their sentinel (:23, :271-287).
+"""
+import numpy as np
+import pytest
+import torch
+
+import attn_cases as A
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _dev(a, dev):
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.float16).copy()).to(dev)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+class Device:
+    def __init__(self, fx, dev, q_dtype=torch.float32):
+        self.fx = fx
+        self.q = torch.from_numpy(fx.q).to(dev).to(q_dtype)
+        self.k = _dev(fx.k_pool, dev)
+        self.v = _dev(fx.v_pool, dev)
+        self.tables = _dev(fx.tables, dev)
+        self.owners = _dev(fx.owners, dev)
+        self.positions = _dev(fx.positions, dev)
+        self.segments = _dev(fx.segments, dev)
+        self.out = torch.full((fx.rows * A.D + 64,), A.SENTINEL, dtype=torch.float32, device=dev)
+
+    def reset(self):
+        self.out.fill_(A.SENTINEL)
+
+    def result(self):
+        torch.cuda.synchronize()
+        host = self.out.cpu().numpy()
+        assert np.all(host[self.fx.rows * A.D:] == A.SENTINEL), "output guard overwritten"
+        body = host[:self.fx.rows * A.D].reshape(self.fx.rows, A.D)
+        assert np.all(np.isfinite(body)), "nonfinite output"
+        return body
+
+
+def run_segments(gpu, d):
+    fx = d.fx
+    gpu.attention_prefill_tiled(d.q, d.k, d.v, None, None, d.out, d.tables, d.segments,
+                                len(fx.case.slices), fx.max_chunk, A.STRIDE, A.HEADS, A.KV_HEADS,
+                                A.HD, A.LAYERS, A.LAYER, A.KD, False, 1024)
+
+
+def run_owners(gpu, d):
+    fx = d.fx
+    gpu.attention_prefill_packed(d.q, d.k, d.v, d.out, d.tables, d.owners, d.positions, fx.rows,
+                                 A.STRIDE, A.HEADS, A.KV_HEADS, A.HD, A.LAYERS, A.LAYER, A.KD,
+                                 A.CONTEXT)
+
+
+CASES = A.cases()
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c.name for c in CASES])
+def test_corpus_segments_and_owners_match_oracle(gpu, dev, case):
+    fx = A.fixture(case)
+    want = A.oracle_out(fx)
+    d = Device(fx, dev)
+    errs = []
+    for runner in (run_segments, run_owners):
+        d.reset()
+        runner(gpu, d)
+        got = d.result()
+        errs.append(float(np.abs(got - want).max()))
+    print(f"{case.name}: segments {errs[0]:.3e} owners {errs[1]:.3e}")
+    assert max(errs) <= TOL
+
+
+@pytest.mark.parametrize("case", [c for c in CASES if c.name.startswith("boundary-")],
+                         ids=lambda c: c.name)
+def test_future_pages_do_not_affect_output(gpu, dev, case):
+    fx = A.fixture(case)
+    if case.slices[0].start + case.slices[0].len >= A.CONTEXT:
+        pytest.skip("no future page inside the context")
+    poisoned = A.fixture(case, poison_future=True)
+    for runner in (run_segments, run_owners):
+        d = Device(fx, dev)
+        runner(gpu, d)
+        clean = d.result()
+        p = Device(poisoned, dev)
+        runner(gpu, p)
+        assert np.array_equal(clean.view(np.uint32), p.result().view(np.uint32))
+
+
+def test_single_sequence_params_and_contiguous_forms(gpu, dev):
+    """attention_prefill_paged (params[5] offset) and attention_prefill (contiguous)."""
+    for case in [c for c in CASES if c.name in ("single-1024", "single-941", "offset-255")]:
+        fx = A.fixture(case)
+        want = A.oracle_out(fx)
+        d = Device(fx, dev)
+        s0 = case.slices[0]
+        rows = s0.len
+        params = _dev(np.array([0, 0, 0, 0, 0, s0.start], np.int32), dev)
+        gpu.attention_prefill_paged(d.q[:rows], d.k, d.v, d.out, d.tables[0], rows,
+                                    A.HEADS, A.KV_HEADS, A.HD, A.LAYERS, A.LAYER, A.KD,
+                                    A.CONTEXT, params)
+        got = d.result()[:rows]
+        assert np.abs(got - want[:rows]).max() <= TOL
+        # contiguous cache holding the same history for that request at layer 1
+        cap = A.CONTEXT
+        k_c = np.zeros(A.LAYERS * cap * A.KD, np.uint16)
+        v_c = np.zeros_like(k_c)
+        n_hist = s0.start + s0.len
+        kd = oracle.f32_to_f16_bits(oracle.gather(0, fx.k_pool, fx.tables[0], n_hist, A.KD,
+                                                  A.LAYERS, A.LAYER))
+        vd = oracle.f32_to_f16_bits(oracle.gather(1, fx.v_pool, fx.tables[0], n_hist, A.KD,
+                                                  A.LAYERS, A.LAYER))
+        for kind, cache, src in ((0, k_c, kd), (1, v_c, vd)):
+            oracle.cache_store(oracle.STORE_CONTIG, kind, cache, src, rows=n_hist, kv_dim=A.KD,
+                               layer_base=A.LAYER * cap * A.KD, pos_offset=0)
+        d.reset()
+        gpu.attention_prefill(d.q[:rows], _dev(k_c, dev), _dev(v_c, dev), d.out, rows,
+                              A.HEADS, A.KV_HEADS, A.HD, cap, A.KD, A.LAYER * cap * A.KD,
+                              s0.start)
+        got_c = d.result()[:rows]
+        # same keys, same arithmetic: the contiguous form is bit-identical to the paged one
+        assert np.array_equal(got_c.view(np.uint32), got.view(np.uint32))
+
+
+def test_composition_order_and_page_reuse_invariance(gpu, dev):
+    """gpu_attention_validation.rs:639-682: each request's bits are independent of which other
+    requests share the call, their order, and the physical pages assigned."""
+    expected = {}
+    checks = 0
+    for count in (16, 1, 8, 2, 4, 16):
+        for order in range(3):
+            case = A.homogeneous("composition", count, 17, 511, A.SEED + count + order)
+            if order == 1:
+                case.slices.reverse()
+            if order == 2:
+                k = count // 2
+                case.slices = case.slices[k:] + case.slices[:k]
+            fx = A.fixture(case)
+            for runner in (run_segments, run_owners):
+                d = Device(fx, dev)
+                runner(gpu, d)
+                out = d.result()
+                for row, s in enumerate(case.slices):
+                    bits = out[row * 17:(row + 1) * 17].view(np.uint32).tobytes()
+                    key = (runner.__name__, s.id)
+                    if key in expected:
+                        assert bits == expected[key], f"{runner.__name__} request {s.id}"
+                        checks += 1
+                    else:
+                        expected[key] = bits
+    assert checks > 50
+
+
+def test_fp16_query_and_fp16_output(gpu, dev):
+    case = [c for c in CASES if c.name == "ragged-profile-0"][0]
+    fx = A.fixture(case)
+    q16 = fx.q.astype(np.float16).astype(np.float32)
+    want = A.oracle_out(fx, q=q16)
+    d = Device(fx, dev, q_dtype=torch.float16)
+    out16 = torch.zeros(fx.rows, A.D, dtype=torch.float16, device=dev)
+    gpu.attention_prefill_tiled(d.q, d.k, d.v, None, None, out16, d.tables, d.segments,
+                                len(case.slices), fx.max_chunk, A.STRIDE, A.HEADS, A.KV_HEADS,
+                                A.HD, A.LAYERS, A.LAYER, A.KD)
+    torch.cuda.synchronize()
+    assert np.abs(out16.float().cpu().numpy() - want).max() <= TOL + 2e-3
+
+
+def _packed_config_check(gpu, dev, cfg, seed):
+    """Append every sequence's K/V through the packed scatter, then segment prefill."""
+    rng = np.random.default_rng(seed)
+    kv = cfg.kv_dim
+    rows = cfg.rows
+    owners = np.concatenate([np.full(n, i, np.int32) for i, n in enumerate(cfg.seq_lens)])
+    positions = np.concatenate([np.arange(n, dtype=np.int32) for n in cfg.seq_lens])
+    k_src = oracle.f32_to_f16_bits(rng.standard_normal((rows, kv)))
+    v_src = oracle.f32_to_f16_bits(rng.standard_normal((rows, kv)))
+    q = oracle.f32_to_f16_bits(rng.standard_normal((rows, cfg.n_head * 64)))
+    n_elem = cfg.n_pages * cfg.n_layer * 16 * kv
+    stride = cfg.tables.shape[1]
+    k_pool = torch.zeros(n_elem, dtype=torch.float16, device=dev)
+    v_pool = torch.zeros(n_elem, dtype=torch.float16, device=dev)
+    d_tab, d_own, d_pos = _dev(cfg.tables, dev), _dev(owners, dev), _dev(positions, dev)
+    gpu.cache_store_packed_paged(_dev(k_src, dev), k_pool, d_tab, d_own, d_pos, rows, kv, stride,
+                                 cfg.n_layer, 0, kind="k")
+    gpu.cache_store_packed_paged(_dev(v_src, dev), v_pool, d_tab, d_own, d_pos, rows, kv, stride,
+                                 cfg.n_layer, 0, kind="v")
+    from crucible_amd.paged import segments_from_cu_seqlens
+    seg, max_chunk = segments_from_cu_seqlens(cfg.cu_seqlens)
+    out = torch.zeros(rows, cfg.n_head * 64, device=dev)
+    gpu.attention_prefill_tiled(_dev(q, dev), k_pool, v_pool, None, None, out, d_tab,
+                                _dev(seg, dev), len(cfg.seq_lens), max_chunk, stride, cfg.n_head,
+                                cfg.n_kv_head, 64, cfg.n_layer, 0, kv)
+    torch.cuda.synchronize()
+    kp = k_pool.cpu().numpy().view(np.uint16)
+    vp = v_pool.cpu().numpy().view(np.uint16)
+    want = oracle.attention_paged_rows(oracle.f16_bits_to_f32(q), kp, vp, cfg.tables,
+                                       positions + 1, table_index=owners, n_head=cfg.n_head,
+                                       n_kv_head=cfg.n_kv_head, head_dim=64, table_stride=stride,
+                                       n_layer=cfg.n_layer, layer=0)
+    err = float(np.abs(out.cpu().numpy() - want).max())
+    print(f"{cfg.name}: max-abs {err:.3e}")
+    assert err <= TOL
+
+
+def test_config1_causal_prefill_512(gpu, dev):
+    from crucible_amd.workloads import config1_prefill
+    for n_kv in (12, 3):
+        _packed_config_check(gpu, dev, config1_prefill(n_kv_head=n_kv), 11)
+
+
+def test_config4_packed_varlen_350m(gpu, dev):
+    from crucible_amd.workloads import config4_packed
+    _packed_config_check(gpu, dev, config4_packed(), 12)

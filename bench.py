@@ -1,0 +1,406 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path (one JSON line on stdout).
+
+Headline workload: continuous-batching paged decode at batch 16,
+120m preset geometry (12 query heads, 3 KV heads of head_dim 64, 12 layers), fp16 KV in
+16-token pages from an 8192-page pool, context lengths seeded U[64, 2048]. One step is,
+for every layer, the KV append of one new token per sequence (K and V, f32 -> fp16) and
+paged decode attention over len + 1 keys, done by one fused launch per layer. The
+12-layer step is captured once per batch in a HIP graph and replayed, so the timed
+region measures the device work, not Python.
+
+Consecutive steps rotate over several disjoint batches drawn from the same pool, so a
+step never finds its KV pages in the 256 MB last-level cache from the previous step.
+
+value  = algorithmic bytes of the whole step (KV pages read, appended rows, queries,
+         outputs, tables) / wall time of the timed steps, in GB/s.
+roofline = the one kernel of the step (fused append + paged decode attention): algorithmic
+         bytes per launch over its average launch duration, HIP events on the replay stream.
+cpu_baseline = the reference's CPU attention path (gather + torch SDPA, fp32) on the host
+         cores, on a bounded sample of the same workload.
+extras = the same step as the reference's three launches per layer and as attention
+         alone, batch-1 decode (config 2), the MHA stress variant of config 3, and the
+         causal (config 1) and packed (config 4) prefill kernels.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
+METRIC = "paged-attn decode HBM GB/s (% peak); prefill attn TFLOP/s; 120M tok/s at b16"
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=300)
+    p.add_argument("--warmup", type=int, default=30)
+    p.add_argument("--kv-heads", type=int, default=3, help="3 = 120m preset (GQA), 12 = MHA")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extras", action="store_true")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="also run a plain 256 MiB device copy (PMC traffic calibration)")
+    return p.parse_args()
+
+
+# ---------------------------------------------------------------- decode workload
+
+class DecodeBench:
+    """Config 3 (or 2) on the device: pools, per-layer inputs, one graph per rotation."""
+
+    def __init__(self, gpu, dev, *, batch, n_head, n_kv_head, n_layer, n_pages, max_seq,
+                 rotations, seed, fixed_lens=None):
+        import numpy as np
+        import torch
+
+        from crucible_amd import workloads as W
+        from crucible_amd.gpu import pool_elems
+
+        self.gpu, self.dev = gpu, dev
+        self.batch, self.n_head, self.n_kv, self.n_layer = batch, n_head, n_kv_head, n_layer
+        self.kv_dim = n_kv_head * 64
+        self.max_seq = max_seq
+        self.stride = max_seq // 16
+        rng = np.random.default_rng(seed)
+        # draw batches until the pool is used up (at most `rotations`)
+        self.lens, self.tables = [], []
+        perm = rng.permutation(n_pages).astype(np.int32)
+        cur = 0
+        for _ in range(rotations):
+            if fixed_lens is not None:
+                existing = np.asarray(fixed_lens, np.int32) - 1
+            else:
+                existing = rng.integers(64, max_seq, size=batch).astype(np.int32)
+            lens = existing + 1
+            need = [W.ceil_div(int(n), 16) for n in lens]
+            if cur + sum(need) > n_pages:
+                break
+            tab = np.zeros((batch, self.stride), np.int32)
+            for b, k in enumerate(need):
+                tab[b, :k] = perm[cur:cur + k]
+                cur += k
+            self.lens.append(lens)
+            self.tables.append(tab)
+        self.rotations = len(self.lens)
+        n = pool_elems(n_pages, n_layer, self.kv_dim)
+        self.k_pool = W.device_normal((n,), torch.float16, seed + 11, dev)
+        self.v_pool = W.device_normal((n,), torch.float16, seed + 12, dev)
+        self.q = W.device_normal((n_layer, batch, n_head * 64), torch.float16, seed + 13, dev)
+        self.src_k = W.device_normal((n_layer, batch, self.kv_dim), torch.float32, seed + 14, dev)
+        self.src_v = W.device_normal((n_layer, batch, self.kv_dim), torch.float32, seed + 15, dev)
+        self.out = torch.zeros((n_layer, batch, n_head * 64), dtype=torch.float32, device=dev)
+        self.d_tables = [torch.from_numpy(t).to(dev) for t in self.tables]
+        self.d_lens = [torch.from_numpy(x).to(dev) for x in self.lens]
+        self.d_pos = [torch.from_numpy(x - 1).to(dev) for x in self.lens]
+        self.ws = gpu.workspace(batch, n_head, max_seq)
+
+    # algorithmic bytes ----------------------------------------------------------
+    def decode_bytes(self, r: int) -> int:
+        """One decode launch: K and V of every visible key (fp16), fp16 q, f32 out,
+        the used table entries and the lengths."""
+        lens = self.lens[r].astype("int64")
+        kv = int(lens.sum()) * 2 * self.kv_dim * 2
+        pages = int(sum((int(n) + 15) // 16 for n in lens))
+        return kv + self.batch * self.n_head * 64 * (2 + 4) + 4 * pages + 4 * self.batch
+
+    def append_bytes(self) -> int:
+        """K and V appends of one layer: f32 rows in, fp16 rows out, positions, table reads."""
+        return 2 * (self.batch * self.kv_dim * (4 + 2) + 8 * self.batch)
+
+    def step_bytes(self, r: int) -> int:
+        return self.n_layer * (self.decode_bytes(r) + self.append_bytes())
+
+    # launches ---------------------------------------------------------------------
+    def append(self, r: int, layer: int):
+        g = self.gpu
+        for src, pool, kind in ((self.src_k, self.k_pool, "k"), (self.src_v, self.v_pool, "v")):
+            g.cache_store_rows_paged(src[layer], pool, self.d_tables[r], self.d_pos[r],
+                                     self.batch, self.kv_dim, self.stride, self.n_layer, layer,
+                                     kind=kind)
+
+    def decode(self, r: int, layer: int):
+        self.gpu.attention_decode_paged(
+            self.q[layer], self.k_pool, self.v_pool, self.out[layer], self.d_tables[r],
+            self.d_lens[r], self.batch, self.n_head, self.n_kv, 64, self.stride, self.n_layer,
+            layer, self.kv_dim, self.max_seq, workspace=self.ws)
+
+    def fused(self, r: int, layer: int):
+        self.gpu.attention_decode_paged_append(
+            self.q[layer], self.src_k[layer], self.src_v[layer], self.k_pool, self.v_pool,
+            self.out[layer], self.d_tables[r], self.d_pos[r], self.d_lens[r], self.batch,
+            self.n_head, self.n_kv, 64, self.stride, self.n_layer, layer, self.kv_dim,
+            self.max_seq, workspace=self.ws)
+
+    def step(self, r: int, mode: str):
+        """One 12-layer step: 'fused' (one launch per layer), 'separate' (the reference's
+        append K, append V, decode), or 'decode' (attention only)."""
+        for layer in range(self.n_layer):
+            if mode == "fused":
+                self.fused(r, layer)
+            elif mode == "separate":
+                self.append(r, layer)
+                self.decode(r, layer)
+            else:
+                self.decode(r, layer)
+
+    def capture(self, mode: str):
+        """One graph per rotation holding a full step."""
+        import torch
+
+        s = torch.cuda.Stream(self.dev)
+        s.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(s):
+            for r in range(self.rotations):
+                self.step(r, mode)
+        torch.cuda.current_stream(self.dev).wait_stream(s)
+        torch.cuda.synchronize(self.dev)
+        graphs = []
+        for r in range(self.rotations):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.step(r, mode)
+            graphs.append(g)
+        torch.cuda.synchronize(self.dev)
+        return graphs
+
+    def time_steps(self, graphs, steps: int, warmup: int, bytes_fn=None):
+        """Wall time of `steps` graph replays (rotating batches), HIP events on the replay
+        stream alongside; returns (ms per step by wall clock, ms per step by events, bytes)."""
+        import torch
+
+        for i in range(warmup):
+            graphs[i % len(graphs)].replay()
+        flush_llc(self.dev)
+        torch.cuda.synchronize(self.dev)
+        stream = torch.cuda.current_stream(self.dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        bytes_fn = bytes_fn or self.step_bytes
+        nbytes = sum(bytes_fn(i % len(graphs)) for i in range(steps))
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for i in range(steps):
+            graphs[i % len(graphs)].replay()
+        e1.record(stream)
+        torch.cuda.synchronize(self.dev)
+        wall = time.perf_counter() - t0
+        return wall * 1e3 / steps, e0.elapsed_time(e1) / steps, nbytes / steps
+
+
+def flush_llc(dev):
+    """Touch 512 MiB so the 256 MB last-level cache holds nothing of the workload."""
+    import torch
+
+    buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+    del buf
+
+
+# ---------------------------------------------------------------- prefill workloads
+
+def bench_prefill(gpu, dev, cfg, launches: int = 50):
+    """Time the segment-form prefill kernel (gpu.rs:1606-1751 path) on config 1 or 4."""
+    import numpy as np
+    import torch
+
+    from crucible_amd import workloads as W
+    from crucible_amd.gpu import pool_elems
+    from crucible_amd.paged import segments_from_cu_seqlens
+
+    kv_dim = cfg.kv_dim
+    rows = cfg.rows
+    stride = cfg.tables.shape[1]
+    k_pool = W.device_normal((pool_elems(cfg.n_pages, 1, kv_dim),), torch.float16, cfg.seed + 1, dev)
+    v_pool = W.device_normal((pool_elems(cfg.n_pages, 1, kv_dim),), torch.float16, cfg.seed + 2, dev)
+    q = W.device_normal((rows, cfg.n_head * 64), torch.float16, cfg.seed + 3, dev)
+    out = torch.empty((rows, cfg.n_head * 64), dtype=torch.float32, device=dev)
+    seg, max_chunk = segments_from_cu_seqlens(cfg.cu_seqlens)
+    d_seg = torch.from_numpy(np.ascontiguousarray(seg)).to(dev)
+    d_tab = torch.from_numpy(cfg.tables).to(dev)
+
+    def run():
+        gpu.attention_prefill_tiled(q, k_pool, v_pool, None, None, out, d_tab, d_seg,
+                                    len(cfg.seq_lens), max_chunk, stride, cfg.n_head,
+                                    cfg.n_kv_head, 64, 1, 0, kv_dim)
+
+    for _ in range(5):
+        run()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(launches)]
+    for a, b in ev:
+        a.record(stream)
+        run()
+        b.record(stream)
+    torch.cuda.synchronize(dev)
+    ms = sorted(a.elapsed_time(b) for a, b in ev)
+    avg = sum(ms) / len(ms)
+    tflops = cfg.flops() / (avg * 1e-3) / 1e12
+    return {"workload": cfg.name, "n_head": cfg.n_head, "n_kv_head": cfg.n_kv_head,
+            "seq_lens": [int(x) for x in cfg.seq_lens], "flops": cfg.flops(),
+            "us_per_launch": round(avg * 1e3, 3), "us_median": round(ms[len(ms) // 2] * 1e3, 3),
+            "tflops": round(tflops, 3), "frac_of_mfma_f16_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 5)}
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(bench: DecodeBench, seconds: float):
+    from oracle import cpu_path
+
+    cores = cpu_path.threads()
+    lens = bench.lens[0]
+    cpu = cpu_path.DecodeBatchCPU(lens, bench.n_layer, bench.n_head, bench.n_kv, seed=1)
+    reps, s_per_step = cpu_path.time_bounded(cpu.step, seconds)
+    gbs = bench.step_bytes(0) / s_per_step / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "ms_per_step": round(s_per_step * 1e3, 3),
+            "sample": (f"{reps} full {bench.n_layer}-layer decode steps of batch 0 "
+                       f"(16 sequences, lens {int(lens.min())}..{int(lens.max())}): per layer "
+                       f"and sequence a row append, a page gather and torch SDPA, fp32, "
+                       f"torch {__import__('torch').__version__}")}
+
+
+# ---------------------------------------------------------------- main
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the attention path shards by sequence or KV head, see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    import numpy as np  # noqa: F401
+    import torch
+
+    from crucible_amd import workloads as W
+    from crucible_amd.gpu import Gpu
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    gpu = Gpu(0)
+
+    def log(msg):
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    log(f"{gpu.version()} on {torch.cuda.get_device_name(0)}")
+    b16 = DecodeBench(gpu, dev, batch=16, n_head=12, n_kv_head=args.kv_heads, n_layer=12,
+                      n_pages=8192, max_seq=2048, rotations=7, seed=W.BASE_SEED + 2)
+    log(f"config 3: {b16.rotations} rotations, lens of rotation 0: {b16.lens[0].tolist()}")
+    fused_graphs = b16.capture("fused")
+    log("graphs captured")
+
+    # headline: the whole step (12 fused append + decode launches), timed steps
+    ms_per_step, ev_ms_per_step, step_bytes = b16.time_steps(fused_graphs, args.steps,
+                                                             args.warmup)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"timed {args.steps} steps: {ms_per_step:.4f} ms/step (events {ev_ms_per_step:.4f}), "
+        f"{value:.1f} GB/s")
+
+    # dominant kernel: the fused decode kernel is the only kernel of the step, so its
+    # average launch duration is the event-timed step over its 12 launches (graph replay:
+    # each launch starts when the previous one ends, as in the rocprof trace)
+    launch_us = ev_ms_per_step * 1e3 / b16.n_layer
+    bytes_per_launch = step_bytes / b16.n_layer
+    achieved = bytes_per_launch / (launch_us * 1e-6) / 1e9
+    log(f"fused decode launch: {launch_us:.2f} us avg, {achieved:.1f} GB/s")
+    roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "decode_kernel<1, 8, false, true> (append + split-K attention + "
+                          "combine, one launch per layer)",
+                "us_per_launch": round(launch_us, 3),
+                "algorithmic_bytes_per_launch": int(bytes_per_launch)}
+    del fused_graphs
+
+    extras = {}
+    if not args.no_extras:
+        # the reference's three launches per layer, and attention alone, same batches
+        for mode in ("separate", "decode"):
+            graphs = b16.capture(mode)
+            attn_only = (lambda r: b16.n_layer * b16.decode_bytes(r)) if mode == "decode" else None
+            ms, ev, by = b16.time_steps(graphs, max(60, args.steps // 4), 10, attn_only)
+            extras[f"step_{mode}"] = {"ms_per_step": round(ms, 5),
+                                      "us_per_layer": round(ev * 1e3 / b16.n_layer, 3),
+                                      "gbs": round(by / (ev * 1e-3) / 1e9, 2)}
+            del graphs
+        # config 2: batch 1, ctx 1024, 4096-page pool
+        b1 = DecodeBench(gpu, dev, batch=1, n_head=12, n_kv_head=args.kv_heads, n_layer=12,
+                         n_pages=4096, max_seq=1024, rotations=48, seed=W.BASE_SEED + 1,
+                         fixed_lens=[1024])
+        graphs = b1.capture("decode")
+        ms, ev, _ = b1.time_steps(graphs, 96, 10)
+        by1 = b1.decode_bytes(0)
+        extras["decode_b1_ctx1024"] = {"us_per_launch": round(ev * 1e3 / 12, 3),
+                                       "gbs": round(by1 / (ev * 1e-3 / 12) / 1e9, 2),
+                                       "bytes_per_launch": int(by1)}
+        del graphs, b1
+        if args.kv_heads != 12:
+            mha = DecodeBench(gpu, dev, batch=16, n_head=12, n_kv_head=12, n_layer=12,
+                              n_pages=8192, max_seq=2048, rotations=7, seed=W.BASE_SEED + 2)
+            graphs = mha.capture("fused")
+            ms, ev, by = mha.time_steps(graphs, 60, 10)
+            gbs = by / (ev * 1e-3) / 1e9
+            extras["fused_b16_mha12"] = {"us_per_launch": round(ev * 1e3 / 12, 3),
+                                         "gbs": round(gbs, 2),
+                                         "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                         "bytes_per_launch": int(by / 12)}
+            del graphs, mha
+        torch.cuda.empty_cache()
+        extras["prefill_config1"] = bench_prefill(gpu, dev, W.config1_prefill(n_kv_head=12))
+        extras["prefill_config1_gqa3"] = bench_prefill(gpu, dev, W.config1_prefill(n_kv_head=3))
+        extras["packed_config4"] = bench_prefill(gpu, dev, W.config4_packed())
+        for k, v in extras.items():
+            log(f"{k}: {v}")
+
+    if args.copy_probe:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        log("copy probe: 5 x 256 MiB device copies")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(b16, args.cpu_seconds)
+        log(f"cpu baseline: {cpu}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "config3 paged decode b16, ctx U[64,2048], 12 layers, "
+                               "append + attention per layer",
+                   "batch": 16, "n_head": 12, "n_kv_head": args.kv_heads, "head_dim": 64,
+                   "n_layer": 12, "page_tokens": 16, "pool_pages": 8192,
+                   "rotations": b16.rotations, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extras": extras,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,16 +1,22 @@
-// Paged decode attention for gfx950: split-K over pages, MFMA for QK^T and PV.
+// Paged decode attention for gfx950: split-K over pages, MFMA for QK^T and PV, and the
+// cross-split combine fused into the same launch.
 //
 // Reference semantics (engine/kernels/kernels.cu:1741-1839, attention_decode_paged_f32):
 // for request b and query head h, kv head g = h / (n_head / n_kv_head),
 //   s_j = (q . k_j) / sqrt(64) for j < seq_lens[b];  out = softmax(s) . V.
 // seq_lens[b] <= 0 marks an inactive request (no output is written).
 //
-// Work decomposition. A workgroup owns one (request b, kv head g, split s); a split
-// is WAVES * PAGES consecutive logical pages. Each of the 4 waves owns PAGES pages and
-// serves all n_rep query heads that share kv head g, so a K/V page is read from HBM
-// once per GQA group, not once per query head. Grid size depends only on
-// (batch, n_kv_head, max_seq), never on the current lengths, so the launch can be
-// captured in a hipGraph; splits past a request's end exit at once.
+// Work decomposition. A workgroup owns one (request b, kv head g, split s); a split is
+// WAVES * PAGES consecutive logical pages. Each wave owns PAGES pages and serves all
+// n_rep query heads that share kv head g, so a K/V page is read from HBM once per GQA
+// group, not once per query head. Grid size depends only on (batch, n_kv_head, max_seq),
+// never on the current lengths, so the launch can be captured in a hipGraph; splits past
+// a request's end exit at once.
+//
+// Latency chain. The request length and the page ids of the wave's pages are loaded
+// together (page ids below the table capacity are always in bounds), so one dependent
+// round trip precedes the K/V loads, and every K/V load of the wave is in flight before
+// any arithmetic.
 //
 // Per page and wave (16 tokens):
 //   S^T[16 tok x 16 col] = K[16 tok x 64] . Q^T[64 x 16 col]   2x mfma_f32_16x16x32_f16
@@ -20,12 +26,17 @@
 //     4 dim blocks x mfma_f32_16x16x16f16, with P split into fp16 hi + lo parts so
 //     the product keeps ~22 bits of P (an f32 query is split the same way for QK).
 // K operands come straight from the page (row `tok`, 8 channels per lane); V operands
-// come straight from the transposed V page (channel row, 4 slots per lane). No LDS is
-// needed until the 4 waves of a workgroup merge their partial softmax states.
+// come straight from the transposed V page (channel row, 4 slots per lane). LDS is only
+// used to merge the waves' softmax states.
 //
-// The combine across splits (reference kernels.cu:806-850) uses the exact algebra
-//   M = max m_s, L = sum l_s 2^(m_s - M), out = sum o_s 2^(m_s - M) / L
-// and a request that fits in one split is written directly by its only workgroup.
+// Combine across splits (reference kernels.cu:806-850), exact algebra in base 2:
+//   M = max m_s, L = sum l_s 2^(m_s - M), out = sum o_s 2^(m_s - M) / L.
+// A request that fits in one split is written directly by its only workgroup. Otherwise
+// every split writes its partial (o, m, l) with agent-coherent stores, waits for them to
+// complete, and bumps a per-(request, kv head) counter; the workgroup that brings the counter to the number of active splits
+// resets it to zero and performs the combine. Counters therefore read zero between
+// launches: the workspace must be zeroed once when it is allocated, and one workspace
+// serves one launch at a time.
 #include "common.hpp"
 
 #include <cmath>
@@ -34,40 +45,42 @@
 namespace crucible {
 namespace {
 
-constexpr int kWaves = 4;
-
-enum LenMode { kLensArray = 0, kPositionsPlusOne = 1, kParamsSeq = 2 };
-
 struct DecodeArgs {
-    const void* q;
-    const half_t* k_pool;
-    const half_t* v_pool;
-    void* out;
+    // Everything the first loads need sits at the front, so one kernel-argument fetch
+    // covers it and the length and page-id loads can issue together.
     const int32_t* tables;       // nullptr: contiguous cache (page = pos >> 4)
-    const int32_t* table_index;  // nullptr: row b uses table row b
-    const int32_t* lens;
+    const int32_t* lens;         // request b's length is lens[b * lens_stride + lens_off]
+    int64_t table_stride;
+    int lens_stride;             // 1: per-request lengths; 0: one length in params
+    int lens_off;                // 0, or CRUCIBLE_PARAM_SEQ for a params buffer
+    int max_pages;               // ceil(max_seq / 16) <= table_stride
+    int split_pages;
+    int max_seq;
+    int n_kv_head;
+    const void* q;
+    half_t* k_pool;              // written only by the fused append
+    half_t* v_pool;
+    void* out;
+    const int32_t* positions;    // fused append: row b goes to position positions[b]
+    const void* k_new;           // fused append: [batch][kv_dim] rows (f32 or fp16)
+    const void* v_new;
+    int kv_new_f16;
     float* po;                   // [batch][n_head][n_splits][64]
     float* pm;                   // [batch][n_head][n_splits]
     float* pl;                   // [batch][n_head][n_splits]
+    uint32_t* counters;          // [batch * n_kv_head]; nullptr: combine in a second kernel
     PoolAddr addr;
-    int64_t table_stride;
     int64_t q_row_stride;        // elements between query rows (n_head * 64)
-    int len_mode;
     int batch;
     int n_head;
-    int n_kv_head;
     int n_rep;
     int n_splits;
-    int split_pages;
-    int max_seq;
     int out_f16;
     float scale_log2;            // (1/sqrt(64)) * log2(e)
 };
 
 __device__ __forceinline__ int request_len(const DecodeArgs& a, int b) {
-    int len;
-    if (a.len_mode == kParamsSeq) len = a.lens[kParamSeq];
-    else len = a.lens[b] + (a.len_mode == kPositionsPlusOne ? 1 : 0);
+    const int len = a.lens[b * a.lens_stride + a.lens_off];
     return len < a.max_seq ? len : a.max_seq;  // never index past the table
 }
 
@@ -80,37 +93,147 @@ __device__ __forceinline__ void store_out4(const DecodeArgs& a, int64_t off, flo
     }
 }
 
-template <int PAGES, bool QF32>
-__global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
-    __shared__ float4_t s_acc[kWaves][16][17];  // [wave][col][dim/4], padded
-    __shared__ float s_m[kWaves][16];
-    __shared__ float s_l[kWaves][16];
+// Partials cross workgroups on different XCDs, each with its own L2. They are written and
+// read as agent-scope atomics (write-through stores and L2-coherent loads), so no L2
+// writeback or invalidate is needed around the counter that orders them.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float load_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merge the partials of splits [0, n_active) for query head hh, dims 4*d4 .. 4*d4+3.
+// Loads are issued eight splits at a time so the merge costs n_active / 8 round trips.
+__device__ __forceinline__ void combine_partials(const DecodeArgs& a, int b, int hh, int d4,
+                                                 int n_active) {
+    const int64_t slot0 = ((int64_t)b * a.n_head + hh) * a.n_splits;
+    float M = -INFINITY;
+    float L = 0.0f;
+    float4_t o = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < n_active; s0 += 8) {
+        float mv[8], lv[8];
+        float4_t ov[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (s0 + j < n_active) {
+                const int64_t slot = slot0 + s0 + j;
+                mv[j] = load_coherent(a.pm + slot);
+                lv[j] = load_coherent(a.pl + slot);
+                const float* po = a.po + slot * kHeadDim + 4 * d4;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ov[j][r] = load_coherent(po + r);
+            } else {
+                mv[j] = -INFINITY;
+                lv[j] = 0.0f;
+                ov[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        float mx = M;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, mv[j]);
+        const float sc = fast_exp2(M - mx);  // M = -inf on the first pass: sc = 0, L = o = 0
+        L *= sc;
+        o = o * sc;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (lv[j] > 0.0f) {
+                const float w = fast_exp2(mv[j] - mx);
+                L += lv[j] * w;
+                o += ov[j] * w;
+            }
+        }
+        M = mx;
+    }
+    store_out4(a, (int64_t)b * a.q_row_stride + (int64_t)hh * kHeadDim + 4 * d4, o * (1.0f / L));
+}
+
+// New K/V values of the appended row for this lane's operand slots, rounded to fp16
+// (RNE, the conversion the standalone append kernel uses). K: lanes of column `slot`
+// take channels 8*grp..+7 and 32+8*grp..+7 of kv head g; V: lanes of group slot >> 2
+// take channels 16*db + col.
+struct NewRow {
+    half8_t k0, k1;
+    half_t v[4];
+};
+
+__device__ __forceinline__ half_t to_half(const void* src, bool f16, int64_t i) {
+    return f16 ? static_cast<const half_t*>(src)[i] : (half_t) static_cast<const float*>(src)[i];
+}
+
+__device__ __forceinline__ NewRow load_new_row(const DecodeArgs& a, int b, int g, int col,
+                                               int grp, int slot) {
+    NewRow r{};
+    const int64_t row = (int64_t)b * a.addr.kv_dim + g * kHeadDim;
+    const bool f16 = a.kv_new_f16;
+    if (col == slot) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            r.k0[j] = to_half(a.k_new, f16, row + 8 * grp + j);
+            r.k1[j] = to_half(a.k_new, f16, row + 32 + 8 * grp + j);
+        }
+    }
+    if (grp == (slot >> 2)) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) r.v[db] = to_half(a.v_new, f16, row + 16 * db + col);
+    }
+    return r;
+}
+
+// Store the appended row's kv-head-g slice into its page: the bytes
+// cache_store_rows_paged writes for that slice.
+__device__ __forceinline__ void store_new_row(const DecodeArgs& a, const NewRow& r, int64_t base,
+                                              int g, int col, int grp, int slot) {
+    if (col == slot) {
+        half_t* kp = a.k_pool + base + (int64_t)slot * a.addr.kv_dim + g * kHeadDim + 8 * grp;
+        *reinterpret_cast<half8_t*>(kp) = r.k0;
+        *reinterpret_cast<half8_t*>(kp + 32) = r.k1;
+    }
+    if (grp == (slot >> 2)) {
+        half_t* vp = a.v_pool + base + (int64_t)(g * kHeadDim + col) * kPageTokens + slot;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) vp[db * 16 * kPageTokens] = r.v[db];
+    }
+}
+
+template <int PAGES, int WAVES, bool QF32, bool APPEND>
+__global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
+    __shared__ float4_t s_acc[WAVES][16][17];  // [wave][col][dim/4], padded
+    __shared__ float s_m[WAVES][16];
+    __shared__ float s_l[WAVES][16];
+    __shared__ int s_last;
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int col = lane & 15;
     const int grp = lane >> 4;
 
-    const int unit = blockIdx.x;
-    const int s = unit % a.n_splits;
-    const int bg = unit / a.n_splits;
-    const int g = bg % a.n_kv_head;
-    const int b = bg / a.n_kv_head;
+    // grid = (split, kv head, request): no integer division on the way to the loads
+    const int s = blockIdx.x;
+    const int g = blockIdx.y;
+    const int b = blockIdx.z;
+    const int bg = b * a.n_kv_head + g;
 
+    // Length, append position and page ids in one round trip.
+    const int32_t* table = a.tables ? a.tables + (int64_t)b * a.table_stride : nullptr;
+    const int wp0 = s * a.split_pages + wave * PAGES;
+    int64_t page[PAGES];
+#pragma unroll
+    for (int i = 0; i < PAGES; ++i) {
+        const int p = wp0 + i;
+        page[i] = (table && p < a.max_pages) ? (int64_t)table[p] : (int64_t)p;
+    }
     const int len = request_len(a, b);
-    if (len <= 0) return;
-    const int n_pages = (len + kPageMask) >> kPageShift;
-    const int p_begin = s * a.split_pages;
-    if (p_begin >= n_pages) return;
-    const int n_active = (n_pages + a.split_pages - 1) / a.split_pages;
-    const int wp0 = p_begin + wave * PAGES;
-    const int wp_end = min(wp0 + PAGES, n_pages);
+    int apos = -1;  // position of the row this workgroup appends, or -1
+    if constexpr (APPEND) {
+        const int pos = a.positions[b];
+        if (pos >= 0 && pos < a.max_pages * kPageTokens && (pos >> kPageShift) / a.split_pages == s)
+            apos = pos;
+    }
 
-    const int32_t* table = nullptr;
-    if (a.tables)
-        table = a.tables + (int64_t)(a.table_index ? a.table_index[b] : b) * a.table_stride;
-
-    // Query operand: B[k = channel][col = head], 8 channels per lane per MFMA.
+    // Query operand: B[k = channel][col = head], 8 channels per lane per MFMA. Loaded
+    // before the length is known (the address does not depend on it).
     const int h = g * a.n_rep + col;
     half8_t qh0 = {}, qh1 = {}, ql0 = {}, ql1 = {};
     if (col < a.n_rep) {
@@ -132,16 +255,35 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
         }
     }
 
+    const int n_pages = len > 0 ? (len + kPageMask) >> kPageShift : 0;
+    const int p_begin = s * a.split_pages;
+    const bool attend = p_begin < n_pages;
+    if (!attend && apos < 0) return;
+    // index of the appended row's page among this wave's pages (wave-uniform), or -1
+    const int aidx = (apos >= 0 && (apos >> kPageShift) >= wp0 && (apos >> kPageShift) < wp0 + PAGES)
+                         ? (apos >> kPageShift) - wp0 : -1;
+    const int aslot = apos & kPageMask;
+    if (!attend) {
+        // append only: the row lies past the attended length
+        if (aidx >= 0) {
+            const NewRow nr = load_new_row(a, b, g, col, grp, aslot);
+#pragma unroll
+            for (int i = 0; i < PAGES; ++i)
+                if (i == aidx) store_new_row(a, nr, block_base(a.addr, page[i]), g, col, grp, aslot);
+        }
+        return;
+    }
+    const int n_active = (n_pages + a.split_pages - 1) / a.split_pages;
+    const int wp_end = min(wp0 + PAGES, n_pages);
+
     // Issue every load of this wave's pages before any arithmetic.
     half8_t ka[PAGES][2];
     half4_t va[PAGES][4];
     const int kv_dim = a.addr.kv_dim;
 #pragma unroll
     for (int i = 0; i < PAGES; ++i) {
-        const int p = wp0 + i;
-        if (p < wp_end) {
-            const int64_t page = table ? (int64_t)table[p] : (int64_t)p;
-            const int64_t base = block_base(a.addr, page);
+        if (wp0 + i < wp_end) {
+            const int64_t base = block_base(a.addr, page[i]);
             const half_t* kp = a.k_pool + base + (int64_t)col * kv_dim + g * kHeadDim + 8 * grp;
             ka[i][0] = *reinterpret_cast<const half8_t*>(kp);
             ka[i][1] = *reinterpret_cast<const half8_t*>(kp + 32);
@@ -149,6 +291,27 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
             for (int db = 0; db < 4; ++db)
                 va[i][db] = *reinterpret_cast<const half4_t*>(vp + db * 16 * kPageTokens);
+        }
+    }
+    if (APPEND && aidx >= 0) {
+        // The appended row replaces what the page held in this wave's operands and is
+        // written to the page for later steps.
+        const NewRow nr = load_new_row(a, b, g, col, grp, aslot);
+#pragma unroll
+        for (int i = 0; i < PAGES; ++i) {
+            if (i == aidx) {
+                if (wp0 + i < wp_end) {
+                    if (col == aslot) {
+                        ka[i][0] = nr.k0;
+                        ka[i][1] = nr.k1;
+                    }
+                    if (grp == (aslot >> 2)) {
+#pragma unroll
+                        for (int db = 0; db < 4; ++db) va[i][db][aslot & 3] = nr.v[db];
+                    }
+                }
+                store_new_row(a, nr, block_base(a.addr, page[i]), g, col, grp, aslot);
+            }
         }
     }
 
@@ -209,7 +372,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
 
-    // Merge the 4 waves' states: acc[db][r] = O^T[16*db + 4*grp + r][col].
+    // Merge the waves' states: acc[db][r] = O^T[16*db + 4*grp + r][col].
     if (grp == 0) {
         s_m[wave][col] = m;
         s_l[wave][col] = l;
@@ -221,34 +384,56 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
     const int t = threadIdx.x;
     const int ccol = t >> 4;  // query head within the group
     const int d4 = t & 15;    // dims 4*d4 .. 4*d4+3
-    if (ccol >= a.n_rep) return;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][ccol]);
-    float L = 0.0f;
-    float4_t o = {};
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-        if (s_l[w][ccol] > 0.0f) {
-            const float wgt = fast_exp2(s_m[w][ccol] - M);
-            L += s_l[w][ccol] * wgt;
-            o += s_acc[w][ccol][d4] * wgt;
-        }
-    }
+    const bool owner = ccol < a.n_rep;
     const int hh = g * a.n_rep + ccol;
-    if (n_active == 1) {
-        store_out4(a, (int64_t)b * a.q_row_stride + (int64_t)hh * kHeadDim + 4 * d4, o * (1.0f / L));
-    } else {
-        const int64_t slot = ((int64_t)b * a.n_head + hh) * a.n_splits + s;
-        *reinterpret_cast<float4_t*>(a.po + slot * kHeadDim + 4 * d4) = o;
-        if (d4 == 0) {
-            a.pm[slot] = M;
-            a.pl[slot] = L;
+    if (owner) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) M = fmaxf(M, s_m[w][ccol]);
+        float L = 0.0f;
+        float4_t o = {};
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            if (s_l[w][ccol] > 0.0f) {
+                const float wgt = fast_exp2(s_m[w][ccol] - M);
+                L += s_l[w][ccol] * wgt;
+                o += s_acc[w][ccol][d4] * wgt;
+            }
+        }
+        if (n_active == 1) {
+            store_out4(a, (int64_t)b * a.q_row_stride + (int64_t)hh * kHeadDim + 4 * d4, o * (1.0f / L));
+        } else {
+            const int64_t slot = ((int64_t)b * a.n_head + hh) * a.n_splits + s;
+            float* po = a.po + slot * kHeadDim + 4 * d4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) store_coherent(po + r, o[r]);
+            if (d4 == 0) {
+                store_coherent(a.pm + slot, M);
+                store_coherent(a.pl + slot, L);
+            }
+            // The partial is published once these stores are acknowledged: wait for them
+            // before the workgroup barrier that precedes the counter increment.
+            __builtin_amdgcn_s_waitcnt(0);
         }
     }
+    if (n_active == 1 || a.counters == nullptr) return;  // uniform across the workgroup
+
+    __syncthreads();
+    if (t == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(&a.counters[bg], 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        const int last = prev == (uint32_t)(n_active - 1);
+        if (last)  // ready for the next launch
+            __hip_atomic_store(&a.counters[bg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (owner) combine_partials(a, b, hh, d4, n_active);
 }
 
-// One workgroup per (request, kv head): merges the split partials of the n_rep heads.
+// Second-pass combine for callers that own the partials without a counter
+// (attention_split): one workgroup per (request, kv head).
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
     const int b = blockIdx.x / a.n_kv_head;
     const int g = blockIdx.x % a.n_kv_head;
@@ -257,58 +442,68 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
     const int n_pages = (len + kPageMask) >> kPageShift;
     const int n_active = (n_pages + a.split_pages - 1) / a.split_pages;
     if (n_active <= 1) return;
-    const int t = threadIdx.x;
-    const int ccol = t >> 4;
-    const int d4 = t & 15;
+    const int ccol = threadIdx.x >> 4;
     if (ccol >= a.n_rep) return;
-    const int hh = g * a.n_rep + ccol;
-    const int64_t slot0 = ((int64_t)b * a.n_head + hh) * a.n_splits;
-    float M = -INFINITY;
-    for (int s = 0; s < n_active; ++s) M = fmaxf(M, a.pm[slot0 + s]);
-    float L = 0.0f;
-    float4_t o = {};
-    for (int s = 0; s < n_active; ++s) {
-        const float wgt = fast_exp2(a.pm[slot0 + s] - M);
-        L += a.pl[slot0 + s] * wgt;
-        o += *reinterpret_cast<const float4_t*>(a.po + (slot0 + s) * kHeadDim + 4 * d4) * wgt;
-    }
-    store_out4(a, (int64_t)b * a.q_row_stride + (int64_t)hh * kHeadDim + 4 * d4, o * (1.0f / L));
+    combine_partials(a, b, g * a.n_rep + ccol, threadIdx.x & 15, n_active);
 }
 
-// Pages per wave. A split (one workgroup) covers 4x this many pages. Larger splits
-// mean fewer partials to merge; smaller ones mean more waves in flight.
-int pages_per_wave(int64_t batch, int64_t n_kv_head, int64_t max_pages) {
+struct DecodeShape {
+    int pages;  // pages per wave
+    int waves;  // waves per workgroup
+};
+
+// Pages per wave and waves per workgroup. A split covers pages * waves pages: larger
+// splits mean fewer partials to merge, smaller ones more workgroups in flight.
+DecodeShape decode_shape(int64_t batch, int64_t n_kv_head, int64_t max_pages) {
+    // page-units = (request, kv head, page) triples the grid is sized for
+    const int64_t units = batch * n_kv_head * max_pages;
+    DecodeShape sh{1, 4};                 // 4-page splits: few requests, short contexts
+    if (units > 2048) sh = {1, 8};        // 8-page splits (e.g. b16 x 3 kv heads x 2048)
+    if (units > 8192) sh = {2, 8};        // 16-page splits (e.g. b16 x 12 kv heads x 2048)
     if (const char* env = std::getenv("CRUCIBLE_DECODE_PAGES")) {
         const int v = std::atoi(env);
-        if (v == 1 || v == 2 || v == 4) return v;
+        if (v == 1 || v == 2 || v == 4) sh.pages = v;
     }
-    const int64_t work = batch * n_kv_head * max_pages;
-    if (work >= 16384) return 4;
-    if (work >= 4096) return 2;
-    return 1;
+    if (const char* env = std::getenv("CRUCIBLE_DECODE_WAVES")) {
+        const int v = std::atoi(env);
+        if (v == 4 || v == 8) sh.waves = v;
+    }
+    return sh;
 }
 
-int launch_decode(DecodeArgs a, int pages, bool q_f32, hipStream_t stream, const char* what) {
-    const int64_t units = (int64_t)a.batch * a.n_kv_head * a.n_splits;
-    CRUCIBLE_CHECK(units > 0 && units <= INT32_MAX, CRUCIBLE_ERR_INVALID, "%s: grid too large",
-                   what);
-    const dim3 grid((unsigned)units), block(256);
-#define CRUCIBLE_DECODE_CASE(P)                                                              \
-    case P:                                                                                   \
-        if (q_f32) hipLaunchKernelGGL((decode_split_kernel<P, true>), grid, block, 0, stream, a); \
-        else hipLaunchKernelGGL((decode_split_kernel<P, false>), grid, block, 0, stream, a);  \
-        break;
-    switch (pages) {
-        CRUCIBLE_DECODE_CASE(1)
-        CRUCIBLE_DECODE_CASE(2)
-        CRUCIBLE_DECODE_CASE(4)
-        default:
-            set_error(CRUCIBLE_ERR_INVALID, "%s: bad pages per wave %d", what, pages);
-            return CRUCIBLE_ERR_INVALID;
+template <bool QF32, bool APPEND>
+bool launch_shape(const DecodeArgs& a, DecodeShape sh, dim3 grid, hipStream_t stream) {
+#define CRUCIBLE_DECODE_CASE(P, W)                                                           \
+    if (sh.pages == P && sh.waves == W) {                                                     \
+        hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND>), grid, dim3(W * 64), 0, stream, a); \
+        return true;                                                                          \
     }
+    CRUCIBLE_DECODE_CASE(1, 4)
+    CRUCIBLE_DECODE_CASE(2, 4)
+    CRUCIBLE_DECODE_CASE(4, 4)
+    CRUCIBLE_DECODE_CASE(1, 8)
+    CRUCIBLE_DECODE_CASE(2, 8)
+    CRUCIBLE_DECODE_CASE(4, 8)
 #undef CRUCIBLE_DECODE_CASE
+    return false;
+}
+
+int launch_decode(DecodeArgs a, DecodeShape sh, bool q_f32, hipStream_t stream,
+                  const char* what) {
+    CRUCIBLE_CHECK(a.n_splits > 0 && a.n_kv_head <= 65535 && a.batch <= 65535,
+                   CRUCIBLE_ERR_INVALID, "%s: grid (%d, %d, %d) too large", what, a.n_splits,
+                   a.n_kv_head, a.batch);
+    const dim3 grid((unsigned)a.n_splits, (unsigned)a.n_kv_head, (unsigned)a.batch);
+    const bool append = a.positions != nullptr;
+    bool launched;
+    if (append) launched = q_f32 ? launch_shape<true, true>(a, sh, grid, stream)
+                                 : launch_shape<false, true>(a, sh, grid, stream);
+    else launched = q_f32 ? launch_shape<true, false>(a, sh, grid, stream)
+                          : launch_shape<false, false>(a, sh, grid, stream);
+    CRUCIBLE_CHECK(launched, CRUCIBLE_ERR_INVALID, "%s: bad decode shape %d x %d", what,
+                   sh.pages, sh.waves);
     if (int rc = fail_launch(what)) return rc;
-    if (a.n_splits > 1) {
+    if (a.n_splits > 1 && a.counters == nullptr) {
         hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(a.batch * a.n_kv_head)),
                            dim3(256), 0, stream, a);
         if (int rc = fail_launch(what)) return rc;
@@ -332,8 +527,15 @@ int check_geometry(const char* what, int64_t n_head, int64_t n_kv_head, int64_t 
     return CRUCIBLE_OK;
 }
 
-size_t workspace_floats(int64_t batch, int64_t n_head, int64_t n_splits) {
+// Workspace: partial o, m, l for every (request, query head, split), then one counter
+// per (request, kv head). Sized for the smallest split (1 page x 4 waves).
+size_t partial_floats(int64_t batch, int64_t n_head, int64_t n_splits) {
     return (size_t)batch * n_head * n_splits * (kHeadDim + 2);
+}
+
+size_t workspace_need(int64_t batch, int64_t n_head, int64_t n_splits) {
+    return partial_floats(batch, n_head, n_splits) * sizeof(float) +
+           (size_t)batch * n_head * sizeof(uint32_t);
 }
 
 void bind_workspace(DecodeArgs& a, void* ws) {
@@ -342,6 +544,44 @@ void bind_workspace(DecodeArgs& a, void* ws) {
     a.po = f;
     a.pm = f + n * kHeadDim;
     a.pl = a.pm + n;
+    a.counters = reinterpret_cast<uint32_t*>(f + partial_floats(a.batch, a.n_head, a.n_splits));
+}
+
+DecodeArgs common_args(const void* q, const void* k, const void* v, void* out, int out_dtype,
+                       int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t max_seq) {
+    DecodeArgs a{};
+    a.q = q;
+    a.k_pool = static_cast<half_t*>(const_cast<void*>(k));  // written only by the fused append
+    a.v_pool = static_cast<half_t*>(const_cast<void*>(v));
+    a.out = out;
+    a.q_row_stride = n_head * kHeadDim;
+    a.batch = (int)batch;
+    a.n_head = (int)n_head;
+    a.n_kv_head = (int)n_kv_head;
+    a.n_rep = (int)(n_head / n_kv_head);
+    a.max_seq = (int)max_seq;
+    a.max_pages = (int)((max_seq + kPageMask) >> kPageShift);
+    a.out_f16 = out_dtype == CRUCIBLE_F16;
+    a.scale_log2 = 0.125f * kLog2e;
+    return a;
+}
+
+// Split the request into workgroups, bind the workspace and launch.
+int decode_with_workspace(DecodeArgs& a, bool q_f32, void* workspace, size_t workspace_bytes,
+                          hipStream_t stream, const char* what) {
+    const DecodeShape sh = decode_shape(a.batch, a.n_kv_head, a.max_pages);
+    a.split_pages = sh.pages * sh.waves;
+    a.n_splits = (a.max_pages + a.split_pages - 1) / a.split_pages;
+    if (a.n_splits > 1) {
+        const size_t need = workspace_need(a.batch, a.n_head, a.n_splits);
+        CRUCIBLE_CHECK(workspace && workspace_bytes >= need, CRUCIBLE_ERR_WORKSPACE,
+                       "%s: workspace needs %zu bytes, got %zu", what, need,
+                       workspace ? workspace_bytes : (size_t)0);
+        CRUCIBLE_CHECK(((uintptr_t)workspace & 15) == 0, CRUCIBLE_ERR_WORKSPACE,
+                       "%s: workspace must be 16-byte aligned", what);
+        bind_workspace(a, workspace);
+    }
+    return launch_decode(a, sh, q_f32, stream, what);
 }
 
 }  // namespace
@@ -353,8 +593,8 @@ extern "C" size_t crucible_attention_decode_workspace_bytes(int64_t batch, int64
                                                             int64_t max_seq) {
     if (batch <= 0 || n_head <= 0 || max_seq <= 0) return 0;
     const int64_t max_pages = (max_seq + kPageMask) >> kPageShift;
-    const int64_t n_splits = (max_pages + kWaves - 1) / kWaves;  // worst case: 1 page per wave
-    return workspace_floats(batch, n_head, n_splits) * sizeof(float);
+    const int64_t n_splits = (max_pages + 3) / 4;  // the smallest split: 1 page x 4 waves
+    return workspace_need(batch, n_head, n_splits);
 }
 
 extern "C" int crucible_attention_decode_paged(
@@ -379,36 +619,57 @@ extern "C" int crucible_attention_decode_paged(
                        max_seq <= INT32_MAX,
                    CRUCIBLE_ERR_INVALID, "%s: max_seq %lld must be in 1..table_stride*16", what,
                    (long long)max_seq);
-    DecodeArgs a{};
-    a.q = q;
-    a.k_pool = static_cast<const half_t*>(k_pool);
-    a.v_pool = static_cast<const half_t*>(v_pool);
-    a.out = out;
+    DecodeArgs a = common_args(q, k_pool, v_pool, out, out_dtype, batch, n_head, n_kv_head,
+                               max_seq);
     a.tables = page_tables;
     a.lens = seq_lens;
-    a.len_mode = kLensArray;
+    a.lens_stride = 1;
     a.addr.kv_dim = (int32_t)kv_dim;
     a.addr.page_stride = n_layer * kPageTokens * kv_dim;
     a.addr.layer_off = layer * kPageTokens * kv_dim;
     a.table_stride = table_stride;
-    a.q_row_stride = n_head * kHeadDim;
-    a.batch = (int)batch;
-    a.n_head = (int)n_head;
-    a.n_kv_head = (int)n_kv_head;
-    a.n_rep = (int)(n_head / n_kv_head);
-    a.max_seq = (int)max_seq;
-    a.out_f16 = out_dtype == CRUCIBLE_F16;
-    a.scale_log2 = 0.125f * kLog2e;
-    const int64_t max_pages = (max_seq + kPageMask) >> kPageShift;
-    const int pages = pages_per_wave(batch, n_kv_head, max_pages);
-    a.split_pages = pages * kWaves;
-    a.n_splits = (int)((max_pages + a.split_pages - 1) / a.split_pages);
-    const size_t need = workspace_floats(batch, n_head, a.n_splits) * sizeof(float);
-    CRUCIBLE_CHECK(a.n_splits == 1 || (workspace && workspace_bytes >= need),
-                   CRUCIBLE_ERR_WORKSPACE, "%s: workspace needs %zu bytes, got %zu", what, need,
-                   workspace ? workspace_bytes : (size_t)0);
-    if (a.n_splits > 1) bind_workspace(a, workspace);
-    return launch_decode(a, pages, q_dtype == CRUCIBLE_F32, stream, what);
+    return decode_with_workspace(a, q_dtype == CRUCIBLE_F32, workspace, workspace_bytes, stream,
+                                 what);
+}
+
+extern "C" int crucible_attention_decode_paged_append(
+    const void* q, int q_dtype, const void* k_new, const void* v_new, int kv_dtype, void* k_pool,
+    void* v_pool, void* out, int out_dtype, const int32_t* page_tables, const int32_t* positions,
+    const int32_t* seq_lens, int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
+    int64_t table_stride, int64_t n_layer, int64_t layer, int64_t kv_dim, int64_t max_seq,
+    void* workspace, size_t workspace_bytes, crucible_stream_t stream) {
+    const char* what = "attention_decode_paged_append";
+    CRUCIBLE_CHECK(dtype_ok(q_dtype) && dtype_ok(out_dtype) && dtype_ok(kv_dtype),
+                   CRUCIBLE_ERR_INVALID, "%s: bad dtype", what);
+    if (int rc = check_geometry(what, n_head, n_kv_head, head_dim, kv_dim)) return rc;
+    CRUCIBLE_CHECK(batch >= 0 && batch <= INT32_MAX, CRUCIBLE_ERR_INVALID, "%s: batch %lld",
+                   what, (long long)batch);
+    if (batch == 0) return CRUCIBLE_OK;
+    CRUCIBLE_CHECK(q && k_new && v_new && k_pool && v_pool && out && page_tables && positions &&
+                       seq_lens,
+                   CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
+    CRUCIBLE_CHECK(n_layer > 0 && layer >= 0 && layer < n_layer, CRUCIBLE_ERR_INVALID,
+                   "%s: layer %lld outside n_layer %lld", what, (long long)layer,
+                   (long long)n_layer);
+    CRUCIBLE_CHECK(table_stride > 0 && max_seq > 0 && max_seq <= table_stride * kPageTokens &&
+                       max_seq <= INT32_MAX,
+                   CRUCIBLE_ERR_INVALID, "%s: max_seq %lld must be in 1..table_stride*16", what,
+                   (long long)max_seq);
+    DecodeArgs a = common_args(q, k_pool, v_pool, out, out_dtype, batch, n_head, n_kv_head,
+                               max_seq);
+    a.tables = page_tables;
+    a.lens = seq_lens;
+    a.lens_stride = 1;
+    a.positions = positions;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.kv_new_f16 = kv_dtype == CRUCIBLE_F16;
+    a.addr.kv_dim = (int32_t)kv_dim;
+    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
+    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    a.table_stride = table_stride;
+    return decode_with_workspace(a, q_dtype == CRUCIBLE_F32, workspace, workspace_bytes, stream,
+                                 what);
 }
 
 extern "C" int crucible_attention_decode(const void* q, int q_dtype, const void* k_cache,
@@ -426,34 +687,15 @@ extern "C" int crucible_attention_decode(const void* q, int q_dtype, const void*
                    "%s: null buffer", what);
     CRUCIBLE_CHECK(max_seq > 0 && max_seq <= INT32_MAX && layer_base >= 0, CRUCIBLE_ERR_INVALID,
                    "%s: max_seq %lld", what, (long long)max_seq);
-    DecodeArgs a{};
-    a.q = q;
-    a.k_pool = static_cast<const half_t*>(k_cache);
-    a.v_pool = static_cast<const half_t*>(v_cache);
-    a.out = out;
+    DecodeArgs a = common_args(q, k_cache, v_cache, out, out_dtype, 1, n_head, n_kv_head,
+                               max_seq);
     a.lens = params;
-    a.len_mode = kParamsSeq;
+    a.lens_off = kParamSeq;
     a.addr.kv_dim = (int32_t)cache_stride;
     a.addr.page_stride = kPageTokens * cache_stride;
     a.addr.layer_off = layer_base;
-    a.q_row_stride = n_head * kHeadDim;
-    a.batch = 1;
-    a.n_head = (int)n_head;
-    a.n_kv_head = (int)n_kv_head;
-    a.n_rep = (int)(n_head / n_kv_head);
-    a.max_seq = (int)max_seq;
-    a.out_f16 = out_dtype == CRUCIBLE_F16;
-    a.scale_log2 = 0.125f * kLog2e;
-    const int64_t max_pages = (max_seq + kPageMask) >> kPageShift;
-    const int pages = pages_per_wave(1, n_kv_head, max_pages);
-    a.split_pages = pages * kWaves;
-    a.n_splits = (int)((max_pages + a.split_pages - 1) / a.split_pages);
-    const size_t need = workspace_floats(1, n_head, a.n_splits) * sizeof(float);
-    CRUCIBLE_CHECK(a.n_splits == 1 || (workspace && workspace_bytes >= need),
-                   CRUCIBLE_ERR_WORKSPACE, "%s: workspace needs %zu bytes, got %zu", what, need,
-                   workspace ? workspace_bytes : (size_t)0);
-    if (a.n_splits > 1) bind_workspace(a, workspace);
-    return launch_decode(a, pages, q_dtype == CRUCIBLE_F32, stream, what);
+    return decode_with_workspace(a, q_dtype == CRUCIBLE_F32, workspace, workspace_bytes, stream,
+                                 what);
 }
 
 extern "C" int crucible_attention_split(const void* q, int q_dtype, const void* k_cache,
@@ -472,29 +714,21 @@ extern "C" int crucible_attention_split(const void* q, int q_dtype, const void* 
                    CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
     CRUCIBLE_CHECK(capacity > 0 && capacity <= INT32_MAX && layer_base >= 0,
                    CRUCIBLE_ERR_INVALID, "%s: capacity %lld", what, (long long)capacity);
-    DecodeArgs a{};
-    a.q = q;
-    a.k_pool = static_cast<const half_t*>(k_cache);
-    a.v_pool = static_cast<const half_t*>(v_cache);
-    a.out = out;
+    DecodeArgs a = common_args(q, k_cache, v_cache, out, out_dtype, 1, n_head, n_kv_head,
+                               capacity);
     a.lens = params;
-    a.len_mode = kParamsSeq;
+    a.lens_off = kParamSeq;
     a.addr.kv_dim = (int32_t)cache_stride;
     a.addr.page_stride = kPageTokens * cache_stride;
     a.addr.layer_off = layer_base;
-    a.q_row_stride = n_head * kHeadDim;
-    a.batch = 1;
-    a.n_head = (int)n_head;
-    a.n_kv_head = (int)n_kv_head;
-    a.n_rep = (int)(n_head / n_kv_head);
-    a.max_seq = (int)capacity;
-    a.out_f16 = out_dtype == CRUCIBLE_F16;
-    a.scale_log2 = 0.125f * kLog2e;
-    // 128-position chunks as in the reference (gpu.rs:37 ATTN_CHUNK): 4 waves x 2 pages.
+    // 128-position chunks as in the reference (gpu.rs:37 ATTN_CHUNK): 4 waves x 2 pages,
+    // partials in the caller's buffers, combined by a second kernel.
+    const DecodeShape sh{2, 4};
     a.split_pages = 8;
     a.n_splits = (int)((capacity + 127) / 128);
     a.po = partial_o;
     a.pm = partial_m;
     a.pl = partial_l;
-    return launch_decode(a, 2, q_dtype == CRUCIBLE_F32, stream, what);
+    a.counters = nullptr;
+    return launch_decode(a, sh, q_dtype == CRUCIBLE_F32, stream, what);
 }

@@ -76,7 +76,7 @@ class Gpu:
         ws = self._workspaces.get(key)
         if ws is None:
             nbytes = self.lib.crucible_attention_decode_workspace_bytes(batch, n_head, max_seq)
-            ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=self.device)
+            ws = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=self.device)
             self._workspaces[key] = ws
         return ws
 
@@ -143,6 +143,29 @@ class Gpu:
         _lib.check(self.lib.crucible_attention_decode_paged(
             _ptr(q), _dtype(q, "q"), _ptr(k_pool), _ptr(v_pool), _ptr(out), _dtype(out, "out"),
             _ptr(page_tables), _ptr(seq_lens), batch, n_head, n_kv_head, head_dim, table_stride,
+            n_layer, layer, kv_dim, max_seq, _ptr(ws), ws.numel() * ws.element_size(),
+            self._stream()))
+
+    def attention_decode_paged_append(self, q, k_new, v_new, k_pool, v_pool, out, page_tables,
+                                      positions, seq_lens, batch, n_head, n_kv_head, head_dim,
+                                      table_stride, n_layer, layer, kv_dim, max_seq,
+                                      workspace=None):
+        """Fused gpu_model.rs:1434-1507 sequence: append K and V rows at positions[b], then
+        decode with seq_lens, in one launch (same pool bytes and output as the three calls)."""
+        _need(q, "q", numel=batch * n_head * head_dim)
+        _need(out, "out", numel=batch * n_head * head_dim)
+        _need(k_new, "k_new", numel=batch * kv_dim)
+        _need(v_new, "v_new", dtype=k_new.dtype, numel=batch * kv_dim)
+        _need(k_pool, "k_pool", dtype=torch.float16)
+        _need(v_pool, "v_pool", dtype=torch.float16)
+        _need(page_tables, "page_tables", dtype=torch.int32, numel=batch * table_stride)
+        _need(positions, "positions", dtype=torch.int32, numel=batch)
+        _need(seq_lens, "seq_lens", dtype=torch.int32, numel=batch)
+        ws = workspace if workspace is not None else self.workspace(batch, n_head, max_seq)
+        _lib.check(self.lib.crucible_attention_decode_paged_append(
+            _ptr(q), _dtype(q, "q"), _ptr(k_new), _ptr(v_new), _dtype(k_new, "k_new"),
+            _ptr(k_pool), _ptr(v_pool), _ptr(out), _dtype(out, "out"), _ptr(page_tables),
+            _ptr(positions), _ptr(seq_lens), batch, n_head, n_kv_head, head_dim, table_stride,
             n_layer, layer, kv_dim, max_seq, _ptr(ws), ws.numel() * ws.element_size(),
             self._stream()))
 

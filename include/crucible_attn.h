@@ -107,7 +107,11 @@ int crucible_cache_store_packed_paged(const void* src, int src_dtype, void* pool
  * (out_dtype). head_dim must be 64 and n_head a multiple of n_kv_head with
  * n_head / n_kv_head <= 16. Query head h reads KV head h / (n_head / n_kv_head).
  * The split-K partials live in a caller-provided workspace of at least
- * crucible_attention_decode_workspace_bytes(...) bytes (no allocation here).
+ * crucible_attention_decode_workspace_bytes(...) bytes (no allocation here),
+ * 16-byte aligned. The workspace also holds one counter per (request, kv head)
+ * that orders the in-kernel combine of the splits: zero it once when it is
+ * allocated; every launch leaves it zeroed again. A workspace serves one launch
+ * at a time (launches that share one must be ordered, e.g. on one stream).
  */
 
 size_t crucible_attention_decode_workspace_bytes(int64_t batch, int64_t n_head,
@@ -123,6 +127,23 @@ int crucible_attention_decode_paged(const void* q, int q_dtype, const void* k_po
                                     int64_t layer, int64_t kv_dim, int64_t max_seq,
                                     void* workspace, size_t workspace_bytes,
                                     crucible_stream_t stream);
+
+/* Fused form of the reference's per-layer decode sequence (gpu_model.rs:1434-1507):
+ *   Gpu::cache_store_rows_paged(k_new -> k_pool, positions)   (gpu.rs:1405-1439)
+ *   Gpu::cache_store_rows_paged(v_new -> v_pool, positions)
+ *   Gpu::attention_decode_paged(q, ..., seq_lens)             (gpu.rs:1441-1500)
+ * in one launch. Row b < batch is appended at positions[b] (k_new/v_new are
+ * [batch][kv_dim] in kv_dtype, rounded to fp16); the pools receive exactly the
+ * bytes the two appends write, and `out` is what attention_decode_paged computes
+ * after them (seq_lens[b] <= 0: no output for b, the row is still appended).
+ * Same workspace as attention_decode_paged. */
+int crucible_attention_decode_paged_append(
+    const void* q, int q_dtype, const void* k_new, const void* v_new, int kv_dtype,
+    void* k_pool, void* v_pool, void* out, int out_dtype, const int32_t* page_tables,
+    const int32_t* positions, const int32_t* seq_lens, int64_t batch, int64_t n_head,
+    int64_t n_kv_head, int64_t head_dim, int64_t table_stride, int64_t n_layer, int64_t layer,
+    int64_t kv_dim, int64_t max_seq, void* workspace, size_t workspace_bytes,
+    crucible_stream_t stream);
 
 /* Replaces Gpu::attention_decode (gpu.rs:762-817; kernels.cu:288-389): one
  * sequence in a contiguous cache, visible length params[CRUCIBLE_PARAM_SEQ]. */

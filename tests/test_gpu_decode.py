@@ -229,3 +229,90 @@ def test_config3_decode_b16_all_layers(gpu, dev):
         worst = max(worst, float(np.abs(out.cpu().numpy() - want).max()))
     print(f"config3 all layers: max-abs {worst:.3e}")
     assert worst <= TOL
+
+
+# ---------------------------------------------------------------- fused append + decode
+
+def _fused_vs_separate(gpu, dev, lens, positions, n_head, n_kv, kv_dtype=torch.float32,
+                       n_layer=3, layer=1, seed=0, stride=None, shapes=None):
+    """Run the fused entry and the reference's three calls on copies of the same pools;
+    return (fused pools, separate pools, fused out, separate out) as host arrays."""
+    rng = np.random.default_rng(seed)
+    batch = len(lens)
+    kv = n_kv * 64
+    stride = stride or max(1, -(-max(max(lens), max(positions) + 1, 1) // 16))
+    need = [max(-(-max(n, 1) // 16), (p >> 4) + 1) for n, p in zip(lens, positions)]
+    n_pages = sum(need) + 3
+    kp, vp = random_pools(rng, n_pages, n_layer, kv)
+    tables = disjoint_tables(rng, n_pages, [16 * k for k in need], stride)
+    q = rng.standard_normal((batch, n_head * 64)).astype(np.float16)
+    k_new = (rng.standard_normal((batch, kv)) * 2).astype(np.float32)
+    v_new = (rng.standard_normal((batch, kv)) * 2).astype(np.float32)
+    d_q = _dev(q, dev)
+    d_tab = _dev(tables, dev)
+    d_pos = _dev(np.asarray(positions, np.int32), dev)
+    d_len = _dev(np.asarray(lens, np.int32), dev)
+    d_kn = torch.from_numpy(k_new).to(dev).to(kv_dtype)
+    d_vn = torch.from_numpy(v_new).to(dev).to(kv_dtype)
+    max_seq = stride * 16
+    # separate: append K, append V, decode
+    k1, v1 = _dev(kp, dev), _dev(vp, dev)
+    out1 = torch.full((batch, n_head * 64), SENTINEL, device=dev)
+    gpu.cache_store_rows_paged(d_kn, k1, d_tab, d_pos, batch, kv, stride, n_layer, layer, kind="k")
+    gpu.cache_store_rows_paged(d_vn, v1, d_tab, d_pos, batch, kv, stride, n_layer, layer, kind="v")
+    gpu.attention_decode_paged(d_q, k1, v1, out1, d_tab, d_len, batch, n_head, n_kv, 64, stride,
+                               n_layer, layer, kv, max_seq)
+    # fused
+    k2, v2 = _dev(kp, dev), _dev(vp, dev)
+    out2 = torch.full((batch, n_head * 64), SENTINEL, device=dev)
+    gpu.attention_decode_paged_append(d_q, d_kn, d_vn, k2, v2, out2, d_tab, d_pos, d_len, batch,
+                                      n_head, n_kv, 64, stride, n_layer, layer, kv, max_seq)
+    torch.cuda.synchronize()
+    return (k2.cpu().numpy().view(np.uint16), v2.cpu().numpy().view(np.uint16),
+            k1.cpu().numpy().view(np.uint16), v1.cpu().numpy().view(np.uint16),
+            out2.cpu().numpy(), out1.cpu().numpy(), q, tables)
+
+
+@pytest.mark.parametrize("n_head,n_kv", [(12, 3), (12, 12), (16, 4), (12, 1)])
+@pytest.mark.parametrize("kv_dtype", [torch.float32, torch.float16])
+def test_fused_append_decode_equals_separate_calls(gpu, dev, n_head, n_kv, kv_dtype):
+    lens = [1, 15, 16, 17, 32, 33, 255, 256, 257, 700, 1024, 2048]
+    positions = [n - 1 for n in lens]
+    k2, v2, k1, v1, o2, o1, q, tables = _fused_vs_separate(
+        gpu, dev, lens, positions, n_head, n_kv, kv_dtype, seed=n_head + n_kv)
+    assert np.array_equal(k2, k1) and np.array_equal(v2, v1), "pool bytes differ"
+    assert np.array_equal(o2.view(np.uint32), o1.view(np.uint32)), "outputs differ"
+    # and both match the oracle on the appended pools
+    want = _oracle(q.astype(np.float32), k1, v1, tables, lens, n_head, n_kv, 3, 1)
+    assert np.abs(o2 - want).max() <= TOL
+
+
+def test_fused_append_off_the_last_slot_and_inactive_rows(gpu, dev):
+    """Rows appended inside the attended range, past it (a later page), and for inactive
+    requests (len 0) give the same pools and outputs as the separate calls."""
+    lens = [40, 40, 0, 300, 17, 129]
+    positions = [20, 100, 5, 299, 16, 128]
+    for rep in range(3):  # repeated launches reuse the workspace counters
+        k2, v2, k1, v1, o2, o1, _, _ = _fused_vs_separate(gpu, dev, lens, positions, 12, 3,
+                                                          seed=70 + rep)
+        assert np.array_equal(k2, k1) and np.array_equal(v2, v1)
+        active = [b for b, n in enumerate(lens) if n > 0]
+        assert np.array_equal(o2[active].view(np.uint32), o1[active].view(np.uint32))
+        assert np.all(o2[2] == SENTINEL)
+
+
+def test_decode_shapes_agree(gpu, dev, monkeypatch):
+    """Every split shape (pages per wave x waves per workgroup) gives the oracle's answer,
+    with the fused and plain entries, on lengths that exercise 1..many splits."""
+    lens = [3, 64, 65, 500, 1023, 2048, 1500, 16]
+    positions = [n - 1 for n in lens]
+    for pages in ("1", "2", "4"):
+        for waves in ("4", "8"):
+            monkeypatch.setenv("CRUCIBLE_DECODE_PAGES", pages)
+            monkeypatch.setenv("CRUCIBLE_DECODE_WAVES", waves)
+            k2, v2, k1, v1, o2, o1, q, tables = _fused_vs_separate(
+                gpu, dev, lens, positions, 12, 3, seed=int(pages) * 10 + int(waves))
+            assert np.array_equal(k2, k1) and np.array_equal(v2, v1)
+            assert np.array_equal(o2.view(np.uint32), o1.view(np.uint32)), (pages, waves)
+            want = _oracle(q.astype(np.float32), k1, v1, tables, lens, 12, 3, 3, 1)
+            assert np.abs(o2 - want).max() <= TOL, (pages, waves)

@@ -196,6 +196,21 @@ class DecodeBench:
         return wall * 1e3 / steps, e0.elapsed_time(e1) / steps, nbytes / steps
 
 
+def pmc_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
+    (profiles/decode_b16_gqa3_pmc_traffic.txt: FETCH_SIZE and WRITE_SIZE runs scaled by a
+    copy kernel of known size), or None when the summary is for another kernel."""
+    path = os.path.join(ROOT, "profiles", "decode_b16_gqa3_pmc_traffic.txt")
+    try:
+        fields = dict(line.split(": ", 1) for line in open(path).read().splitlines()
+                      if ": " in line and not line.startswith(" "))
+    except OSError:
+        return None
+    if fields.get("kernel", "").strip() != kernel:
+        return None
+    return int(fields["traffic_bytes_per_launch"])
+
+
 def flush_llc(dev):
     """Touch 512 MiB so the 256 MB last-level cache holds nothing of the workload."""
     import torch
@@ -316,10 +331,12 @@ def main():
     bytes_per_launch = step_bytes / b16.n_layer
     achieved = bytes_per_launch / (launch_us * 1e-6) / 1e9
     log(f"fused decode launch: {launch_us:.2f} us avg, {achieved:.1f} GB/s")
+    kernel = "decode_kernel<1, 8, false, true, true>"
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "decode_kernel<1, 8, false, true> (append + split-K attention + "
-                          "combine, one launch per layer)",
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": pmc_traffic(kernel),
+                "kernel": kernel + " (append + split-K attention + combine, one launch "
+                                   "per layer)",
                 "us_per_launch": round(launch_us, 3),
                 "algorithmic_bytes_per_launch": int(bytes_per_launch)}
     del fused_graphs

@@ -46,34 +46,35 @@ namespace crucible {
 namespace {
 
 struct DecodeArgs {
-    // Everything the first loads need sits at the front, so one kernel-argument fetch
-    // covers it and the length and page-id loads can issue together.
+    // The first 64 bytes hold everything the prologue needs (one scalar fetch).
     const int32_t* tables;       // nullptr: contiguous cache (page = pos >> 4)
     const int32_t* lens;         // request b's length is lens[b * lens_stride + lens_off]
-    int64_t table_stride;
+    const int32_t* positions;    // fused append: row b goes to position positions[b]
+    const void* q;
+    int32_t table_stride;
+    int32_t q_row_stride;        // elements between query rows (n_head * 64)
     int lens_stride;             // 1: per-request lengths; 0: one length in params
     int lens_off;                // 0, or CRUCIBLE_PARAM_SEQ for a params buffer
     int max_pages;               // ceil(max_seq / 16) <= table_stride
-    int split_pages;
+    int split_shift;             // a split covers 1 << split_shift pages
     int max_seq;
-    int n_kv_head;
-    const void* q;
+    int n_rep;
+    // the rest
     half_t* k_pool;              // written only by the fused append
     half_t* v_pool;
     void* out;
-    const int32_t* positions;    // fused append: row b goes to position positions[b]
     const void* k_new;           // fused append: [batch][kv_dim] rows (f32 or fp16)
     const void* v_new;
-    int kv_new_f16;
     float* po;                   // [batch][n_head][n_splits][64]
     float* pm;                   // [batch][n_head][n_splits]
     float* pl;                   // [batch][n_head][n_splits]
     uint32_t* counters;          // [batch * n_kv_head]; nullptr: combine in a second kernel
     PoolAddr addr;
-    int64_t q_row_stride;        // elements between query rows (n_head * 64)
+    uint32_t po_bytes;           // size of po (buffer-resource bound)
+    int kv_new_f16;
+    int n_kv_head;
     int batch;
     int n_head;
-    int n_rep;
     int n_splits;
     int out_f16;
     float scale_log2;            // (1/sqrt(64)) * log2(e)
@@ -109,6 +110,7 @@ __device__ __forceinline__ float load_coherent(const float* p) {
 __device__ __forceinline__ void combine_partials(const DecodeArgs& a, int b, int hh, int d4,
                                                  int n_active) {
     const int64_t slot0 = ((int64_t)b * a.n_head + hh) * a.n_splits;
+    const __amdgpu_buffer_rsrc_t po_rsrc = make_rsrc(a.po, a.po_bytes);
     float M = -INFINITY;
     float L = 0.0f;
     float4_t o = {0.f, 0.f, 0.f, 0.f};
@@ -121,9 +123,10 @@ __device__ __forceinline__ void combine_partials(const DecodeArgs& a, int b, int
                 const int64_t slot = slot0 + s0 + j;
                 mv[j] = load_coherent(a.pm + slot);
                 lv[j] = load_coherent(a.pl + slot);
-                const float* po = a.po + slot * kHeadDim + 4 * d4;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) ov[j][r] = load_coherent(po + r);
+                ov[j] = __builtin_bit_cast(
+                    float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                  po_rsrc, (uint32_t)(slot * kHeadDim + 4 * d4) * 4u, 0,
+                                  kPolicyCoherent));
             } else {
                 mv[j] = -INFINITY;
                 lv[j] = 0.0f;
@@ -158,25 +161,48 @@ struct NewRow {
     half_t v[4];
 };
 
-__device__ __forceinline__ half_t to_half(const void* src, bool f16, int64_t i) {
-    return f16 ? static_cast<const half_t*>(src)[i] : (half_t) static_cast<const float*>(src)[i];
-}
-
+// One uniform branch on the source dtype, then every load of the row is issued back to
+// back (vector loads for K, four scalar loads for V) before any conversion waits on them.
 __device__ __forceinline__ NewRow load_new_row(const DecodeArgs& a, int b, int g, int col,
                                                int grp, int slot) {
     NewRow r{};
     const int64_t row = (int64_t)b * a.addr.kv_dim + g * kHeadDim;
-    const bool f16 = a.kv_new_f16;
-    if (col == slot) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            r.k0[j] = to_half(a.k_new, f16, row + 8 * grp + j);
-            r.k1[j] = to_half(a.k_new, f16, row + 32 + 8 * grp + j);
+    const bool k_lane = col == slot;
+    const bool v_lane = grp == (slot >> 2);
+    if (a.kv_new_f16) {
+        const half_t* k = static_cast<const half_t*>(a.k_new) + row;
+        const half_t* v = static_cast<const half_t*>(a.v_new) + row;
+        if (k_lane) {
+            r.k0 = *reinterpret_cast<const half8_t*>(k + 8 * grp);
+            r.k1 = *reinterpret_cast<const half8_t*>(k + 32 + 8 * grp);
         }
-    }
-    if (grp == (slot >> 2)) {
+        if (v_lane) {
 #pragma unroll
-        for (int db = 0; db < 4; ++db) r.v[db] = to_half(a.v_new, f16, row + 16 * db + col);
+            for (int db = 0; db < 4; ++db) r.v[db] = v[16 * db + col];
+        }
+    } else {
+        const float* k = static_cast<const float*>(a.k_new) + row;
+        const float* v = static_cast<const float*>(a.v_new) + row;
+        float4_t k4[4] = {};
+        float vf[4] = {};
+        if (k_lane) {
+            k4[0] = *reinterpret_cast<const float4_t*>(k + 8 * grp);
+            k4[1] = *reinterpret_cast<const float4_t*>(k + 8 * grp + 4);
+            k4[2] = *reinterpret_cast<const float4_t*>(k + 32 + 8 * grp);
+            k4[3] = *reinterpret_cast<const float4_t*>(k + 32 + 8 * grp + 4);
+        }
+        if (v_lane) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) vf[db] = v[16 * db + col];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            r.k0[j] = (half_t)k4[0][j];
+            r.k0[4 + j] = (half_t)k4[1][j];
+            r.k1[j] = (half_t)k4[2][j];
+            r.k1[4 + j] = (half_t)k4[3][j];
+            r.v[j] = (half_t)vf[j];
+        }
     }
     return r;
 }
@@ -197,7 +223,7 @@ __device__ __forceinline__ void store_new_row(const DecodeArgs& a, const NewRow&
     }
 }
 
-template <int PAGES, int WAVES, bool QF32, bool APPEND>
+template <int PAGES, int WAVES, bool QF32, bool APPEND, bool PAGED>
 __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     __shared__ float4_t s_acc[WAVES][16][17];  // [wave][col][dim/4], padded
     __shared__ float s_m[WAVES][16];
@@ -215,25 +241,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     const int b = blockIdx.z;
     const int bg = b * a.n_kv_head + g;
 
-    // Length, append position and page ids in one round trip.
-    const int32_t* table = a.tables ? a.tables + (int64_t)b * a.table_stride : nullptr;
-    const int wp0 = s * a.split_pages + wave * PAGES;
-    int64_t page[PAGES];
-#pragma unroll
-    for (int i = 0; i < PAGES; ++i) {
-        const int p = wp0 + i;
-        page[i] = (table && p < a.max_pages) ? (int64_t)table[p] : (int64_t)p;
-    }
-    const int len = request_len(a, b);
-    int apos = -1;  // position of the row this workgroup appends, or -1
-    if constexpr (APPEND) {
-        const int pos = a.positions[b];
-        if (pos >= 0 && pos < a.max_pages * kPageTokens && (pos >> kPageShift) / a.split_pages == s)
-            apos = pos;
-    }
-
-    // Query operand: B[k = channel][col = head], 8 channels per lane per MFMA. Loaded
-    // before the length is known (the address does not depend on it).
+    // Query operand: B[k = channel][col = head], 8 channels per lane per MFMA. Issued
+    // first: its address does not depend on anything loaded.
     const int h = g * a.n_rep + col;
     half8_t qh0 = {}, qh1 = {}, ql0 = {}, ql1 = {};
     if (col < a.n_rep) {
@@ -255,8 +264,31 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
         }
     }
 
+    // First round trip: the page ids, the length and the append position come from ONE
+    // vector load (lane i < PAGES: page id i; lane PAGES: length; lane PAGES + 1: append
+    // position) and are broadcast with readlane, so no compiler scheduling can split them
+    // into dependent scalar loads. Table indices are clamped into the table, so every
+    // lane's address is in bounds (ids of pages past the request's end are never used).
+    const int wp0 = (s << a.split_shift) + wave * PAGES;
+    const int32_t* src = a.lens + b * a.lens_stride + a.lens_off;
+    if (PAGED && lane < PAGES)
+        src = a.tables + (int64_t)b * a.table_stride + min(wp0 + lane, a.max_pages - 1);
+    if (APPEND && lane == PAGES + 1) src = a.positions + b;
+    const int gathered = *src;
+    int64_t page[PAGES];
+#pragma unroll
+    for (int i = 0; i < PAGES; ++i)
+        page[i] = PAGED ? (int64_t)__builtin_amdgcn_readlane(gathered, i) : (int64_t)(wp0 + i);
+    const int len_raw = __builtin_amdgcn_readlane(gathered, PAGES);
+    const int len = len_raw < a.max_seq ? len_raw : a.max_seq;  // never index past the table
+    const int pos = APPEND ? __builtin_amdgcn_readlane(gathered, PAGES + 1) : -1;
+    int apos = -1;  // position of the row this workgroup appends, or -1
+    if (APPEND && pos >= 0 && pos < (a.max_pages << kPageShift) &&
+        (pos >> (kPageShift + a.split_shift)) == s)
+        apos = pos;
+
     const int n_pages = len > 0 ? (len + kPageMask) >> kPageShift : 0;
-    const int p_begin = s * a.split_pages;
+    const int p_begin = s << a.split_shift;
     const bool attend = p_begin < n_pages;
     if (!attend && apos < 0) return;
     // index of the appended row's page among this wave's pages (wave-uniform), or -1
@@ -273,7 +305,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
         }
         return;
     }
-    const int n_active = (n_pages + a.split_pages - 1) / a.split_pages;
+    const int n_active = (n_pages + (1 << a.split_shift) - 1) >> a.split_shift;
     const int wp_end = min(wp0 + PAGES, n_pages);
 
     // Issue every load of this wave's pages before any arithmetic.
@@ -404,9 +436,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
             store_out4(a, (int64_t)b * a.q_row_stride + (int64_t)hh * kHeadDim + 4 * d4, o * (1.0f / L));
         } else {
             const int64_t slot = ((int64_t)b * a.n_head + hh) * a.n_splits + s;
-            float* po = a.po + slot * kHeadDim + 4 * d4;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) store_coherent(po + r, o[r]);
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(u32x4_t, o), make_rsrc(a.po, a.po_bytes),
+                (uint32_t)(slot * kHeadDim + 4 * d4) * 4u, 0, kPolicyCoherent);
             if (d4 == 0) {
                 store_coherent(a.pm + slot, M);
                 store_coherent(a.pl + slot, L);
@@ -440,7 +472,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
     const int len = request_len(a, b);
     if (len <= 0) return;
     const int n_pages = (len + kPageMask) >> kPageShift;
-    const int n_active = (n_pages + a.split_pages - 1) / a.split_pages;
+    const int n_active = (n_pages + (1 << a.split_shift) - 1) >> a.split_shift;
     if (n_active <= 1) return;
     const int ccol = threadIdx.x >> 4;
     if (ccol >= a.n_rep) return;
@@ -471,11 +503,12 @@ DecodeShape decode_shape(int64_t batch, int64_t n_kv_head, int64_t max_pages) {
     return sh;
 }
 
-template <bool QF32, bool APPEND>
+template <bool QF32, bool APPEND, bool PAGED>
 bool launch_shape(const DecodeArgs& a, DecodeShape sh, dim3 grid, hipStream_t stream) {
 #define CRUCIBLE_DECODE_CASE(P, W)                                                           \
     if (sh.pages == P && sh.waves == W) {                                                     \
-        hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND>), grid, dim3(W * 64), 0, stream, a); \
+        hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED>), grid, dim3(W * 64), 0, \
+                           stream, a);                                                        \
         return true;                                                                          \
     }
     CRUCIBLE_DECODE_CASE(1, 4)
@@ -494,12 +527,16 @@ int launch_decode(DecodeArgs a, DecodeShape sh, bool q_f32, hipStream_t stream,
                    CRUCIBLE_ERR_INVALID, "%s: grid (%d, %d, %d) too large", what, a.n_splits,
                    a.n_kv_head, a.batch);
     const dim3 grid((unsigned)a.n_splits, (unsigned)a.n_kv_head, (unsigned)a.batch);
-    const bool append = a.positions != nullptr;
     bool launched;
-    if (append) launched = q_f32 ? launch_shape<true, true>(a, sh, grid, stream)
-                                 : launch_shape<false, true>(a, sh, grid, stream);
-    else launched = q_f32 ? launch_shape<true, false>(a, sh, grid, stream)
-                          : launch_shape<false, false>(a, sh, grid, stream);
+    if (a.positions)  // the fused append exists for paged pools only
+        launched = q_f32 ? launch_shape<true, true, true>(a, sh, grid, stream)
+                         : launch_shape<false, true, true>(a, sh, grid, stream);
+    else if (a.tables)
+        launched = q_f32 ? launch_shape<true, false, true>(a, sh, grid, stream)
+                         : launch_shape<false, false, true>(a, sh, grid, stream);
+    else
+        launched = q_f32 ? launch_shape<true, false, false>(a, sh, grid, stream)
+                         : launch_shape<false, false, false>(a, sh, grid, stream);
     CRUCIBLE_CHECK(launched, CRUCIBLE_ERR_INVALID, "%s: bad decode shape %d x %d", what,
                    sh.pages, sh.waves);
     if (int rc = fail_launch(what)) return rc;
@@ -510,6 +547,8 @@ int launch_decode(DecodeArgs a, DecodeShape sh, bool q_f32, hipStream_t stream,
     }
     return CRUCIBLE_OK;
 }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 int check_geometry(const char* what, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
                    int64_t kv_dim) {
@@ -545,6 +584,7 @@ void bind_workspace(DecodeArgs& a, void* ws) {
     a.pm = f + n * kHeadDim;
     a.pl = a.pm + n;
     a.counters = reinterpret_cast<uint32_t*>(f + partial_floats(a.batch, a.n_head, a.n_splits));
+    a.po_bytes = (uint32_t)(n * kHeadDim * sizeof(float));
 }
 
 DecodeArgs common_args(const void* q, const void* k, const void* v, void* out, int out_dtype,
@@ -554,7 +594,7 @@ DecodeArgs common_args(const void* q, const void* k, const void* v, void* out, i
     a.k_pool = static_cast<half_t*>(const_cast<void*>(k));  // written only by the fused append
     a.v_pool = static_cast<half_t*>(const_cast<void*>(v));
     a.out = out;
-    a.q_row_stride = n_head * kHeadDim;
+    a.q_row_stride = (int32_t)(n_head * kHeadDim);
     a.batch = (int)batch;
     a.n_head = (int)n_head;
     a.n_kv_head = (int)n_kv_head;
@@ -569,10 +609,19 @@ DecodeArgs common_args(const void* q, const void* k, const void* v, void* out, i
 // Split the request into workgroups, bind the workspace and launch.
 int decode_with_workspace(DecodeArgs& a, bool q_f32, void* workspace, size_t workspace_bytes,
                           hipStream_t stream, const char* what) {
+    // the kernel moves q, pools, out and appended rows in 16-byte vectors
+    CRUCIBLE_CHECK(aligned16(a.q) && aligned16(a.k_pool) && aligned16(a.v_pool) &&
+                       aligned16(a.out) && aligned16(a.k_new) && aligned16(a.v_new),
+                   CRUCIBLE_ERR_INVALID, "%s: q, pools, out and new rows must be 16-byte aligned",
+                   what);
     const DecodeShape sh = decode_shape(a.batch, a.n_kv_head, a.max_pages);
-    a.split_pages = sh.pages * sh.waves;
-    a.n_splits = (a.max_pages + a.split_pages - 1) / a.split_pages;
+    const int split_pages = sh.pages * sh.waves;  // a power of two
+    a.split_shift = __builtin_ctz((unsigned)split_pages);
+    a.n_splits = (a.max_pages + split_pages - 1) / split_pages;
     if (a.n_splits > 1) {
+        CRUCIBLE_CHECK((size_t)a.batch * a.n_head * a.n_splits * kHeadDim * sizeof(float) <
+                           ((size_t)1 << 31),
+                       CRUCIBLE_ERR_INVALID, "%s: split partials exceed 2 GiB", what);
         const size_t need = workspace_need(a.batch, a.n_head, a.n_splits);
         CRUCIBLE_CHECK(workspace && workspace_bytes >= need, CRUCIBLE_ERR_WORKSPACE,
                        "%s: workspace needs %zu bytes, got %zu", what, need,
@@ -615,8 +664,8 @@ extern "C" int crucible_attention_decode_paged(
     CRUCIBLE_CHECK(n_layer > 0 && layer >= 0 && layer < n_layer, CRUCIBLE_ERR_INVALID,
                    "%s: layer %lld outside n_layer %lld", what, (long long)layer,
                    (long long)n_layer);
-    CRUCIBLE_CHECK(table_stride > 0 && max_seq > 0 && max_seq <= table_stride * kPageTokens &&
-                       max_seq <= INT32_MAX,
+    CRUCIBLE_CHECK(table_stride > 0 && table_stride <= INT32_MAX && max_seq > 0 &&
+                       max_seq <= table_stride * kPageTokens && max_seq <= INT32_MAX,
                    CRUCIBLE_ERR_INVALID, "%s: max_seq %lld must be in 1..table_stride*16", what,
                    (long long)max_seq);
     DecodeArgs a = common_args(q, k_pool, v_pool, out, out_dtype, batch, n_head, n_kv_head,
@@ -627,7 +676,7 @@ extern "C" int crucible_attention_decode_paged(
     a.addr.kv_dim = (int32_t)kv_dim;
     a.addr.page_stride = n_layer * kPageTokens * kv_dim;
     a.addr.layer_off = layer * kPageTokens * kv_dim;
-    a.table_stride = table_stride;
+    a.table_stride = (int32_t)table_stride;
     return decode_with_workspace(a, q_dtype == CRUCIBLE_F32, workspace, workspace_bytes, stream,
                                  what);
 }
@@ -651,8 +700,8 @@ extern "C" int crucible_attention_decode_paged_append(
     CRUCIBLE_CHECK(n_layer > 0 && layer >= 0 && layer < n_layer, CRUCIBLE_ERR_INVALID,
                    "%s: layer %lld outside n_layer %lld", what, (long long)layer,
                    (long long)n_layer);
-    CRUCIBLE_CHECK(table_stride > 0 && max_seq > 0 && max_seq <= table_stride * kPageTokens &&
-                       max_seq <= INT32_MAX,
+    CRUCIBLE_CHECK(table_stride > 0 && table_stride <= INT32_MAX && max_seq > 0 &&
+                       max_seq <= table_stride * kPageTokens && max_seq <= INT32_MAX,
                    CRUCIBLE_ERR_INVALID, "%s: max_seq %lld must be in 1..table_stride*16", what,
                    (long long)max_seq);
     DecodeArgs a = common_args(q, k_pool, v_pool, out, out_dtype, batch, n_head, n_kv_head,
@@ -667,7 +716,7 @@ extern "C" int crucible_attention_decode_paged_append(
     a.addr.kv_dim = (int32_t)kv_dim;
     a.addr.page_stride = n_layer * kPageTokens * kv_dim;
     a.addr.layer_off = layer * kPageTokens * kv_dim;
-    a.table_stride = table_stride;
+    a.table_stride = (int32_t)table_stride;
     return decode_with_workspace(a, q_dtype == CRUCIBLE_F32, workspace, workspace_bytes, stream,
                                  what);
 }
@@ -724,11 +773,14 @@ extern "C" int crucible_attention_split(const void* q, int q_dtype, const void* 
     // 128-position chunks as in the reference (gpu.rs:37 ATTN_CHUNK): 4 waves x 2 pages,
     // partials in the caller's buffers, combined by a second kernel.
     const DecodeShape sh{2, 4};
-    a.split_pages = 8;
+    a.split_shift = 3;  // 8 pages
     a.n_splits = (int)((capacity + 127) / 128);
     a.po = partial_o;
     a.pm = partial_m;
     a.pl = partial_l;
     a.counters = nullptr;
+    CRUCIBLE_CHECK((size_t)n_head * a.n_splits * kHeadDim * sizeof(float) < ((size_t)1 << 31),
+                   CRUCIBLE_ERR_INVALID, "%s: split partials exceed 2 GiB", what);
+    a.po_bytes = (uint32_t)((size_t)n_head * a.n_splits * kHeadDim * sizeof(float));
     return launch_decode(a, sh, q_dtype == CRUCIBLE_F32, stream, what);
 }

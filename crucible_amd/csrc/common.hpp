@@ -61,6 +61,19 @@ __device__ __forceinline__ float4_t mfma_16x16x16(half4_t a, half4_t b, float4_t
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
+// Raw buffer resource over [base, base + bytes) for 16-byte loads and stores that carry a
+// cache policy (word 3 is the gfx9 raw-buffer format). Accesses past `bytes` are dropped
+// (stores) or read zero (loads).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// Cache policy sc1: agent-scope coherent (write-through stores, loads that do not hit
+// another XCD's stale L2 line).
+constexpr int kPolicyCoherent = 16;
+
 // log2(e): softmax is evaluated as 2^(s * scale * log2e - m) with m in the same units.
 constexpr float kLog2e = 1.4426950408889634f;
 

@@ -36,7 +36,8 @@
 // complete, and bumps a per-(request, kv head) counter; the workgroup that brings the counter to the number of active splits
 // resets it to zero and performs the combine. Counters therefore read zero between
 // launches: the workspace must be zeroed once when it is allocated, and one workspace
-// serves one launch at a time.
+// serves one launch at a time (calls of any batch size may share it: the counters sit
+// at a fixed place at its start).
 #include "common.hpp"
 
 #include <cmath>
@@ -566,24 +567,27 @@ int check_geometry(const char* what, int64_t n_head, int64_t n_kv_head, int64_t 
     return CRUCIBLE_OK;
 }
 
-// Workspace: partial o, m, l for every (request, query head, split), then one counter
-// per (request, kv head). Sized for the smallest split (1 page x 4 waves).
+// Workspace: a fixed region of kMaxCounters u32 combine counters (index b * n_kv_head + g,
+// the same place for every batch size, so calls of different batch sizes can share one
+// workspace), then partial o, m, l for every (request, query head, split).
+constexpr int64_t kMaxCounters = 65536;
+constexpr size_t kCounterBytes = kMaxCounters * sizeof(uint32_t);
+
 size_t partial_floats(int64_t batch, int64_t n_head, int64_t n_splits) {
     return (size_t)batch * n_head * n_splits * (kHeadDim + 2);
 }
 
 size_t workspace_need(int64_t batch, int64_t n_head, int64_t n_splits) {
-    return partial_floats(batch, n_head, n_splits) * sizeof(float) +
-           (size_t)batch * n_head * sizeof(uint32_t);
+    return kCounterBytes + partial_floats(batch, n_head, n_splits) * sizeof(float);
 }
 
 void bind_workspace(DecodeArgs& a, void* ws) {
-    float* f = static_cast<float*>(ws);
+    a.counters = static_cast<uint32_t*>(ws);
+    float* f = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
     const size_t n = (size_t)a.batch * a.n_head * a.n_splits;
     a.po = f;
     a.pm = f + n * kHeadDim;
     a.pl = a.pm + n;
-    a.counters = reinterpret_cast<uint32_t*>(f + partial_floats(a.batch, a.n_head, a.n_splits));
     a.po_bytes = (uint32_t)(n * kHeadDim * sizeof(float));
 }
 
@@ -622,6 +626,8 @@ int decode_with_workspace(DecodeArgs& a, bool q_f32, void* workspace, size_t wor
         CRUCIBLE_CHECK((size_t)a.batch * a.n_head * a.n_splits * kHeadDim * sizeof(float) <
                            ((size_t)1 << 31),
                        CRUCIBLE_ERR_INVALID, "%s: split partials exceed 2 GiB", what);
+        CRUCIBLE_CHECK((int64_t)a.batch * a.n_kv_head <= kMaxCounters, CRUCIBLE_ERR_INVALID,
+                       "%s: batch * n_kv_head exceeds %lld", what, (long long)kMaxCounters);
         const size_t need = workspace_need(a.batch, a.n_head, a.n_splits);
         CRUCIBLE_CHECK(workspace && workspace_bytes >= need, CRUCIBLE_ERR_WORKSPACE,
                        "%s: workspace needs %zu bytes, got %zu", what, need,

@@ -18,7 +18,9 @@
 // blocks of 16 query rows for one head. Per 64-key tile and 16-row block:
 //   S^T[64 key x 16 q] = K[64 x 64] . Q^T        8x mfma_f32_16x16x32_f16
 //   online softmax per query column (base 2), causal mask by absolute position
-//   O^T[64 dim x 16 q] += V^T[64 x 64 key] . P^T 8x mfma_f32_16x16x32_f16
+//   O^T[64 dim x 16 q] += V^T[64 x 64 key] . P^T 16x mfma_f32_16x16x32_f16, with P
+//     split into fp16 hi + lo parts so the product keeps ~22 bits of P (an f32 query
+//     is split the same way for QK^T)
 // The transposed V pages are copied into LDS as-is (no transpose on the way), and the
 // P^T operand is exactly the register layout the S^T product leaves behind.
 // Tiles are double-buffered in LDS; a wave skips tiles that lie wholly above the
@@ -256,6 +258,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
                     }
                 }
                 half8_t pb[QB][2];
+                half8_t pl[QB][2];  // P = hi + lo: the product keeps ~22 bits of P
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) {
                     float tm = -INFINITY;
@@ -273,9 +276,11 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
                     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const half_t p = (half_t)fast_exp2(sv[qb][kb][r] - mu);
-                            pb[qb][kb >> 1][(kb & 1) * 4 + r] = p;
-                            ps += (float)p;
+                            const float pf = fast_exp2(sv[qb][kb][r] - mu);
+                            const half_t ph = (half_t)pf;
+                            pb[qb][kb >> 1][(kb & 1) * 4 + r] = ph;
+                            pl[qb][kb >> 1][(kb & 1) * 4 + r] = (half_t)(pf - (float)ph);
+                            ps += pf;
                         }
                     l[qb] = l[qb] * alpha + ps;
                     m[qb] = mn;
@@ -292,7 +297,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
                         const half4_t v1 = *reinterpret_cast<const half4_t*>(vrow + 32 * ks + 16 + 4 * grp);
                         const half8_t va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
 #pragma unroll
-                        for (int qb = 0; qb < QB; ++qb) acc[qb][db] = mfma_16x16x32(va, pb[qb][ks], acc[qb][db]);
+                        for (int qb = 0; qb < QB; ++qb) {
+                            acc[qb][db] = mfma_16x16x32(va, pb[qb][ks], acc[qb][db]);
+                            acc[qb][db] = mfma_16x16x32(va, pl[qb][ks], acc[qb][db]);
+                        }
                     }
                 }
             }

@@ -249,3 +249,11 @@ class Gpu:
             _ptr(q), _dtype(q, "q"), _ptr(k_cache), _ptr(v_cache), _ptr(out), _dtype(out, "out"),
             rows, n_head, n_kv_head, head_dim, max_seq, cache_stride, layer_base, pos_offset,
             self._stream()))
+
+    # ------------------------------------------------------------- greedy selection
+    def argmax_rows(self, x, out, rows, cols):
+        """gpu.rs:562-580 with the host rule of sampling.rs:141-150: ties to the lowest
+        index, NaN never wins (a NaN at index 0 yields 0)."""
+        _need(x, "x", dtype=torch.float32, numel=rows * cols)
+        _need(out, "out", dtype=torch.int32, numel=rows)
+        _lib.check(self.lib.crucible_argmax_rows(_ptr(x), _ptr(out), rows, cols, self._stream()))

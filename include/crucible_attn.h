@@ -108,10 +108,12 @@ int crucible_cache_store_packed_paged(const void* src, int src_dtype, void* pool
  * n_head / n_kv_head <= 16. Query head h reads KV head h / (n_head / n_kv_head).
  * The split-K partials live in a caller-provided workspace of at least
  * crucible_attention_decode_workspace_bytes(...) bytes (no allocation here),
- * 16-byte aligned. The workspace also holds one counter per (request, kv head)
- * that orders the in-kernel combine of the splits: zero it once when it is
- * allocated; every launch leaves it zeroed again. A workspace serves one launch
- * at a time (launches that share one must be ordered, e.g. on one stream).
+ * 16-byte aligned. It starts with a fixed region of 65536 u32 counters, one per
+ * (request, kv head) (so batch * n_kv_head <= 65536), that order the in-kernel
+ * combine of the splits: zero the workspace once when it is allocated; every
+ * launch leaves the counters zeroed again. Calls of any batch size may share one
+ * workspace, one launch at a time (launches that share it must be ordered, e.g.
+ * on one stream).
  */
 
 size_t crucible_attention_decode_workspace_bytes(int64_t batch, int64_t n_head,
@@ -213,6 +215,15 @@ int crucible_attention_prefill(const void* q, int q_dtype, const void* k_cache,
                                int64_t n_head, int64_t n_kv_head, int64_t head_dim,
                                int64_t max_seq, int64_t cache_stride, int64_t layer_base,
                                int64_t pos_offset, crucible_stream_t stream);
+
+/* ------------------------------------------------------------------ greedy selection */
+
+/* Replaces Gpu::argmax_rows (gpu.rs:562-580; kernels.cu:1215-1260): out[r] = index of
+ * the largest x[r * cols + i], with the host rule of sampling.rs:141-150 (ties to the
+ * lowest index, -0.0 == +0.0, NaN never displaces an element, a NaN at index 0 yields
+ * 0). x is [rows][cols] f32, out is [rows] int32. */
+int crucible_argmax_rows(const float* x, int32_t* out, int64_t rows, int64_t cols,
+                         crucible_stream_t stream);
 
 /* ------------------------------------------------------------------ host helpers */
 

@@ -296,27 +296,38 @@ int orc_attention_dense(const float* q, const float* k, const float* v, const in
     if (n_kv_head <= 0 || n_head % n_kv_head) return -1;
     const int64_t n_rep = n_head / n_kv_head;
     const int64_t kv_dim = n_kv_head * head_dim;
-    double* s64 = (double*)malloc(sizeof(double) * (size_t)(n_k > 0 ? n_k : 1));
-    float* s32 = (float*)malloc(sizeof(float) * (size_t)(n_k > 0 ? n_k : 1));
-    if (!s64 || !s32) { free(s64); free(s32); return -2; }
-    for (int64_t i = 0; i < n_q; ++i) {
-        const int64_t len = lens[i];
-        if (len <= 0 || len > n_k) continue; /* inactive rows are left untouched */
-        for (int64_t h = 0; h < n_head; ++h) {
-            const int64_t g = h / n_rep;
-            const float* qh = q + i * n_head * head_dim + h * head_dim;
-            float* oh = out + i * n_head * head_dim + h * head_dim;
-            if (precise)
-                attend_one_f64(qh, k + g * head_dim, v + g * head_dim, len, kv_dim, head_dim,
-                               scale, s64, oh, NULL);
-            else
-                attend_one_ref_f32(qh, k + g * head_dim, v + g * head_dim, len, kv_dim,
-                                   head_dim, (float)scale, s32, oh);
+    int rc = 0;
+    /* Rows are independent: threads split them, each with its own score buffers, and
+     * every value is computed exactly as in the single-threaded loop. */
+#pragma omp parallel
+    {
+        double* s64 = (double*)malloc(sizeof(double) * (size_t)(n_k > 0 ? n_k : 1));
+        float* s32 = (float*)malloc(sizeof(float) * (size_t)(n_k > 0 ? n_k : 1));
+        if (!s64 || !s32) {
+#pragma omp atomic write
+            rc = -2;
+        } else {
+#pragma omp for schedule(dynamic, 1)
+            for (int64_t i = 0; i < n_q; ++i) {
+                const int64_t len = lens[i];
+                if (len <= 0 || len > n_k) continue; /* inactive rows are left untouched */
+                for (int64_t h = 0; h < n_head; ++h) {
+                    const int64_t g = h / n_rep;
+                    const float* qh = q + i * n_head * head_dim + h * head_dim;
+                    float* oh = out + i * n_head * head_dim + h * head_dim;
+                    if (precise)
+                        attend_one_f64(qh, k + g * head_dim, v + g * head_dim, len, kv_dim,
+                                       head_dim, scale, s64, oh, NULL);
+                    else
+                        attend_one_ref_f32(qh, k + g * head_dim, v + g * head_dim, len, kv_dim,
+                                           head_dim, (float)scale, s32, oh);
+                }
+            }
         }
+        free(s64);
+        free(s32);
     }
-    free(s64);
-    free(s32);
-    return 0;
+    return rc;
 }
 
 /*

@@ -77,8 +77,8 @@ def test_invalid_arguments_are_rejected_before_launch():
 
 def test_workspace_size_formula():
     lib = _lib.load()
-    # worst case 4-page splits: ceil(ceil(2048/16)/4) = 32 splits, 66 floats per (b, h, split),
-    # then one 4-byte combine counter per (b, h)
+    # a fixed 65536-counter region (256 KiB), then the worst case of 4-page splits:
+    # ceil(ceil(2048/16)/4) = 32 splits, 66 floats per (b, h, split)
     assert lib.crucible_attention_decode_workspace_bytes(16, 12, 2048) == (
-        16 * 12 * 32 * 66 * 4 + 16 * 12 * 4)
+        65536 * 4 + 16 * 12 * 32 * 66 * 4)
     assert lib.crucible_attention_decode_workspace_bytes(0, 12, 2048) == 0

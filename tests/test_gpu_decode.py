@@ -316,3 +316,29 @@ def test_decode_shapes_agree(gpu, dev, monkeypatch):
             assert np.array_equal(o2.view(np.uint32), o1.view(np.uint32)), (pages, waves)
             want = _oracle(q.astype(np.float32), k1, v1, tables, lens, 12, 3, 3, 1)
             assert np.abs(o2 - want).max() <= TOL, (pages, waves)
+
+
+def test_workspace_shared_across_batch_sizes(gpu, dev):
+    """One workspace (sized for the largest batch) serves decode calls whose batch size
+    changes from call to call, as the engine's active count does step to step."""
+    rng = np.random.default_rng(90)
+    n_head, n_kv, n_layer, max_batch, stride = 12, 3, 2, 16, 128
+    nbytes = gpu.lib.crucible_attention_decode_workspace_bytes(max_batch, n_head, stride * 16)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    n_pages = max_batch * stride + 2
+    kp, vp = random_pools(rng, n_pages, n_layer, n_kv * 64)
+    d_k, d_v = _dev(kp, dev), _dev(vp, dev)
+    for batch in (16, 5, 11, 16, 1, 16):
+        lens = rng.integers(1, stride * 16 + 1, batch)
+        tables = disjoint_tables(rng, n_pages, lens, stride)
+        q = rng.standard_normal((batch, n_head * 64)).astype(np.float16).astype(np.float32)
+        out = torch.full((batch, n_head * 64), SENTINEL, device=dev)
+        gpu.attention_decode_paged(_dev(q.astype(np.float16), dev), d_k, d_v, out,
+                                   _dev(tables, dev), _dev(lens.astype(np.int32), dev), batch,
+                                   n_head, n_kv, 64, stride, n_layer, 1, n_kv * 64, stride * 16,
+                                   workspace=ws)
+        torch.cuda.synchronize()
+        want = _oracle(q, kp, vp, tables, lens, n_head, n_kv, n_layer, 1)
+        assert np.abs(out.cpu().numpy() - want).max() <= TOL, batch
+    # every counter is back to zero
+    assert int(ws[:65536 * 4].view(torch.int32).abs().sum()) == 0

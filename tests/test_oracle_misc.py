@@ -28,8 +28,21 @@ def test_argmax_adversarial_rows():
     nan_mid = np.ones(vocab, np.float32)
     nan_mid[500], nan_mid[900] = np.nan, 4.0
     all_nan = np.full(vocab, np.nan, np.float32)
+    # beyond the reference's rows: NaN before the maximum, signed zeros, infinities
+    nan_early = np.ones(vocab, np.float32)
+    nan_early[[1, 100, 1023]] = np.nan
+    nan_early[2000] = 3.0
+    zeros = np.full(vocab, -1.0, np.float32)
+    zeros[10], zeros[20] = np.float32(-0.0), np.float32(0.0)
+    inf = np.zeros(vocab, np.float32)
+    inf[[77, 78]] = np.inf
+    neg_inf = np.full(vocab, -np.inf, np.float32)
+    neg_inf[3000] = -1e30
+    last_finite = np.full(vocab, np.nan, np.float32)
+    last_finite[0], last_finite[-1] = -5.0, 7.0
     cases = [(dense, 31337), (tied, 100), (first, 0), (last, vocab - 1), (close, 4242),
-             (all_neg, 0), (nan_first, 0), (nan_mid, 900), (all_nan, 0)]
+             (all_neg, 0), (nan_first, 0), (nan_mid, 900), (all_nan, 0), (nan_early, 2000),
+             (zeros, 10), (inf, 77), (neg_inf, 3000), (last_finite, vocab - 1)]
     for row, want in cases:
         assert oracle.argmax(row) == want
 

@@ -13,18 +13,24 @@
 //   PARAMS    one table, position params[5] + r (attention_prefill_paged, gpu.rs:1502-1549)
 //   CONTIG    contiguous cache, position pos_offset + r (attention_prefill, gpu.rs:1886-1934)
 //
-// Workgroup = 4 waves = (4 / HPW) row slices x HPW query heads of one GQA group, so the
-// HPW heads that share a kv head share every K/V tile staged in LDS. A wave owns QB
-// blocks of 16 query rows for one head. Per 64-key tile and 16-row block:
-//   S^T[64 key x 16 q] = K[64 x 64] . Q^T        8x mfma_f32_16x16x32_f16
+// Workgroup = 8 waves: 4 slots = (4 / HPW) row slices x HPW query heads of one GQA
+// group, so the HPW heads that share a kv head share every K/V tile staged in LDS, and
+// two waves per slot that split each 64-key tile into halves (their online-softmax
+// states merge at the end). A slot owns QB blocks of 16 query rows for one head. Per
+// 64-key tile and 16-row block, each wave of the pair computes its 32 keys:
+//   S^T[32 key x 16 q] = K[32 x 64] . Q^T        4x mfma_f32_16x16x32_f16
 //   online softmax per query column (base 2), causal mask by absolute position
-//   O^T[64 dim x 16 q] += V^T[64 x 64 key] . P^T 16x mfma_f32_16x16x32_f16, with P
+//   O^T[64 dim x 16 q] += V^T[64 x 32 key] . P^T 8x mfma_f32_16x16x32_f16, with P
 //     split into fp16 hi + lo parts so the product keeps ~22 bits of P (an f32 query
 //     is split the same way for QK^T)
 // The transposed V pages are copied into LDS as-is (no transpose on the way), and the
 // P^T operand is exactly the register layout the S^T product leaves behind.
-// Tiles are double-buffered in LDS; a wave skips tiles that lie wholly above the
-// causal diagonal of its rows (the workgroup still loads up to its last row).
+// Tiles stream into a ring of kBufs LDS buffers with direct-to-LDS loads
+// (global_load_lds_dwordx4, no register staging), kBufs - 1 tiles ahead of the one being
+// computed, so HBM latency overlaps the MFMA work; 16-byte chunks of each 128-byte LDS
+// row are XOR-swizzled by row so the operand reads stay (almost) free of bank conflicts.
+// A wave skips tiles that lie wholly above the causal diagonal of its rows (the
+// workgroup still loads up to its last row).
 //
 // Rows of a workgroup are processed in runs of one owner (table). SEGMENTS, PARAMS and
 // CONTIG tiles are always a single run; an OWNERS tile that straddles two requests
@@ -40,8 +46,13 @@ namespace {
 enum RowMode { kSegments = 0, kOwners = 1, kParams = 2, kContig = 3 };
 
 constexpr int kKeyTile = 64;
-constexpr int kLdsPad = 8;                   // halfs of padding per LDS row
-constexpr int kLdsRow = kKeyTile + kLdsPad;  // 72 halfs = 144 bytes
+constexpr int kBufs = 4;  // LDS ring depth: tiles kt+1 .. kt+3 load while tile kt computes
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0], expcnt[6:4] = 7 (no wait), lgkmcnt[11:8])
+constexpr int kWaitVm0Lgkm0 = 0x0070;
+constexpr int kWaitVm2Lgkm0 = 0x0072;
+constexpr int kWaitVm4Lgkm0 = 0x0074;
+constexpr int kThreads = 512;  // 8 waves: 4 row/head slots x 2 key halves
 
 struct PrefillArgs {
     const void* q;
@@ -66,33 +77,43 @@ struct PrefillArgs {
     float scale_log2;
 };
 
+// `tables` is passed on its own, read-only and unaliased, so the page-id loads of the
+// tile loop compile to scalar loads (lgkmcnt) that never wait on the in-flight tiles.
 template <int HPW, int QB, bool QF32>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
+                                                      const int32_t* __restrict__ tables) {
     constexpr int RS = 4 / HPW;          // row slices per workgroup
     constexpr int WROWS = 16 * QB;       // rows per wave
     constexpr int R = RS * WROWS;        // rows per workgroup
 
-    __shared__ half_t s_k[2][kKeyTile][kLdsRow];  // [buf][key][dim]
-    __shared__ half_t s_v[2][64][kLdsRow];        // [buf][dim][key]
+    // ring of key tiles, 128-byte rows whose 16-byte chunks are XOR-swizzled by row
+    __shared__ half_t s_k[kBufs][kKeyTile][64];   // [buf][key][dim]
+    __shared__ half_t s_v[kBufs][64][kKeyTile];   // [buf][dim][key]
     __shared__ int s_owner[R];
     __shared__ int s_pos[R];
     __shared__ int s_row[R];
+    __shared__ uint64_t s_mask[2];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int col = lane & 15;
     const int grp = lane >> 4;
-    const int rs = wave / HPW;
-    const int hi = wave % HPW;
+    // Waves w and w + 4 own the same rows and head (slot w & 3) and split every key tile:
+    // wave w takes keys 0..31 of each tile, wave w + 4 keys 32..63. Two waves per SIMD
+    // then interleave their MFMA/softmax chains; their states merge at the end.
+    const int kh = wave >> 2;   // key half
+    const int slot = wave & 3;
+    const int rs = slot / HPW;
+    const int hi = slot % HPW;
 
     const int groups_per_kv = a.n_rep / HPW;
     const int g = blockIdx.x / groups_per_kv;
     const int h = g * a.n_rep + (blockIdx.x % groups_per_kv) * HPW + hi;
 
     // ---- rows of this tile: (packed row, owner, absolute position); -1 = none
+    int row = -1, owner = 0, pos = 0;
     if (tid < R) {
-        int row = -1, owner = 0, pos = 0;
         const int64_t local = (int64_t)blockIdx.y * R + tid;
         if (a.mode == kSegments) {
             const int32_t* seg = a.segments + 4 * (int64_t)blockIdx.z;
@@ -117,8 +138,13 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
         s_owner[tid] = owner;
         s_pos[tid] = pos;
     }
+    // valid-row masks of rows 0..63 and 64..127 (R <= 128, so waves 0 and 1 cover them)
+    const uint64_t vmask = __ballot(tid < R && row >= 0);
+    if (wave < 2 && lane == 0) s_mask[wave] = vmask;
     __syncthreads();
-    if (s_row[0] < 0 && a.mode != kOwners) return;  // uniform: tile past the chunk end
+    const uint64_t mask0 = s_mask[0];
+    const uint64_t mask1 = R > 64 ? s_mask[1] : 0;
+    if (mask0 == 0 && mask1 == 0) return;  // uniform: no row of this tile is valid
 
     // ---- per-lane query state for each 16-row block
     const int64_t ld_q = (int64_t)a.n_head * kHeadDim;
@@ -157,67 +183,89 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     }
 
     const int kv_dim = a.addr.kv_dim;
-    // Cooperative tile loader: K as [key][dim] (thread: key t/4, dims 16*(t%4)..+15),
-    // V^T as [dim][key] (thread: page t/64 of the tile, channel t%64, 16 slots).
-    const int lk_key = tid >> 2, lk_c = (tid & 3) * 16;
-    const int lv_pg = tid >> 6, lv_d = tid & 63;
+    // The query operands are complete before the first tile load is issued, so no wait
+    // for them can land inside the tile loop (where it would also wait for the tiles).
+    __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
 
-    // ---- runs of one owner
-    int r0 = 0;
+    // ---- runs of one owner (the values come from LDS: readfirstlane makes the compiler
+    // treat them as the wave-uniform values they are, so page ids load as scalars)
+    // Segment, params and contiguous tiles hold one run of consecutive positions: its
+    // rows are the span of valid rows, read off the masks. Owner tiles may hold several
+    // runs (one per request) and are scanned row by row.
+    const int first_valid = mask0 ? __builtin_ctzll(mask0) : 64 + __builtin_ctzll(mask1);
+    const int last_valid = mask1 ? 127 - __builtin_clzll(mask1) : 63 - __builtin_clzll(mask0);
+    int r0 = a.mode == kOwners ? 0 : first_valid;
     while (r0 < R) {
-        // next run start: first valid row at or after r0
-        while (r0 < R && s_row[r0] < 0) ++r0;
-        if (r0 >= R) break;
-        const int owner = s_owner[r0];
-        int r1 = r0 + 1;
-        while (r1 < R && s_row[r1] >= 0 && s_owner[r1] == owner) ++r1;
-        int hist_end = 0;
-        for (int r = r0; r < r1; ++r) hist_end = max(hist_end, s_pos[r] + 1);
-        // this wave's last visible key within the run
-        int wave_last = -1;
-        for (int r = max(r0, rs * WROWS); r < min(r1, rs * WROWS + WROWS); ++r)
-            wave_last = max(wave_last, s_pos[r]);
+        int r1, owner, hist_end, wave_last;
+        const int wlo = rs * WROWS, whi = rs * WROWS + WROWS;
+        if (a.mode != kOwners) {
+            r1 = last_valid + 1;
+            owner = s_owner[r0];
+            hist_end = s_pos[last_valid] + 1;
+            const int lo = max(r0, wlo), hi = min(r1, whi);
+            wave_last = lo < hi ? s_pos[hi - 1] : -1;
+        } else {
+            // next run start: first valid row at or after r0
+            while (r0 < R && s_row[r0] < 0) ++r0;
+            if (r0 >= R) break;
+            owner = s_owner[r0];
+            r1 = r0 + 1;
+            while (r1 < R && s_row[r1] >= 0 && s_owner[r1] == owner) ++r1;
+            hist_end = 0;
+            for (int r = r0; r < r1; ++r) hist_end = max(hist_end, s_pos[r] + 1);
+            // this wave's last visible key within the run
+            wave_last = -1;
+            for (int r = max(r0, wlo); r < min(r1, whi); ++r) wave_last = max(wave_last, s_pos[r]);
+        }
+        r0 = __builtin_amdgcn_readfirstlane(r0);
+        r1 = __builtin_amdgcn_readfirstlane(r1);
+        owner = __builtin_amdgcn_readfirstlane(owner);
+        hist_end = __builtin_amdgcn_readfirstlane(hist_end);
+        wave_last = __builtin_amdgcn_readfirstlane(wave_last);
 
-        const int32_t* table = a.tables ? a.tables + (int64_t)owner * a.table_stride : nullptr;
+        // Page ids go through the scalar cache (constant address space): the tables are
+        // never written during a launch, and scalar loads (lgkmcnt) never wait on the
+        // in-flight tile loads the way vector loads (vmcnt) would.
+        typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+        const_i32_ptr table = tables ? (const_i32_ptr)(tables + (int64_t)owner * a.table_stride)
+                                     : nullptr;
         const int n_tiles = (hist_end + kKeyTile - 1) / kKeyTile;
+        const int last_page = (hist_end - 1) >> kPageShift;
 
-        half8_t rk[2];
-        half8_t rv[2];
-        auto load_tile = [&](int kt) {
-            const int key = kt * kKeyTile + lk_key;
-            if (key < hist_end) {
-                const int64_t page = table ? (int64_t)table[key >> kPageShift] : (int64_t)(key >> kPageShift);
-                const half_t* kp = a.k_pool + block_base(a.addr, page) +
-                                   (int64_t)(key & kPageMask) * kv_dim + g * kHeadDim + lk_c;
-                rk[0] = *reinterpret_cast<const half8_t*>(kp);
-                rk[1] = *reinterpret_cast<const half8_t*>(kp + 8);
-            } else {
-                rk[0] = rk[1] = half8_t{};
-            }
-            const int key0 = kt * kKeyTile + lv_pg * kPageTokens;
-            if (key0 < hist_end) {
-                const int64_t page = table ? (int64_t)table[key0 >> kPageShift] : (int64_t)(key0 >> kPageShift);
-                const half_t* vp = a.v_pool + block_base(a.addr, page) +
-                                   (int64_t)(g * kHeadDim + lv_d) * kPageTokens;
-                rv[0] = *reinterpret_cast<const half8_t*>(vp);
-                rv[1] = *reinterpret_cast<const half8_t*>(vp + 8);
-                const int valid = hist_end - key0;  // slots >= valid hold no data
-                if (valid < kPageTokens) {
+        // Issue tile t into ring buffer t % kBufs: 4 direct-to-LDS loads per thread.
+        // Page ids past the run's last page are clamped to it (in bounds; masked later).
+        auto issue = [&](int t) {
+            const int buf = t % kBufs;
+            int64_t pg[4];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        if (j >= valid) rv[0][j] = (half_t)0.0f;
-                        if (8 + j >= valid) rv[1][j] = (half_t)0.0f;
-                    }
-                }
-            } else {
-                rv[0] = rv[1] = half8_t{};
+            for (int j = 0; j < 4; ++j) {
+                const int idx = min(t * 4 + j, last_page);
+                pg[j] = table ? (int64_t)table[idx] : (int64_t)idx;
             }
-        };
-        auto store_tile = [&](int buf) {
-            *reinterpret_cast<half8_t*>(&s_k[buf][lk_key][lk_c]) = rk[0];
-            *reinterpret_cast<half8_t*>(&s_k[buf][lk_key][lk_c + 8]) = rk[1];
-            *reinterpret_cast<half8_t*>(&s_v[buf][lv_d][lv_pg * kPageTokens]) = rv[0];
-            *reinterpret_cast<half8_t*>(&s_v[buf][lv_d][lv_pg * kPageTokens + 8]) = rv[1];
+            // K: wave w covers keys 8w .. 8w+7 (page w >> 1 of the tile); lane L puts
+            // chunk (L & 7) ^ (row & 7) of its row at chunk position L & 7.
+            {
+                const int r0k = 8 * wave;
+                const int row = r0k + (lane >> 3);
+                const int c = (lane & 7) ^ (row & 7);
+                const int pj = wave >> 1;
+                const int64_t page = pj == 0 ? pg[0] : pj == 1 ? pg[1] : pj == 2 ? pg[2] : pg[3];
+                const half_t* src = a.k_pool + block_base(a.addr, page) +
+                                    (int64_t)(row & kPageMask) * kv_dim + g * kHeadDim + 8 * c;
+                lds_dma16(src, lds_offset(&s_k[buf][r0k][0]));
+            }
+            // V^T: wave w covers dims 8w .. 8w+7; lane L's chunk c (keys 8c .. 8c+7 of the
+            // tile) comes from page c >> 1, slots 8 * (c & 1) ...
+            {
+                const int d0 = 8 * wave;
+                const int d = d0 + (lane >> 3);
+                const int c = (lane & 7) ^ (d & 7);
+                const int j = c >> 1;
+                const int64_t page = j == 0 ? pg[0] : j == 1 ? pg[1] : j == 2 ? pg[2] : pg[3];
+                const half_t* src = a.v_pool + block_base(a.addr, page) +
+                                    (int64_t)(g * kHeadDim + d) * kPageTokens + 8 * (c & 1);
+                lds_dma16(src, lds_offset(&s_v[buf][d0][0]));
+            }
         };
 
         bool in_run[QB];
@@ -227,20 +275,33 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
             in_run[qb] = my_row[qb] >= 0 && ri >= r0 && ri < r1;
         }
 
-        load_tile(0);
-        store_tile(0);
-        __syncthreads();
-        for (int kt = 0; kt < n_tiles; ++kt) {
-            const int buf = kt & 1;
-            if (kt + 1 < n_tiles) load_tile(kt + 1);
-            const int kbase = kt * kKeyTile;
-            if (wave_last >= kbase) {
-                // S^T blocks: st[qb][kb][r] = S^T[kbase + 16*kb + 4*grp + r][q = col]
-                float sv[QB][4][4];
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb) {
-                    const half8_t a0 = *reinterpret_cast<const half8_t*>(&s_k[buf][16 * kb + col][8 * grp]);
-                    const half8_t a1 = *reinterpret_cast<const half8_t*>(&s_k[buf][16 * kb + col][32 + 8 * grp]);
+        for (int t = 0; t < kBufs - 1; ++t)
+            if (t < n_tiles) issue(t);
+        for (int kt = 0; kt < n_tiles; ++kt) {
+            // Wait for this thread's loads of tile kt (later tiles may stay in flight) and
+            // for its LDS reads of tile kt - 1; the barrier then makes every wave's loads
+            // of tile kt visible and frees tile kt - 1's buffer for tile kt + kBufs - 1.
+            const int ahead = min(kBufs - 2, n_tiles - 1 - kt);
+            if (ahead >= 2) __builtin_amdgcn_s_waitcnt(kWaitVm4Lgkm0);  // 2 loads per tile
+            else if (ahead == 1) __builtin_amdgcn_s_waitcnt(kWaitVm2Lgkm0);
+            else __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+            __builtin_amdgcn_s_barrier();
+            if (kt + kBufs - 1 < n_tiles) issue(kt + kBufs - 1);
+            const int buf = kt % kBufs;
+            const int kbase = kt * kKeyTile;
+            if (wave_last >= kbase + 32 * kh) {
+                // S^T blocks of this wave's key half: st[qb][kk][r] = S^T[key][q = col],
+                // key = kbase + 16 * (2 * kh + kk) + 4 * grp + r
+                float sv[QB][2][4];
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int kb = 2 * kh + kk;
+                    const int row = 16 * kb + col;
+                    const half8_t a0 = *reinterpret_cast<const half8_t*>(
+                        &s_k[buf][row][8 * (grp ^ (row & 7))]);
+                    const half8_t a1 = *reinterpret_cast<const half8_t*>(
+                        &s_k[buf][row][8 * ((4 + grp) ^ (row & 7))]);
 #pragma unroll
                     for (int qb = 0; qb < QB; ++qb) {
                         float4_t st = {0.f, 0.f, 0.f, 0.f};
@@ -253,19 +314,19 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             const int key = kbase + 16 * kb + 4 * grp + r;
-                            sv[qb][kb][r] = (in_run[qb] && key <= my_pos[qb]) ? st[r] * a.scale_log2 : -INFINITY;
+                            sv[qb][kk][r] = (in_run[qb] && key <= my_pos[qb]) ? st[r] * a.scale_log2 : -INFINITY;
                         }
                     }
                 }
-                half8_t pb[QB][2];
-                half8_t pl[QB][2];  // P = hi + lo: the product keeps ~22 bits of P
+                half8_t pb[QB];
+                half8_t pl[QB];  // P = hi + lo: the product keeps ~22 bits of P
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) {
                     float tm = -INFINITY;
 #pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
+                    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) tm = fmaxf(tm, sv[qb][kb][r]);
+                        for (int r = 0; r < 4; ++r) tm = fmaxf(tm, sv[qb][kk][r]);
                     tm = fmaxf(tm, __shfl_xor(tm, 16));
                     tm = fmaxf(tm, __shfl_xor(tm, 32));
                     const float mn = fmaxf(m[qb], tm);
@@ -273,13 +334,13 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
                     const float alpha = fast_exp2(m[qb] - mu);
                     float ps = 0.0f;
 #pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
+                    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const float pf = fast_exp2(sv[qb][kb][r] - mu);
+                            const float pf = fast_exp2(sv[qb][kk][r] - mu);
                             const half_t ph = (half_t)pf;
-                            pb[qb][kb >> 1][(kb & 1) * 4 + r] = ph;
-                            pl[qb][kb >> 1][(kb & 1) * 4 + r] = (half_t)(pf - (float)ph);
+                            pb[qb][kk * 4 + r] = ph;
+                            pl[qb][kk * 4 + r] = (half_t)(pf - (float)ph);
                             ps += pf;
                         }
                     l[qb] = l[qb] * alpha + ps;
@@ -287,27 +348,80 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
                     for (int db = 0; db < 4; ++db) acc[qb][db] = acc[qb][db] * alpha;
                 }
-                // O^T[dim][q] += V^T[dim][32 keys] . P^T[32 keys][q], key pairs (kb 0,1), (2,3)
+                // O^T[dim][q] += V^T[dim][32 keys] . P^T[32 keys][q] over this wave's keys.
+                // Keys past the run's end may hold anything (even NaN): zero them.
+                const bool tail = kbase + kKeyTile > hist_end;
+                const int ks = kh;
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
+                    const int d = 16 * db + col;
+                    {
+                        const int c1 = 4 * ks + (grp >> 1);
+                        const int o = 4 * (grp & 1);
+                        half4_t v0 = *reinterpret_cast<const half4_t*>(
+                            &s_v[buf][d][8 * (c1 ^ (d & 7)) + o]);
+                        half4_t v1 = *reinterpret_cast<const half4_t*>(
+                            &s_v[buf][d][8 * ((c1 + 2) ^ (d & 7)) + o]);
+                        if (tail) {
 #pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) {
-                        const half_t* vrow = &s_v[buf][16 * db + col][0];
-                        const half4_t v0 = *reinterpret_cast<const half4_t*>(vrow + 32 * ks + 4 * grp);
-                        const half4_t v1 = *reinterpret_cast<const half4_t*>(vrow + 32 * ks + 16 + 4 * grp);
+                            for (int r = 0; r < 4; ++r) {
+                                if (kbase + 32 * ks + 4 * grp + r >= hist_end) v0[r] = (half_t)0.0f;
+                                if (kbase + 32 * ks + 16 + 4 * grp + r >= hist_end) v1[r] = (half_t)0.0f;
+                            }
+                        }
                         const half8_t va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
 #pragma unroll
                         for (int qb = 0; qb < QB; ++qb) {
-                            acc[qb][db] = mfma_16x16x32(va, pb[qb][ks], acc[qb][db]);
-                            acc[qb][db] = mfma_16x16x32(va, pl[qb][ks], acc[qb][db]);
+                            acc[qb][db] = mfma_16x16x32(va, pb[qb], acc[qb][db]);
+                            acc[qb][db] = mfma_16x16x32(va, pl[qb], acc[qb][db]);
                         }
                     }
                 }
             }
-            if (kt + 1 < n_tiles) store_tile(buf ^ 1);
-            __syncthreads();
         }
+        // every wave's reads of the last buffers are done before the next run reuses them
+        __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+        __builtin_amdgcn_s_barrier();
+        if (a.mode != kOwners) break;  // a single run
         r0 = r1;
+    }
+
+    // ---- merge the key halves: waves 4..7 hand (m, l, acc) to their partner through
+    // the (now idle) ring; per lane, both hold the same query column and dims. Lane-major
+    // layout keeps the exchange free of bank conflicts: acc (4 x QB x 16 x 64 floats,
+    // 32 KiB at QB = 2) in the K ring, m and l in the V ring.
+    static_assert(4 * QB * 16 * 64 * sizeof(float) <= sizeof(s_k), "merge buffer");
+    float* s_macc = reinterpret_cast<float*>(&s_k[0][0][0]);
+    float* s_ml = reinterpret_cast<float*>(&s_v[0][0][0]);
+    if (kh == 1) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            float* p = s_macc + (slot * QB + qb) * 16 * 64 + lane;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) p[(4 * db + r) * 64] = acc[qb][db][r];
+            float* q = s_ml + (slot * QB + qb) * 2 * 64 + lane;
+            q[0] = m[qb];
+            q[64] = l[qb];
+        }
+    }
+    __syncthreads();
+    if (kh == 1) return;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const float* p = s_macc + (slot * QB + qb) * 16 * 64 + lane;
+        const float* q = s_ml + (slot * QB + qb) * 2 * 64 + lane;
+        const float m1 = q[0], l1 = q[64];
+        const float mx = fmaxf(m[qb], m1);
+        const float mu = mx == -INFINITY ? 0.0f : mx;
+        const float w0 = fast_exp2(m[qb] - mu), w1 = fast_exp2(m1 - mu);
+        l[qb] = l[qb] * w0 + l1 * w1;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[qb][db][r] = acc[qb][db][r] * w0 + p[(4 * db + r) * 64] * w1;
     }
 
     // ---- normalise and write: lane (q = col, grp) holds dims 16*db + 4*grp .. +3
@@ -336,8 +450,12 @@ int heads_per_wg(int n_rep) { return (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2
 
 template <int HPW, int QB>
 void launch_hq(const PrefillArgs& a, bool q_f32, dim3 grid, hipStream_t stream) {
-    if (q_f32) hipLaunchKernelGGL((prefill_kernel<HPW, QB, true>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((prefill_kernel<HPW, QB, false>), grid, dim3(256), 0, stream, a);
+    if (q_f32)
+        hipLaunchKernelGGL((prefill_kernel<HPW, QB, true>), grid, dim3(kThreads), 0, stream, a,
+                           a.tables);
+    else
+        hipLaunchKernelGGL((prefill_kernel<HPW, QB, false>), grid, dim3(kThreads), 0, stream, a,
+                           a.tables);
 }
 
 // tile_rows_total: rows spanned by grid.y (max_chunk or rows); z: requests.

@@ -74,6 +74,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // another XCD's stale L2 line).
 constexpr int kPolicyCoherent = 16;
 
+// Direct-to-LDS 16-byte load: every lane of the wave moves 16 bytes from `src` to
+// LDS byte offset lds_base + 16 * lane (global_load_lds_dwordx4, M0 = lds_base, which
+// must be wave-uniform). Issued through inline asm so the compiler does not track the
+// LDS write: the caller orders it with its own s_waitcnt vmcnt + s_barrier, which lets
+// several tiles stay in flight while earlier ones are read (the compiler would otherwise
+// wait for every outstanding load before each LDS read).
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(lds_base)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
+}
+
 // log2(e): softmax is evaluated as 2^(s * scale * log2e - m) with m in the same units.
 constexpr float kLog2e = 1.4426950408889634f;
 

@@ -15,19 +15,20 @@
 //
 // Workgroup = 8 waves: 4 slots = (4 / HPW) row slices x HPW query heads of one GQA
 // group, so the HPW heads that share a kv head share every K/V tile staged in LDS, and
-// two waves per slot that split each 64-key tile into halves (their online-softmax
-// states merge at the end). A slot owns QB blocks of 16 query rows for one head. Per
-// 64-key tile and 16-row block, each wave of the pair computes its 32 keys:
-//   S^T[32 key x 16 q] = K[32 x 64] . Q^T        4x mfma_f32_16x16x32_f16
-//   online softmax per query column (base 2), causal mask by absolute position
-//   O^T[64 dim x 16 q] += V^T[64 x 32 key] . P^T 8x mfma_f32_16x16x32_f16, with P
+// two waves per slot that take alternate 64-key tiles (their online-softmax states merge
+// at the end). A slot owns QB blocks of 16 query rows for one head. Per 64-key tile and
+// 16-row block, the wave that owns the tile computes:
+//   S^T[64 key x 16 q] = K[64 x 64] . Q^T        8x mfma_f32_16x16x32_f16
+//   online softmax per query column (base 2), causal mask by absolute position (skipped
+//     for tiles wholly below the diagonal), lazy rescaling of the accumulators
+//   O^T[64 dim x 16 q] += V^T[64 x 64 key] . P^T 16x mfma_f32_16x16x32_f16, with P
 //     split into fp16 hi + lo parts so the product keeps ~22 bits of P (an f32 query
 //     is split the same way for QK^T)
 // The transposed V pages are copied into LDS as-is (no transpose on the way), and the
 // P^T operand is exactly the register layout the S^T product leaves behind.
-// Tiles stream into a ring of kBufs LDS buffers with direct-to-LDS loads
-// (global_load_lds_dwordx4, no register staging), kBufs - 1 tiles ahead of the one being
-// computed, so HBM latency overlaps the MFMA work; 16-byte chunks of each 128-byte LDS
+// Tiles stream into a ring of KB LDS buffers with direct-to-LDS loads
+// (global_load_lds_dwordx4, no register staging), a pair of tiles or two ahead of the
+// pair being computed, so HBM latency overlaps the MFMA work; 16-byte chunks of each 128-byte LDS
 // row are XOR-swizzled by row so the operand reads stay (almost) free of bank conflicts.
 // A wave skips tiles that lie wholly above the causal diagonal of its rows (the
 // workgroup still loads up to its last row).
@@ -46,13 +47,43 @@ namespace {
 enum RowMode { kSegments = 0, kOwners = 1, kParams = 2, kContig = 3 };
 
 constexpr int kKeyTile = 64;
-constexpr int kBufs = 4;  // LDS ring depth: tiles kt+1 .. kt+3 load while tile kt computes
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0], expcnt[6:4] = 7 (no wait), lgkmcnt[11:8])
 constexpr int kWaitVm0Lgkm0 = 0x0070;
-constexpr int kWaitVm2Lgkm0 = 0x0072;
 constexpr int kWaitVm4Lgkm0 = 0x0074;
-constexpr int kThreads = 512;  // 8 waves: 4 row/head slots x 2 key halves
+constexpr int kWaitVm8Lgkm0 = 0x0078;
+constexpr int kThreads = 512;  // 8 waves: 4 row/head slots x 2 tile parities
+constexpr float kLazyLog2 = 8.0f;  // running-max slack (log2 units) before a rescale
+
+// Max over lanes L and L ^ 16 (resp. L ^ 32): two steps reduce the 4 lane groups of a
+// column. v_permlane16_swap a, b swaps the odd 16-lane rows of a with the even rows of b
+// (permlane32_swap: the upper half of a with the lower half of b), so from a = b = v each
+// lane ends with v[L] in one operand and v[L ^ 16] (resp. v[L ^ 32]) in the other. It is
+// written as asm because this compiler's builtin returns the first operand in both halves
+// of its result. s_nop 1 covers the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ float max_xor16(float v) {
+    float a = v, b = v;
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float max_xor32(float v) {
+    float a = v, b = v;
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return fmaxf(a, b);
+}
+
+// P = hi + lo in fp16: hi truncates (v_cvt_pkrtz), lo = RNE(p - hi), which is exact to
+// about 2^-22 relative.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ half4_t split_hi(const float (&p)[4]) {
+    const half2_t a = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(p[0], p[1]));
+    const half2_t b = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(p[2], p[3]));
+    return half4_t{a[0], a[1], b[0], b[1]};
+}
+__device__ __forceinline__ half4_t split_lo(const float (&p)[4], half4_t h) {
+    return half4_t{(half_t)(p[0] - (float)h[0]), (half_t)(p[1] - (float)h[1]),
+                   (half_t)(p[2] - (float)h[2]), (half_t)(p[3] - (float)h[3])};
+}
 
 struct PrefillArgs {
     const void* q;
@@ -79,7 +110,8 @@ struct PrefillArgs {
 
 // `tables` is passed on its own, read-only and unaliased, so the page-id loads of the
 // tile loop compile to scalar loads (lgkmcnt) that never wait on the in-flight tiles.
-template <int HPW, int QB, bool QF32>
+// KB: LDS ring depth in key tiles (4 or 6): KB / 2 - 1 pairs of tiles load ahead.
+template <int HPW, int QB, bool QF32, int KB>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                                                       const int32_t* __restrict__ tables) {
     constexpr int RS = 4 / HPW;          // row slices per workgroup
@@ -87,8 +119,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
     constexpr int R = RS * WROWS;        // rows per workgroup
 
     // ring of key tiles, 128-byte rows whose 16-byte chunks are XOR-swizzled by row
-    __shared__ half_t s_k[kBufs][kKeyTile][64];   // [buf][key][dim]
-    __shared__ half_t s_v[kBufs][64][kKeyTile];   // [buf][dim][key]
+    __shared__ half_t s_k[KB][kKeyTile][64];   // [buf][key][dim]
+    __shared__ half_t s_v[KB][64][kKeyTile];   // [buf][dim][key]
     __shared__ int s_owner[R];
     __shared__ int s_pos[R];
     __shared__ int s_row[R];
@@ -232,10 +264,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
         const int n_tiles = (hist_end + kKeyTile - 1) / kKeyTile;
         const int last_page = (hist_end - 1) >> kPageShift;
 
-        // Issue tile t into ring buffer t % kBufs: 4 direct-to-LDS loads per thread.
+        // Issue tile t into ring buffer t % KB: 2 direct-to-LDS loads per thread.
         // Page ids past the run's last page are clamped to it (in bounds; masked later).
         auto issue = [&](int t) {
-            const int buf = t % kBufs;
+            const int buf = t % KB;
             int64_t pg[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -275,28 +307,37 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
             in_run[qb] = my_row[qb] >= 0 && ri >= r0 && ri < r1;
         }
 
+        // Tiles go in pairs: wave w computes tile 2i + (w >> 2) of pair i, so each wave of
+        // a slot runs half of the tiles and the two halves' softmax chains overlap.
+        constexpr int PS = KB / 2;  // pair slots in the ring
+        const int n_pairs = (n_tiles + 1) / 2;
 #pragma unroll
-        for (int t = 0; t < kBufs - 1; ++t)
-            if (t < n_tiles) issue(t);
-        for (int kt = 0; kt < n_tiles; ++kt) {
-            // Wait for this thread's loads of tile kt (later tiles may stay in flight) and
-            // for its LDS reads of tile kt - 1; the barrier then makes every wave's loads
-            // of tile kt visible and frees tile kt - 1's buffer for tile kt + kBufs - 1.
-            const int ahead = min(kBufs - 2, n_tiles - 1 - kt);
-            if (ahead >= 2) __builtin_amdgcn_s_waitcnt(kWaitVm4Lgkm0);  // 2 loads per tile
-            else if (ahead == 1) __builtin_amdgcn_s_waitcnt(kWaitVm2Lgkm0);
+        for (int p = 0; p < PS - 1; ++p)
+            if (p < n_pairs) {
+                issue(2 * p);
+                issue(2 * p + 1);  // past n_tiles: a clamped, in-bounds load nobody reads
+            }
+        for (int ip = 0; ip < n_pairs; ++ip) {
+            // Wait for this thread's loads of pair ip (later pairs may stay in flight, 4
+            // loads each) and its LDS reads of pair ip - 1; the barrier then makes every
+            // wave's loads visible and frees pair ip - 1's buffers for pair ip + PS - 1.
+            const int ahead = min(PS - 2, n_pairs - 1 - ip);
+            if (ahead >= 2) __builtin_amdgcn_s_waitcnt(kWaitVm8Lgkm0);
+            else if (ahead == 1) __builtin_amdgcn_s_waitcnt(kWaitVm4Lgkm0);
             else __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
             __builtin_amdgcn_s_barrier();
-            if (kt + kBufs - 1 < n_tiles) issue(kt + kBufs - 1);
-            const int buf = kt % kBufs;
-            const int kbase = kt * kKeyTile;
-            if (wave_last >= kbase + 32 * kh) {
-                // S^T blocks of this wave's key half: st[qb][kk][r] = S^T[key][q = col],
-                // key = kbase + 16 * (2 * kh + kk) + 4 * grp + r
-                float sv[QB][2][4];
+            if (ip + PS - 1 < n_pairs) {
+                issue(2 * (ip + PS - 1));
+                issue(2 * (ip + PS - 1) + 1);
+            }
+            const int t = 2 * ip + kh;
+            const int kbase = t * kKeyTile;
+            if (t < n_tiles && wave_last >= kbase) {
+                const int buf = t % KB;
+                // S^T blocks: st[qb][kb] = S^T[kbase + 16*kb + 4*grp + r][q = col]
+                float4_t st[QB][4];
 #pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    const int kb = 2 * kh + kk;
+                for (int kb = 0; kb < 4; ++kb) {
                     const int row = 16 * kb + col;
                     const half8_t a0 = *reinterpret_cast<const half8_t*>(
                         &s_k[buf][row][8 * (grp ^ (row & 7))]);
@@ -304,58 +345,85 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                         &s_k[buf][row][8 * ((4 + grp) ^ (row & 7))]);
 #pragma unroll
                     for (int qb = 0; qb < QB; ++qb) {
-                        float4_t st = {0.f, 0.f, 0.f, 0.f};
-                        st = mfma_16x16x32(a0, qh[qb][0], st);
-                        st = mfma_16x16x32(a1, qh[qb][1], st);
+                        float4_t c = {0.f, 0.f, 0.f, 0.f};
+                        c = mfma_16x16x32(a0, qh[qb][0], c);
+                        c = mfma_16x16x32(a1, qh[qb][1], c);
                         if constexpr (QF32) {
-                            st = mfma_16x16x32(a0, ql[qb][0], st);
-                            st = mfma_16x16x32(a1, ql[qb][1], st);
+                            c = mfma_16x16x32(a0, ql[qb][0], c);
+                            c = mfma_16x16x32(a1, ql[qb][1], c);
                         }
+                        st[qb][kb] = c;
+                    }
+                }
+                // Scale to base 2 and mask; a tile that every row of the wave sees whole
+                // (below the diagonal, all rows in the run) needs no mask.
+                bool lane_full = true;
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb)
+                    lane_full = lane_full && in_run[qb] && my_pos[qb] >= kbase + kKeyTile - 1;
+                const bool full = __all(lane_full);
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             const int key = kbase + 16 * kb + 4 * grp + r;
-                            sv[qb][kk][r] = (in_run[qb] && key <= my_pos[qb]) ? st[r] * a.scale_log2 : -INFINITY;
+                            const float x = st[qb][kb][r] * a.scale_log2;
+                            st[qb][kb][r] = (full || (in_run[qb] && key <= my_pos[qb])) ? x : -INFINITY;
                         }
-                    }
-                }
-                half8_t pb[QB];
-                half8_t pl[QB];  // P = hi + lo: the product keeps ~22 bits of P
+                half8_t pb[QB][2];
+                half8_t pl[QB][2];  // P = hi + lo: the product keeps ~22 bits of P
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) {
                     float tm = -INFINITY;
 #pragma unroll
-                    for (int kk = 0; kk < 2; ++kk)
+                    for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) tm = fmaxf(tm, sv[qb][kk][r]);
-                    tm = fmaxf(tm, __shfl_xor(tm, 16));
-                    tm = fmaxf(tm, __shfl_xor(tm, 32));
-                    const float mn = fmaxf(m[qb], tm);
-                    const float mu = (mn == -INFINITY) ? 0.0f : mn;
-                    const float alpha = fast_exp2(m[qb] - mu);
+                        for (int r = 0; r < 4; ++r) tm = fmaxf(tm, st[qb][kb][r]);
+                    tm = max_xor32(max_xor16(tm));
+                    // Lazy rescale: the running max moves only when the tile's max exceeds
+                    // it by more than kLazyLog2, so P stays <= 2^kLazyLog2 and most tiles
+                    // skip rescaling the accumulators. out = acc / l is unchanged.
+                    const bool grow = tm > m[qb] + kLazyLog2;
+                    if (__any(grow)) {
+                        // alpha = 1 where the max is kept (also -inf, where m - m is NaN);
+                        // 0 where it grows from -inf
+                        const float alpha = grow ? fast_exp2(m[qb] - tm) : 1.0f;
+                        const float mn = grow ? tm : m[qb];
+                        l[qb] *= alpha;
+#pragma unroll
+                        for (int db = 0; db < 4; ++db) acc[qb][db] = acc[qb][db] * alpha;
+                        m[qb] = mn;
+                    }
+                    const float mu = (m[qb] == -INFINITY) ? 0.0f : m[qb];
                     float ps = 0.0f;
 #pragma unroll
-                    for (int kk = 0; kk < 2; ++kk)
+                    for (int kb = 0; kb < 4; ++kb) {
+                        float pf[4];
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const float pf = fast_exp2(sv[qb][kk][r] - mu);
-                            const half_t ph = (half_t)pf;
-                            pb[qb][kk * 4 + r] = ph;
-                            pl[qb][kk * 4 + r] = (half_t)(pf - (float)ph);
-                            ps += pf;
+                            pf[r] = fast_exp2(st[qb][kb][r] - mu);
+                            ps += pf[r];
                         }
-                    l[qb] = l[qb] * alpha + ps;
-                    m[qb] = mn;
+                        const half4_t h = split_hi(pf);
+                        const half4_t lo = split_lo(pf, h);
 #pragma unroll
-                    for (int db = 0; db < 4; ++db) acc[qb][db] = acc[qb][db] * alpha;
+                        for (int r = 0; r < 4; ++r) {
+                            pb[qb][kb >> 1][(kb & 1) * 4 + r] = h[r];
+                            pl[qb][kb >> 1][(kb & 1) * 4 + r] = lo[r];
+                        }
+                    }
+                    l[qb] += ps;
                 }
-                // O^T[dim][q] += V^T[dim][32 keys] . P^T[32 keys][q] over this wave's keys.
+                // O^T[dim][q] += V^T[dim][32 keys] . P^T[32 keys][q], key halves ks = 0, 1.
                 // Keys past the run's end may hold anything (even NaN): zero them.
                 const bool tail = kbase + kKeyTile > hist_end;
-                const int ks = kh;
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
                     const int d = 16 * db + col;
-                    {
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
                         const int c1 = 4 * ks + (grp >> 1);
                         const int o = 4 * (grp & 1);
                         half4_t v0 = *reinterpret_cast<const half4_t*>(
@@ -372,8 +440,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                         const half8_t va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
 #pragma unroll
                         for (int qb = 0; qb < QB; ++qb) {
-                            acc[qb][db] = mfma_16x16x32(va, pb[qb], acc[qb][db]);
-                            acc[qb][db] = mfma_16x16x32(va, pl[qb], acc[qb][db]);
+                            acc[qb][db] = mfma_16x16x32(va, pb[qb][ks], acc[qb][db]);
+                            acc[qb][db] = mfma_16x16x32(va, pl[qb][ks], acc[qb][db]);
                         }
                     }
                 }
@@ -448,14 +516,20 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
 
 int heads_per_wg(int n_rep) { return (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1; }
 
-template <int HPW, int QB>
-void launch_hq(const PrefillArgs& a, bool q_f32, dim3 grid, hipStream_t stream) {
-    if (q_f32)
-        hipLaunchKernelGGL((prefill_kernel<HPW, QB, true>), grid, dim3(kThreads), 0, stream, a,
+template <int HPW, int QB, bool QF32>
+void launch_kb(const PrefillArgs& a, int kb, dim3 grid, hipStream_t stream) {
+    if (kb == 6)
+        hipLaunchKernelGGL((prefill_kernel<HPW, QB, QF32, 6>), grid, dim3(kThreads), 0, stream, a,
                            a.tables);
     else
-        hipLaunchKernelGGL((prefill_kernel<HPW, QB, false>), grid, dim3(kThreads), 0, stream, a,
+        hipLaunchKernelGGL((prefill_kernel<HPW, QB, QF32, 4>), grid, dim3(kThreads), 0, stream, a,
                            a.tables);
+}
+
+template <int HPW, int QB>
+void launch_hq(const PrefillArgs& a, bool q_f32, int kb, dim3 grid, hipStream_t stream) {
+    if (q_f32) launch_kb<HPW, QB, true>(a, kb, grid, stream);
+    else launch_kb<HPW, QB, false>(a, kb, grid, stream);
 }
 
 // tile_rows_total: rows spanned by grid.y (max_chunk or rows); z: requests.
@@ -471,19 +545,26 @@ int launch_prefill(const PrefillArgs& a, int64_t tile_rows_total, int64_t z, boo
         if (v == 1 || v == 2) qb = v;
     }
     const int64_t gy = tiles(qb);
+    // A grid that fits the chip at one workgroup per CU affords the deeper ring (96 KiB
+    // of LDS); larger grids keep two workgroups per CU.
+    int kb = (gx * gy * z <= 256) ? 6 : 4;
+    if (const char* env = std::getenv("CRUCIBLE_PREFILL_BUFS")) {
+        const int v = std::atoi(env);
+        if (v == 4 || v == 6) kb = v;
+    }
     CRUCIBLE_CHECK(gx <= INT32_MAX && gy <= 65535 && z <= 65535, CRUCIBLE_ERR_INVALID,
                    "%s: grid (%lld, %lld, %lld) too large", what, (long long)gx, (long long)gy,
                    (long long)z);
     const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)z);
     if (hpw == 4) {
-        if (qb == 2) launch_hq<4, 2>(a, q_f32, grid, stream);
-        else launch_hq<4, 1>(a, q_f32, grid, stream);
+        if (qb == 2) launch_hq<4, 2>(a, q_f32, kb, grid, stream);
+        else launch_hq<4, 1>(a, q_f32, kb, grid, stream);
     } else if (hpw == 2) {
-        if (qb == 2) launch_hq<2, 2>(a, q_f32, grid, stream);
-        else launch_hq<2, 1>(a, q_f32, grid, stream);
+        if (qb == 2) launch_hq<2, 2>(a, q_f32, kb, grid, stream);
+        else launch_hq<2, 1>(a, q_f32, kb, grid, stream);
     } else {
-        if (qb == 2) launch_hq<1, 2>(a, q_f32, grid, stream);
-        else launch_hq<1, 1>(a, q_f32, grid, stream);
+        if (qb == 2) launch_hq<1, 2>(a, q_f32, kb, grid, stream);
+        else launch_hq<1, 1>(a, q_f32, kb, grid, stream);
     }
     return fail_launch(what);
 }

@@ -20,7 +20,7 @@ KAT_PATH = os.path.join(BUILD, "paging_kat")
 
 ARCH = "gfx950"
 DEVICE_SOURCES = ["kv_append.hip", "attn_decode.hip", "attn_prefill.hip", "argmax.hip",
-                  "abi_common.cpp", "paging.cpp"]
+                  "model_ops.hip", "abi_common.cpp", "paging.cpp"]
 # Packed-FP32 instructions stay off: hipcc would otherwise form v_pk_* f32 ops on its own.
 HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

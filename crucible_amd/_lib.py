@@ -41,6 +41,12 @@ SIGNATURES = {
     "crucible_attention_prefill_tiled": ([_P, _I, _P, _P, _P, _P, _P, _I, _P, _P] + [_I64] * 9 + [_I, _I64, _P], _I),
     "crucible_attention_prefill": ([_P, _I, _P, _P, _P, _I] + [_I64] * 8 + [_P], _I),
     "crucible_argmax_rows": ([_P, _P, _I64, _I64, _P], _I),
+    "crucible_linear_f64acc": ([_P, _I64, _P, ctypes.c_float, _P, _I64, _I64, _P, _P, _I64, _I64,
+                                _P], _I),
+    "crucible_linear_swiglu_f64acc": ([_P, _I64, _P, ctypes.c_float, _P, _P, _I64, _I64, _P,
+                                       _I64, _I64, _P], _I),
+    "crucible_rmsnorm_rows": ([_P, _I64, _P, ctypes.c_float, _P, _I64, _I64, _I64, _P], _I),
+    "crucible_rope_split_qkv": ([_P, _I64, _P, _P, _P, _P, _P, _P] + [_I64] * 5 + [_P], _I),
     "crucible_segments_from_cu_seqlens": ([_P, _I64, _P, _P], _I64),
     "crucible_page_pool_new": ([_I64, _I64, _I64], _P),
     "crucible_page_pool_free": ([_P], None),

@@ -1,0 +1,371 @@
+// Decode-step kernels around the attention path: the batched projections, RMSNorm and
+// RoPE of the reference decoder (engine/src/model.rs:183-299, forward_cached), with the
+// reference CPU arithmetic:
+//   matvec (ops.rs:17-32): f32 operands, every product and the sum in f64, one rounding
+//     to f32 at the end. The products and sums run here on the f64 MFMA
+//     (v_mfma_f64_16x16x4f64) in another order; the sum stays f64, so the rounded f32
+//     result is the reference's unless the two f64 sums straddle an f32 rounding
+//     boundary.
+//   rmsnorm (ops.rs:39-52): f64 mean of squares, scale = 1 / sqrt(mean + eps) in f64,
+//     h = f32(f64(x) * scale) * w.
+//   silu (ops.rs:83-85) on the gate, times up (model.rs:257-260).
+//   RoPE (ops.rs:94-136): element i pairs with i + 32: lo*c - hi*s, lo*s + hi*c.
+// These replace the batched GEMV and the row kernels of the reference's GPU decode step
+// (kernels.cu:1539-1607 gemv_batch, :968-1047 rmsnorm/rope/swiglu batch kernels), which
+// accumulate in f32; keeping the CPU reference's f64 accumulation is what makes greedy
+// decoding token-identical to it.
+//
+// Floating-point contraction is off in this file, so each f32 operation rounds on its own
+// as the reference's do.
+#include "common.hpp"
+
+#include <cmath>
+
+#pragma clang fp contract(off)
+
+namespace crucible {
+namespace {
+
+typedef double double4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kLinWaves = 8;               // the K range is split over the 8 waves
+constexpr int kLinThreads = 64 * kLinWaves;
+constexpr int kLinK = 32;                  // K per chunk: 8 per lane group, 8 MFMA steps
+
+enum LinMode { kPlain = 0, kResidual = 1, kSwiGLU = 2 };
+
+__device__ __forceinline__ double4_t mfma_f64(double a, double b, double4_t c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+struct LinArgs {
+    const float* x;
+    int64_t ldx;
+    const float* norm_w;  // fused RMSNorm weight, or nullptr
+    double eps;
+    const half_t* w;      // [n_out][k_in]; the gate rows in SwiGLU mode
+    const half_t* w2;     // SwiGLU: the up rows
+    const float* resid;   // kResidual: out = resid + y
+    float* out;
+    int64_t ldo;
+    int rows;
+    int n_out;
+    int k_in;
+};
+
+template <int NB>
+struct Chunk {
+    float4_t x0, x1;
+    half8_t w[NB];
+};
+
+// out tile = 16 rows x (16 * NB) columns (kSwiGLU: 16 columns of gate and of up).
+//
+// f64 MFMA 16x16x4 operand layout: lane l supplies A[l & 15][kslot] and B[kslot][l & 15]
+// with kslot = l >> 4, and holds D[(l >> 4) + 4 r][l & 15], r = 0..3. Lane group g
+// (= l >> 4) owns k = kbeg + k0 + 8 g + j of each 32-wide chunk at MFMA step j, for A
+// (the activations) and B (the weights) alike.
+template <bool NORM, int MODE, int NB>
+__global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
+    __shared__ double s_scale[16];
+    __shared__ double s_red[kLinWaves][NB][4][64];  // [wave][block][r][lane]
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int col = lane & 15;
+    const int g = lane >> 4;
+    const int m0 = blockIdx.y * 16;
+    const int n0 = blockIdx.x * 16 * (MODE == kSwiGLU ? 1 : NB);
+
+    if constexpr (NORM) {
+        // sum of squares of row tid >> 5 over k = (tid & 31) + 32 i, in f64
+        const int r = tid >> 5, t = tid & 31;
+        double ss = 0.0;
+        if (m0 + r < a.rows) {
+            const float* xr = a.x + (int64_t)(m0 + r) * a.ldx;
+            for (int k = t; k < a.k_in; k += 32) {
+                const double v = (double)xr[k];
+                ss += v * v;
+            }
+        }
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 32);
+        if (t == 0) s_scale[r] = 1.0 / sqrt(ss / (double)a.k_in + a.eps);
+        __syncthreads();
+    }
+
+    // wave w takes chunks [w * nc / 8, (w + 1) * nc / 8) of the nc = k_in / 32 chunks
+    const int nc = a.k_in / kLinK;
+    const int c0 = wave * nc / kLinWaves, c1 = (wave + 1) * nc / kLinWaves;
+    const int kw = (c1 - c0) * kLinK;
+    const int kbeg = c0 * kLinK + 8 * g;
+    const int row = m0 + col;
+    const bool row_ok = row < a.rows;
+    const float* xp = a.x + (int64_t)(row_ok ? row : 0) * a.ldx + kbeg;
+    const float* nwp = NORM ? a.norm_w + kbeg : nullptr;
+    const double scale = NORM ? s_scale[col] : 1.0;
+    const half_t* wp[NB];
+    bool n_ok[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const half_t* base = (MODE == kSwiGLU && j == 1) ? a.w2 : a.w;
+        const int n = n0 + col + (MODE == kSwiGLU ? 0 : 16 * j);
+        n_ok[j] = n < a.n_out;
+        wp[j] = base + (int64_t)(n_ok[j] ? n : 0) * a.k_in + kbeg;
+    }
+
+    auto load = [&](int k0) {
+        Chunk<NB> c;
+        c.x0 = *reinterpret_cast<const float4_t*>(xp + k0);
+        c.x1 = *reinterpret_cast<const float4_t*>(xp + k0 + 4);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) c.w[j] = *reinterpret_cast<const half8_t*>(wp[j] + k0);
+        return c;
+    };
+
+    double4_t acc[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[j] = double4_t{0.0, 0.0, 0.0, 0.0};
+
+    Chunk<NB> cur;
+    if (kw > 0) cur = load(0);
+    for (int k0 = 0; k0 < kw; k0 += kLinK) {
+        Chunk<NB> nxt = cur;
+        if (k0 + kLinK < kw) nxt = load(k0 + kLinK);
+        float xs[8] = {cur.x0[0], cur.x0[1], cur.x0[2], cur.x0[3],
+                       cur.x1[0], cur.x1[1], cur.x1[2], cur.x1[3]};
+        if constexpr (NORM) {
+            const float4_t w0 = *reinterpret_cast<const float4_t*>(nwp + k0);
+            const float4_t w1 = *reinterpret_cast<const float4_t*>(nwp + k0 + 4);
+            const float nw[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xs[i] = (float)((double)xs[i] * scale) * nw[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const double av = row_ok ? (double)xs[i] : 0.0;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const double bv = n_ok[j] ? (double)(float)cur.w[j][i] : 0.0;
+                acc[j] = mfma_f64(av, bv, acc[j]);
+            }
+        }
+        cur = nxt;
+    }
+
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_red[wave][j][r][lane] = acc[j][r];
+    __syncthreads();
+
+    // fixed summation order over the waves: the result does not depend on scheduling
+    constexpr int kOut = 256 * (MODE == kSwiGLU ? 1 : NB);
+    for (int o = tid; o < kOut; o += kLinThreads) {
+        const int blk = o >> 8, rem = o & 255;
+        const int l = rem & 63, r = rem >> 6;
+        const int orow = m0 + (l >> 4) + 4 * r;
+        const int on = n0 + 16 * blk + (l & 15);
+        if (orow >= a.rows || on >= a.n_out) continue;
+        double y = 0.0;
+#pragma unroll
+        for (int w = 0; w < kLinWaves; ++w) y += s_red[w][blk][r][l];
+        float* dst = a.out + (int64_t)orow * a.ldo + on;
+        if constexpr (MODE == kSwiGLU) {
+            double u = 0.0;
+#pragma unroll
+            for (int w = 0; w < kLinWaves; ++w) u += s_red[w][1][r][l];
+            const float gf = (float)y;
+            *dst = gf / (1.0f + expf(-gf)) * (float)u;
+        } else if constexpr (MODE == kResidual) {
+            *dst = a.resid[(int64_t)orow * a.ldo + on] + (float)y;
+        } else {
+            *dst = (float)y;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- RMSNorm rows
+
+constexpr int kNormThreads = 256;
+
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __restrict__ x,
+                                                               int64_t ldx,
+                                                               const float* __restrict__ w,
+                                                               double eps, float* out,
+                                                               int64_t ldo, int n) {
+    __shared__ double s_part[kNormThreads / 64];
+    const float* xr = x + (int64_t)blockIdx.x * ldx;
+    double ss = 0.0;
+    for (int k = threadIdx.x; k < n; k += kNormThreads) {
+        const double v = (double)xr[k];
+        ss += v * v;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int i = 0; i < kNormThreads / 64; ++i) tot += s_part[i];
+    const double scale = 1.0 / sqrt(tot / (double)n + eps);
+    float* orow = out + (int64_t)blockIdx.x * ldo;
+    for (int k = threadIdx.x; k < n; k += kNormThreads)
+        orow[k] = (float)((double)xr[k] * scale) * w[k];
+}
+
+// ---------------------------------------------------------------- RoPE + split
+
+// One thread per (row, head, i < 32) of the fused [q | k | v] row: q and k heads rotate,
+// v heads copy. A position outside the tables yields NaN rows (no out-of-range read).
+__global__ void rope_split_kernel(const float* __restrict__ qkv, int64_t ld, float* q,
+                                  float* k, float* v, const float* __restrict__ cos_t,
+                                  const float* __restrict__ sin_t,
+                                  const int32_t* __restrict__ positions, int rows, int n_head,
+                                  int n_kv_head, int max_pos) {
+    const int heads = n_head + 2 * n_kv_head;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)rows * heads * 32) return;
+    const int i = (int)(idx & 31);
+    const int head = (int)((idx >> 5) % heads);
+    const int row = (int)((idx >> 5) / heads);
+    const float* src = qkv + (int64_t)row * ld + head * 64;
+    const float lo = src[i], hi = src[i + 32];
+    float* dst;
+    if (head < n_head) dst = q + ((int64_t)row * n_head + head) * 64;
+    else if (head < n_head + n_kv_head) dst = k + ((int64_t)row * n_kv_head + head - n_head) * 64;
+    else dst = v + ((int64_t)row * n_kv_head + head - n_head - n_kv_head) * 64;
+    if (head >= n_head + n_kv_head) {
+        dst[i] = lo;
+        dst[i + 32] = hi;
+        return;
+    }
+    const int pos = positions[row];
+    if (pos < 0 || pos >= max_pos) {
+        dst[i] = dst[i + 32] = __builtin_nanf("");
+        return;
+    }
+    const float c = cos_t[(int64_t)pos * 32 + i];
+    const float s = sin_t[(int64_t)pos * 32 + i];
+    dst[i] = lo * c - hi * s;
+    dst[i + 32] = lo * s + hi * c;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+template <bool NORM, int MODE, int NB>
+void launch_linear(const LinArgs& a, hipStream_t stream) {
+    const int cols = 16 * (MODE == kSwiGLU ? 1 : NB);
+    const dim3 grid((unsigned)((a.n_out + cols - 1) / cols), (unsigned)((a.rows + 15) / 16));
+    hipLaunchKernelGGL((linear_kernel<NORM, MODE, NB>), grid, dim3(kLinThreads), 0, stream, a);
+}
+
+int check_linear(const char* what, const float* x, int64_t ldx, const float* norm_w,
+                 const void* w, int64_t n_out, int64_t k_in, const float* out, int64_t ldo,
+                 int64_t rows) {
+    CRUCIBLE_CHECK(x && w && out, CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
+    CRUCIBLE_CHECK(rows >= 0 && rows <= 16 * 65535, CRUCIBLE_ERR_INVALID, "%s: rows %lld",
+                   what, (long long)rows);
+    CRUCIBLE_CHECK(n_out > 0 && n_out <= INT32_MAX, CRUCIBLE_ERR_INVALID, "%s: n_out %lld",
+                   what, (long long)n_out);
+    CRUCIBLE_CHECK(k_in > 0 && k_in % 32 == 0 && k_in <= (1 << 20), CRUCIBLE_ERR_UNSUPPORTED,
+                   "%s: k_in %lld must be a positive multiple of 32", what, (long long)k_in);
+    CRUCIBLE_CHECK(ldx >= k_in && ldx % 4 == 0 && ldo >= n_out, CRUCIBLE_ERR_INVALID,
+                   "%s: leading dimensions (ldx %lld, ldo %lld)", what, (long long)ldx,
+                   (long long)ldo);
+    CRUCIBLE_CHECK(aligned16(x) && aligned16(w) && (!norm_w || aligned16(norm_w)),
+                   CRUCIBLE_ERR_INVALID, "%s: x, w and norm_w must be 16-byte aligned", what);
+    return CRUCIBLE_OK;
+}
+
+}  // namespace
+}  // namespace crucible
+
+using namespace crucible;
+
+extern "C" int crucible_linear_f64acc(const float* x, int64_t ldx, const float* norm_w, float eps,
+                                      const void* w, int64_t n_out, int64_t k_in,
+                                      const float* resid, float* out, int64_t ldo, int64_t rows,
+                                      crucible_stream_t stream) {
+    const char* what = "crucible_linear_f64acc";
+    const int rc = check_linear(what, x, ldx, norm_w, w, n_out, k_in, out, ldo, rows);
+    if (rc != CRUCIBLE_OK) return rc;
+    if (rows == 0) return CRUCIBLE_OK;
+    LinArgs a{x, ldx, norm_w, (double)eps, static_cast<const half_t*>(w), nullptr, resid, out,
+              ldo, (int)rows, (int)n_out, (int)k_in};
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    // Wide outputs (the vocabulary projection) take 4 column blocks per workgroup so each
+    // activation fragment feeds 4 MFMAs; narrow ones keep more workgroups.
+    const bool wide = n_out >= 16 * 1024;
+    if (resid) {
+        if (norm_w) launch_linear<true, kResidual, 1>(a, s);
+        else launch_linear<false, kResidual, 1>(a, s);
+    } else if (norm_w) {
+        if (wide) launch_linear<true, kPlain, 4>(a, s);
+        else launch_linear<true, kPlain, 1>(a, s);
+    } else {
+        if (wide) launch_linear<false, kPlain, 4>(a, s);
+        else launch_linear<false, kPlain, 1>(a, s);
+    }
+    return fail_launch(what);
+}
+
+extern "C" int crucible_linear_swiglu_f64acc(const float* x, int64_t ldx, const float* norm_w,
+                                             float eps, const void* w_gate, const void* w_up,
+                                             int64_t hidden, int64_t k_in, float* out,
+                                             int64_t ldo, int64_t rows,
+                                             crucible_stream_t stream) {
+    const char* what = "crucible_linear_swiglu_f64acc";
+    int rc = check_linear(what, x, ldx, norm_w, w_gate, hidden, k_in, out, ldo, rows);
+    if (rc != CRUCIBLE_OK) return rc;
+    CRUCIBLE_CHECK(w_up && aligned16(w_up), CRUCIBLE_ERR_INVALID,
+                   "%s: w_up must be a 16-byte aligned buffer", what);
+    if (rows == 0) return CRUCIBLE_OK;
+    LinArgs a{x, ldx, norm_w, (double)eps, static_cast<const half_t*>(w_gate),
+              static_cast<const half_t*>(w_up), nullptr, out, ldo, (int)rows, (int)hidden,
+              (int)k_in};
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (norm_w) launch_linear<true, kSwiGLU, 2>(a, s);
+    else launch_linear<false, kSwiGLU, 2>(a, s);
+    return fail_launch(what);
+}
+
+extern "C" int crucible_rmsnorm_rows(const float* x, int64_t ldx, const float* w, float eps,
+                                     float* out, int64_t ldo, int64_t rows, int64_t n,
+                                     crucible_stream_t stream) {
+    const char* what = "crucible_rmsnorm_rows";
+    CRUCIBLE_CHECK(x && w && out, CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
+    CRUCIBLE_CHECK(rows >= 0 && rows <= INT32_MAX && n > 0 && n <= INT32_MAX && ldx >= n &&
+                       ldo >= n,
+                   CRUCIBLE_ERR_INVALID, "%s: bad shape", what);
+    if (rows == 0) return CRUCIBLE_OK;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), x, ldx, w, (double)eps, out, ldo,
+                       (int)n);
+    return fail_launch(what);
+}
+
+extern "C" int crucible_rope_split_qkv(const float* qkv, int64_t ld, float* q, float* k, float* v,
+                                       const float* cos_table, const float* sin_table,
+                                       const int32_t* positions, int64_t rows, int64_t n_head,
+                                       int64_t n_kv_head, int64_t head_dim, int64_t max_pos,
+                                       crucible_stream_t stream) {
+    const char* what = "crucible_rope_split_qkv";
+    CRUCIBLE_CHECK(qkv && q && k && v && cos_table && sin_table && positions,
+                   CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
+    CRUCIBLE_CHECK(head_dim == 64, CRUCIBLE_ERR_UNSUPPORTED,
+                   "%s: head_dim %lld unsupported (this build implements 64)", what,
+                   (long long)head_dim);
+    CRUCIBLE_CHECK(n_head > 0 && n_kv_head > 0 && n_head <= 4096 && n_kv_head <= 4096 &&
+                       ld >= (n_head + 2 * n_kv_head) * 64 && max_pos > 0 &&
+                       max_pos <= INT32_MAX && rows >= 0 && rows <= (1 << 24),
+                   CRUCIBLE_ERR_INVALID, "%s: bad shape", what);
+    if (rows == 0) return CRUCIBLE_OK;
+    const int64_t threads = rows * (n_head + 2 * n_kv_head) * 32;
+    hipLaunchKernelGGL(rope_split_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), qkv, ld, q, k, v, cos_table,
+                       sin_table, positions, (int)rows, (int)n_head, (int)n_kv_head,
+                       (int)max_pos);
+    return fail_launch(what);
+}

@@ -250,6 +250,63 @@ class Gpu:
             rows, n_head, n_kv_head, head_dim, max_seq, cache_stride, layer_base, pos_offset,
             self._stream()))
 
+    # ------------------------------------------------------------- decode-step glue
+    def linear_f64acc(self, x, w, out, *, norm_w=None, eps=1e-6, resid=None):
+        """out = [resid +] f32(f64-accumulated h . w^T), h = x or rmsnorm(x, norm_w)
+        (ops.rs:17-32 matvec, :39-52 rmsnorm). x [rows][k_in] f32, w [n_out][k_in] fp16,
+        out (and resid) [rows][n_out] f32; resid may be out itself."""
+        rows, k_in = x.shape
+        n_out = w.shape[0]
+        _need(x, "x", dtype=torch.float32)
+        _need(w, "w", dtype=torch.float16, numel=n_out * k_in)
+        _need(out, "out", dtype=torch.float32, numel=rows * n_out)
+        if norm_w is not None:
+            _need(norm_w, "norm_w", dtype=torch.float32, numel=k_in)
+        if resid is not None:
+            _need(resid, "resid", dtype=torch.float32, numel=rows * n_out)
+        _lib.check(self.lib.crucible_linear_f64acc(
+            _ptr(x), k_in, _ptr(norm_w) if norm_w is not None else None, float(eps), _ptr(w),
+            n_out, k_in, _ptr(resid) if resid is not None else None, _ptr(out), n_out, rows,
+            self._stream()))
+
+    def linear_swiglu_f64acc(self, x, w_gate, w_up, out, *, norm_w=None, eps=1e-6):
+        """out = silu(g) * u with g, u the f64-accumulated projections of
+        rmsnorm(x, norm_w) (or x) by w_gate and w_up (model.rs:252-262)."""
+        rows, k_in = x.shape
+        hidden = w_gate.shape[0]
+        _need(x, "x", dtype=torch.float32)
+        _need(w_gate, "w_gate", dtype=torch.float16, numel=hidden * k_in)
+        _need(w_up, "w_up", dtype=torch.float16, numel=hidden * k_in)
+        _need(out, "out", dtype=torch.float32, numel=rows * hidden)
+        if norm_w is not None:
+            _need(norm_w, "norm_w", dtype=torch.float32, numel=k_in)
+        _lib.check(self.lib.crucible_linear_swiglu_f64acc(
+            _ptr(x), k_in, _ptr(norm_w) if norm_w is not None else None, float(eps),
+            _ptr(w_gate), _ptr(w_up), hidden, k_in, _ptr(out), hidden, rows, self._stream()))
+
+    def rmsnorm_rows(self, x, w, out, eps=1e-6):
+        """ops.rs:39-52 on every row of x [rows][n]."""
+        rows, n = x.shape
+        _need(x, "x", dtype=torch.float32)
+        _need(w, "w", dtype=torch.float32, numel=n)
+        _need(out, "out", dtype=torch.float32, numel=rows * n)
+        _lib.check(self.lib.crucible_rmsnorm_rows(_ptr(x), n, _ptr(w), float(eps), _ptr(out), n,
+                                                  rows, n, self._stream()))
+
+    def rope_split_qkv(self, qkv, q, k, v, cos, sin, positions, n_head, n_kv_head):
+        """Split [q | k | v] rows and rotate q, k at positions[row] (ops.rs:124-135)."""
+        rows, ld = qkv.shape
+        _need(qkv, "qkv", dtype=torch.float32)
+        _need(q, "q", dtype=torch.float32, numel=rows * n_head * 64)
+        _need(k, "k", dtype=torch.float32, numel=rows * n_kv_head * 64)
+        _need(v, "v", dtype=torch.float32, numel=rows * n_kv_head * 64)
+        _need(cos, "cos", dtype=torch.float32)
+        _need(sin, "sin", dtype=torch.float32, numel=cos.numel())
+        _need(positions, "positions", dtype=torch.int32, numel=rows)
+        _lib.check(self.lib.crucible_rope_split_qkv(
+            _ptr(qkv), ld, _ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(positions), rows,
+            n_head, n_kv_head, 64, cos.shape[0], self._stream()))
+
     # ------------------------------------------------------------- greedy selection
     def argmax_rows(self, x, out, rows, cols):
         """gpu.rs:562-580 with the host rule of sampling.rs:141-150: ties to the lowest

@@ -11,14 +11,18 @@ Per layer the attention block is this library:
     crucible_attention_prefill_tiled over {packed_start, chunk_len, 0, table} segments;
   * decode: crucible_attention_decode_paged_append (both row appends and the attention
     in one launch).
-Projections, norms and the MLP are torch operations on the device (glue, not the
-path), written to follow the reference CPU arithmetic (engine/src/model.rs:145-299,
-engine/src/ops.rs): RMSNorm with the mean of squares and the scale in f64, half-split
-RoPE from f32 tables whose angles are computed in f64, SwiGLU as g / (1 + exp(-g)) * u,
-pre-norm residual blocks, and a vocabulary projection tied to the token embedding.
-Activations are f32 and KV pages hold fp16. Projections run either as the reference's
-matvec contract (ops.rs:17-32: f32 operands, f64 accumulation, f32 result; weights held
-as f64, `precision="reference"`) or as plain f32 GEMMs (`precision="f32"`).
+Projections, norms and the MLP follow the reference CPU arithmetic
+(engine/src/model.rs:145-299, engine/src/ops.rs): RMSNorm with the mean of squares and
+the scale in f64, half-split RoPE from f32 tables whose angles are computed in f64,
+SwiGLU as g / (1 + exp(-g)) * u, pre-norm residual blocks, and a vocabulary projection
+tied to the token embedding. Activations are f32, weights fp16, KV pages fp16.
+Projections run either as the reference's matvec contract (ops.rs:17-32: f32 operands,
+f64 accumulation, f32 result; `precision="reference"`) or as plain f32 GEMMs
+(`precision="f32"`). In reference precision the decode step is this library's kernels
+end to end: f64-MFMA projections with RMSNorm, residual and SwiGLU fused
+(crucible_linear_f64acc, crucible_linear_swiglu_f64acc), RoPE + q/k/v split, the fused
+append + attention, RMSNorm and the vocabulary projection, then the device argmax. The
+prefill's projections are torch f64 GEMMs (the same contract) over the packed rows.
 
 Paging is the reference allocator (crucible_amd.paged): every request reserves the
 pages it needs through its last generated token up front (prefill.rs:160-172), so the
@@ -130,29 +134,27 @@ class GpuModel:
         self.table_stride = -(-capacity // PAGE_TOKENS)
         dev = self.dev
 
-        wdt = torch.float64 if precision == "reference" else torch.float32
-
         def f32(name):
             return torch.from_numpy(np.ascontiguousarray(weights[name])).to(dev).float()
 
-        def wmat(name):  # projection weights, in the accumulation dtype
-            return torch.from_numpy(np.ascontiguousarray(weights[name])).to(dev).to(wdt)
+        def h16(name):  # projection weights stay fp16 on the device
+            return torch.from_numpy(np.ascontiguousarray(weights[name])).to(dev).half()
 
         self.tok_emb = f32("tok_emb.weight")
-        self.lm_head = wmat("tok_emb.weight")  # tied (model.rs:288-297)
+        self.lm_head = h16("tok_emb.weight")  # tied (model.rs:288-297)
         self.layers = []
         for i in range(cfg.n_layer):
             p = f"blocks.{i}"
             self.layers.append({
                 "attn_norm": f32(f"{p}.attn_norm.weight"),
-                "wqkv": torch.cat([wmat(f"{p}.attn.q_proj.weight"),
-                                   wmat(f"{p}.attn.k_proj.weight"),
-                                   wmat(f"{p}.attn.v_proj.weight")]).contiguous(),
-                "wo": wmat(f"{p}.attn.o_proj.weight"),
+                "wqkv": torch.cat([h16(f"{p}.attn.q_proj.weight"),
+                                   h16(f"{p}.attn.k_proj.weight"),
+                                   h16(f"{p}.attn.v_proj.weight")]).contiguous(),
+                "wo": h16(f"{p}.attn.o_proj.weight"),
                 "mlp_norm": f32(f"{p}.mlp_norm.weight"),
-                "wgu": torch.cat([wmat(f"{p}.mlp.gate_proj.weight"),
-                                  wmat(f"{p}.mlp.up_proj.weight")]).contiguous(),
-                "wd": wmat(f"{p}.mlp.down_proj.weight"),
+                "wg": h16(f"{p}.mlp.gate_proj.weight"),
+                "wu": h16(f"{p}.mlp.up_proj.weight"),
+                "wd": h16(f"{p}.mlp.down_proj.weight"),
             })
         self.final_norm = f32("final_norm.weight")
         cos, sin = rope_tables(cfg.head_dim, capacity, cfg.rope_theta)
@@ -170,12 +172,12 @@ class GpuModel:
         self._graph_batch = None
 
     # ------------------------------------------------------------------ glue ops
-    @staticmethod
-    def _linear(x, w):
-        """x [rows, in] f32 times w [out, in]^T in w's dtype, rounded to f32."""
-        if w.dtype == torch.float32:
-            return x @ w.t()
-        return (x.to(w.dtype) @ w.t()).float()
+    def _linear(self, x, w):
+        """x [rows, in] f32 times the fp16 w [out, in]^T: f64 products and sums rounded
+        once to f32 (reference precision) or an f32 GEMM."""
+        if self.precision == "f32":
+            return x @ w.float().t()
+        return (x.double() @ w.double().t()).float()
 
     def _rmsnorm(self, x, w):
         """ops.rs rmsnorm: scale = 1 / sqrt(mean(x^2) + eps) in f64, out = f32(x * scale) * w."""
@@ -194,8 +196,8 @@ class GpuModel:
 
     def _mlp(self, x, layer):
         h = self._rmsnorm(x, layer["mlp_norm"])
-        gu = self._linear(h, layer["wgu"])
-        g, u = gu[:, :self.cfg.hidden], gu[:, self.cfg.hidden:]
+        g = self._linear(h, layer["wg"])
+        u = self._linear(h, layer["wu"])
         a = g / (1.0 + torch.exp(-g)) * u
         return x + self._linear(a, layer["wd"])
 
@@ -279,6 +281,37 @@ class GpuModel:
     # ------------------------------------------------------------------ decode
     def _decode_step(self, st):
         """One batched decode step on the static buffers in `st` (graph-capturable)."""
+        if self.precision == "reference":
+            self._decode_step_native(st)
+        else:
+            self._decode_step_torch(st)
+        self._advance(st)
+
+    def _decode_step_native(self, st):
+        """The step as this library's kernels (reference arithmetic), 8 launches a layer."""
+        cfg, gpu = self.cfg, self.gpu
+        b = st["batch"]
+        eps = float(np.float32(cfg.norm_eps))
+        x = st["x"]
+        torch.index_select(self.tok_emb, 0, st["tokens"], out=x)
+        for layer_i, layer in enumerate(self.layers):
+            gpu.linear_f64acc(x, layer["wqkv"], st["qkv"], norm_w=layer["attn_norm"], eps=eps)
+            gpu.rope_split_qkv(st["qkv"], st["q"], st["k"], st["v"], self.rope_cos, self.rope_sin,
+                               st["positions"], cfg.n_head, cfg.n_kv_head)
+            gpu.attention_decode_paged_append(st["q"], st["k"], st["v"], self.k_pool, self.v_pool,
+                                              st["attn"], st["tables"], st["positions"],
+                                              st["lens"], b, cfg.n_head, cfg.n_kv_head, 64,
+                                              self.table_stride, cfg.n_layer, layer_i,
+                                              cfg.kv_dim, self.capacity,
+                                              workspace=self.workspace)
+            gpu.linear_f64acc(st["attn"], layer["wo"], x, resid=x)
+            gpu.linear_swiglu_f64acc(x, layer["wg"], layer["wu"], st["act"],
+                                     norm_w=layer["mlp_norm"], eps=eps)
+            gpu.linear_f64acc(st["act"], layer["wd"], x, resid=x)
+        gpu.rmsnorm_rows(x, self.final_norm, st["h"], eps)
+        gpu.linear_f64acc(st["h"], self.lm_head, st["logits"])
+
+    def _decode_step_torch(self, st):
         cfg, gpu = self.cfg, self.gpu
         b = st["batch"]
         cos = self.rope_cos.index_select(0, st["positions"])
@@ -294,7 +327,11 @@ class GpuModel:
             x = x + self._linear(st["attn"], layer["wo"])
             x = self._mlp(x, layer)
         st["logits"].copy_(self._logits(x))
-        gpu.argmax_rows(st["logits"], st["tokens"], b, cfg.vocab_size)
+
+    def _advance(self, st):
+        """Greedy token, history, and the next step's position and length."""
+        b = st["batch"]
+        self.gpu.argmax_rows(st["logits"], st["tokens"], b, self.cfg.vocab_size)
         st["history"].index_copy_(0, st["step"], st["tokens"].view(1, b))
         st["positions"].add_(1)
         st["lens"].add_(1)
@@ -329,6 +366,14 @@ class GpuModel:
                 "positions": torch.from_numpy(lens).to(dev),       # position of the token fed
                 "lens": torch.from_numpy(lens + 1).to(dev),        # keys visible after append
                 "attn": torch.empty((batch, cfg.n_embd), dtype=torch.float32, device=dev),
+                "x": torch.empty((batch, cfg.n_embd), dtype=torch.float32, device=dev),
+                "h": torch.empty((batch, cfg.n_embd), dtype=torch.float32, device=dev),
+                "qkv": torch.empty((batch, cfg.n_embd + 2 * cfg.kv_dim), dtype=torch.float32,
+                                   device=dev),
+                "q": torch.empty((batch, cfg.n_embd), dtype=torch.float32, device=dev),
+                "k": torch.empty((batch, cfg.kv_dim), dtype=torch.float32, device=dev),
+                "v": torch.empty((batch, cfg.kv_dim), dtype=torch.float32, device=dev),
+                "act": torch.empty((batch, cfg.hidden), dtype=torch.float32, device=dev),
                 "logits": torch.empty((batch, cfg.vocab_size), dtype=torch.float32, device=dev),
                 "history": torch.zeros((max(n_new - 1, 1), batch), dtype=torch.int32, device=dev),
                 "step": torch.zeros(1, dtype=torch.long, device=dev),

@@ -225,6 +225,50 @@ int crucible_attention_prefill(const void* q, int q_dtype, const void* k_cache,
 int crucible_argmax_rows(const float* x, int32_t* out, int64_t rows, int64_t cols,
                          crucible_stream_t stream);
 
+/* ------------------------------------------------------------------ decode-step glue
+ * The projections and row operations that surround attention in the reference's batched
+ * decode step (gpu_model.rs:1393-1605 queue_decode_batch), with the reference CPU
+ * arithmetic of engine/src/ops.rs so greedy tokens match the CPU model exactly:
+ * projections accumulate every product in f64 and round once to f32 (ops.rs:17-32,
+ * matvec), where the reference GPU kernels accumulate in f32. Weights are fp16
+ * [n_out][k_in] row-major (the reference's [out][in] order); activations are f32.
+ */
+
+/* y[m][n] = f32(sum_k f64(w[n][k]) * f64(h[m][k])) for m < rows, n < n_out; replaces the
+ * batched GEMV (kernels.cu:1539-1607, gpu.rs gemv_batch) for the q/k/v, o, down and
+ * vocabulary projections. h = x, or rmsnorm(x, norm_w, eps) when norm_w is not NULL
+ * (ops.rs:39-52: f64 mean of squares, h = f32(f64(x) * scale) * norm_w). out = y, or
+ * resid + y when resid is not NULL (the residual add of model.rs:237-241,270-274; resid
+ * may equal out, element-wise in place). x [rows][ldx], out and resid [rows][ldo].
+ * k_in must be a multiple of 32; x, w and norm_w 16-byte aligned, ldx a multiple of 4. */
+int crucible_linear_f64acc(const float* x, int64_t ldx, const float* norm_w, float eps,
+                           const void* w, int64_t n_out, int64_t k_in, const float* resid,
+                           float* out, int64_t ldo, int64_t rows, crucible_stream_t stream);
+
+/* SwiGLU input of the MLP (model.rs:252-262): out[m][j] = silu(g) * u with
+ * g = f64-accumulated rmsnorm(x) . w_gate[j], u = the same with w_up[j], each rounded to
+ * f32, and silu(g) = g / (1 + exp(-g)) (ops.rs:83-85). Replaces the gate/up GEMVs and
+ * swiglu_batch_f32 (kernels.cu:1038-1047). w_gate, w_up: [hidden][k_in] fp16. */
+int crucible_linear_swiglu_f64acc(const float* x, int64_t ldx, const float* norm_w, float eps,
+                                  const void* w_gate, const void* w_up, int64_t hidden,
+                                  int64_t k_in, float* out, int64_t ldo, int64_t rows,
+                                  crucible_stream_t stream);
+
+/* RMSNorm of each row (ops.rs:39-52; replaces rmsnorm_batch_f32, kernels.cu:968-996). */
+int crucible_rmsnorm_rows(const float* x, int64_t ldx, const float* w, float eps, float* out,
+                          int64_t ldo, int64_t rows, int64_t n, crucible_stream_t stream);
+
+/* Split fused [q | k | v] rows (n_head, n_kv_head, n_kv_head heads of head_dim) into
+ * contiguous q [rows][n_head*64], k and v [rows][n_kv_head*64], rotating q and k at
+ * positions[row] (RopeTable::apply, ops.rs:124-135; rope_rows_f32, kernels.cu:1677-1706).
+ * cos/sin tables are [max_pos][head_dim/2] f32. A position outside [0, max_pos) writes
+ * NaN rows. */
+int crucible_rope_split_qkv(const float* qkv, int64_t ld, float* q, float* k, float* v,
+                            const float* cos_table, const float* sin_table,
+                            const int32_t* positions, int64_t rows, int64_t n_head,
+                            int64_t n_kv_head, int64_t head_dim, int64_t max_pos,
+                            crucible_stream_t stream);
+
 /* ------------------------------------------------------------------ host helpers */
 
 /* Build prefill segments from cumulative sequence offsets (host memory):

@@ -31,6 +31,8 @@ typedef double double4_t __attribute__((ext_vector_type(4)));
 constexpr int kLinWaves = 8;               // the K range is split over the 8 waves
 constexpr int kLinThreads = 64 * kLinWaves;
 constexpr int kLinK = 32;                  // K per chunk: 8 per lane group, 8 MFMA steps
+constexpr int kLinBatch = 8;               // chunks whose loads are in flight together
+                                           // (1 for the 4-block tiles: registers, occupancy)
 
 enum LinMode { kPlain = 0, kResidual = 1, kSwiGLU = 2 };
 
@@ -79,14 +81,25 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
     const int n0 = blockIdx.x * 16 * (MODE == kSwiGLU ? 1 : NB);
 
     if constexpr (NORM) {
-        // sum of squares of row tid >> 5 over k = (tid & 31) + 32 i, in f64
+        // sum of squares of row tid >> 5 over the float4s t, t + 32, ... of the row, in
+        // f64; loads go out 8 at a time so their latencies overlap
         const int r = tid >> 5, t = tid & 31;
         double ss = 0.0;
         if (m0 + r < a.rows) {
-            const float* xr = a.x + (int64_t)(m0 + r) * a.ldx;
-            for (int k = t; k < a.k_in; k += 32) {
-                const double v = (double)xr[k];
-                ss += v * v;
+            const float4_t* xr = reinterpret_cast<const float4_t*>(a.x + (int64_t)(m0 + r) * a.ldx);
+            const int n4 = a.k_in / 4;
+            for (int i0 = t; i0 < n4; i0 += 32 * 8) {
+                float4_t v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    v[i] = (i0 + 32 * i < n4) ? xr[i0 + 32 * i] : float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const double d = (double)v[i][e];
+                        ss += d * d;
+                    }
             }
         }
 #pragma unroll
@@ -128,30 +141,37 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[j] = double4_t{0.0, 0.0, 0.0, 0.0};
 
-    Chunk<NB> cur;
-    if (kw > 0) cur = load(0);
-    for (int k0 = 0; k0 < kw; k0 += kLinK) {
-        Chunk<NB> nxt = cur;
-        if (k0 + kLinK < kw) nxt = load(k0 + kLinK);
-        float xs[8] = {cur.x0[0], cur.x0[1], cur.x0[2], cur.x0[3],
-                       cur.x1[0], cur.x1[1], cur.x1[2], cur.x1[3]};
-        if constexpr (NORM) {
-            const float4_t w0 = *reinterpret_cast<const float4_t*>(nwp + k0);
-            const float4_t w1 = *reinterpret_cast<const float4_t*>(nwp + k0 + 4);
-            const float nw[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+    // Up to kLinBatch chunks load at once (the weights stream from HBM once: their
+    // latency, not the MFMA, bounds these small-batch products), then feed the MFMA.
+    constexpr int BATCH = NB >= 4 ? 1 : kLinBatch;
+    for (int b0 = 0; b0 < kw; b0 += BATCH * kLinK) {
+        Chunk<NB> ch[BATCH];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) xs[i] = (float)((double)xs[i] * scale) * nw[i];
-        }
+        for (int c = 0; c < BATCH; ++c)
+            if (b0 + c * kLinK < kw) ch[c] = load(b0 + c * kLinK);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const double av = row_ok ? (double)xs[i] : 0.0;
+        for (int c = 0; c < BATCH; ++c) {
+            if (b0 + c * kLinK >= kw) break;
+            const int k0 = b0 + c * kLinK;
+            float xs[8] = {ch[c].x0[0], ch[c].x0[1], ch[c].x0[2], ch[c].x0[3],
+                           ch[c].x1[0], ch[c].x1[1], ch[c].x1[2], ch[c].x1[3]};
+            if constexpr (NORM) {
+                const float4_t w0 = *reinterpret_cast<const float4_t*>(nwp + k0);
+                const float4_t w1 = *reinterpret_cast<const float4_t*>(nwp + k0 + 4);
+                const float nw[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
 #pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                const double bv = n_ok[j] ? (double)(float)cur.w[j][i] : 0.0;
-                acc[j] = mfma_f64(av, bv, acc[j]);
+                for (int i = 0; i < 8; ++i) xs[i] = (float)((double)xs[i] * scale) * nw[i];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const double av = row_ok ? (double)xs[i] : 0.0;
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const double bv = n_ok[j] ? (double)(float)ch[c].w[j][i] : 0.0;
+                    acc[j] = mfma_f64(av, bv, acc[j]);
+                }
             }
         }
-        cur = nxt;
     }
 
 #pragma unroll

@@ -224,7 +224,8 @@ __device__ __forceinline__ void store_new_row(const DecodeArgs& a, const NewRow&
     }
 }
 
-template <int PAGES, int WAVES, bool QF32, bool APPEND, bool PAGED>
+// RMAJOR: grid (kv head, request, split) instead of (split, kv head, request).
+template <int PAGES, int WAVES, bool QF32, bool APPEND, bool PAGED, bool RMAJOR>
 __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     __shared__ float4_t s_acc[WAVES][16][17];  // [wave][col][dim/4], padded
     __shared__ float s_m[WAVES][16];
@@ -236,10 +237,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     const int col = lane & 15;
     const int grp = lane >> 4;
 
-    // grid = (split, kv head, request): no integer division on the way to the loads
-    const int s = blockIdx.x;
-    const int g = blockIdx.y;
-    const int b = blockIdx.z;
+    // Grid (split, kv head, request), or (kv head, request, split) for grids larger than the
+    // chip holds at once: then every request's first splits are dispatched before any
+    // later split, and the later ones (often past the request's end) queue last. Either
+    // way, no integer division on the way to the loads.
+    const int s = RMAJOR ? blockIdx.z : blockIdx.x;
+    const int g = RMAJOR ? blockIdx.x : blockIdx.y;
+    const int b = RMAJOR ? blockIdx.y : blockIdx.z;
     const int bg = b * a.n_kv_head + g;
 
     // Query operand: B[k = channel][col = head], 8 channels per lane per MFMA. Issued
@@ -505,12 +509,17 @@ DecodeShape decode_shape(int64_t batch, int64_t n_kv_head, int64_t max_pages) {
 }
 
 template <bool QF32, bool APPEND, bool PAGED>
-bool launch_shape(const DecodeArgs& a, DecodeShape sh, dim3 grid, hipStream_t stream) {
-#define CRUCIBLE_DECODE_CASE(P, W)                                                           \
-    if (sh.pages == P && sh.waves == W) {                                                     \
-        hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED>), grid, dim3(W * 64), 0, \
-                           stream, a);                                                        \
-        return true;                                                                          \
+bool launch_shape(const DecodeArgs& a, DecodeShape sh, bool rmajor, dim3 grid,
+                  hipStream_t stream) {
+#define CRUCIBLE_DECODE_CASE(P, W)                                                             \
+    if (sh.pages == P && sh.waves == W) {                                                       \
+        if (rmajor)                                                                             \
+            hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, true>), grid,          \
+                               dim3(W * 64), 0, stream, a);                                     \
+        else                                                                                    \
+            hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, false>), grid,         \
+                               dim3(W * 64), 0, stream, a);                                     \
+        return true;                                                                            \
     }
     CRUCIBLE_DECODE_CASE(1, 4)
     CRUCIBLE_DECODE_CASE(2, 4)
@@ -527,17 +536,23 @@ int launch_decode(DecodeArgs a, DecodeShape sh, bool q_f32, hipStream_t stream,
     CRUCIBLE_CHECK(a.n_splits > 0 && a.n_kv_head <= 65535 && a.batch <= 65535,
                    CRUCIBLE_ERR_INVALID, "%s: grid (%d, %d, %d) too large", what, a.n_splits,
                    a.n_kv_head, a.batch);
-    const dim3 grid((unsigned)a.n_splits, (unsigned)a.n_kv_head, (unsigned)a.batch);
+    // Request-major order once the grid exceeds what stays resident at once (the 512-thread
+    // shapes hold 2-3 workgroups per CU by registers: at most 768 on 256 CUs). At or below
+    // that, the split-major order measures faster.
+    bool rmajor = (int64_t)a.n_splits * a.n_kv_head * a.batch > 3 * 256;
+    if (const char* env = std::getenv("CRUCIBLE_DECODE_REQUEST_MAJOR")) rmajor = std::atoi(env) != 0;
+    const dim3 grid = rmajor ? dim3((unsigned)a.n_kv_head, (unsigned)a.batch, (unsigned)a.n_splits)
+                             : dim3((unsigned)a.n_splits, (unsigned)a.n_kv_head, (unsigned)a.batch);
     bool launched;
     if (a.positions)  // the fused append exists for paged pools only
-        launched = q_f32 ? launch_shape<true, true, true>(a, sh, grid, stream)
-                         : launch_shape<false, true, true>(a, sh, grid, stream);
+        launched = q_f32 ? launch_shape<true, true, true>(a, sh, rmajor, grid, stream)
+                         : launch_shape<false, true, true>(a, sh, rmajor, grid, stream);
     else if (a.tables)
-        launched = q_f32 ? launch_shape<true, false, true>(a, sh, grid, stream)
-                         : launch_shape<false, false, true>(a, sh, grid, stream);
+        launched = q_f32 ? launch_shape<true, false, true>(a, sh, rmajor, grid, stream)
+                         : launch_shape<false, false, true>(a, sh, rmajor, grid, stream);
     else
-        launched = q_f32 ? launch_shape<true, false, false>(a, sh, grid, stream)
-                         : launch_shape<false, false, false>(a, sh, grid, stream);
+        launched = q_f32 ? launch_shape<true, false, false>(a, sh, rmajor, grid, stream)
+                         : launch_shape<false, false, false>(a, sh, rmajor, grid, stream);
     CRUCIBLE_CHECK(launched, CRUCIBLE_ERR_INVALID, "%s: bad decode shape %d x %d", what,
                    sh.pages, sh.waves);
     if (int rc = fail_launch(what)) return rc;

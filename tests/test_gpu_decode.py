@@ -301,11 +301,14 @@ def test_fused_append_off_the_last_slot_and_inactive_rows(gpu, dev):
         assert np.all(o2[2] == SENTINEL)
 
 
-def test_decode_shapes_agree(gpu, dev, monkeypatch):
+@pytest.mark.parametrize("order", ["0", "1"])
+def test_decode_shapes_agree(gpu, dev, monkeypatch, order):
     """Every split shape (pages per wave x waves per workgroup) gives the oracle's answer,
-    with the fused and plain entries, on lengths that exercise 1..many splits."""
+    with the fused and plain entries, on lengths that exercise 1..many splits, in both
+    grid orders (split-major and request-major)."""
     lens = [3, 64, 65, 500, 1023, 2048, 1500, 16]
     positions = [n - 1 for n in lens]
+    monkeypatch.setenv("CRUCIBLE_DECODE_REQUEST_MAJOR", order)
     for pages in ("1", "2", "4"):
         for waves in ("4", "8"):
             monkeypatch.setenv("CRUCIBLE_DECODE_PAGES", pages)

@@ -237,10 +237,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     const int col = lane & 15;
     const int grp = lane >> 4;
 
-    // Grid (split, kv head, request), or (kv head, request, split) for grids larger than the
-    // chip holds at once: then every request's first splits are dispatched before any
-    // later split, and the later ones (often past the request's end) queue last. Either
-    // way, no integer division on the way to the loads.
+    // Grid (kv head, request, split), request-major (the default): every request's first
+    // splits are dispatched before any later split, and the later ones (often past the
+    // request's end) queue last; or (split, kv head, request). Either way, no integer
+    // division on the way to the loads.
     const int s = RMAJOR ? blockIdx.z : blockIdx.x;
     const int g = RMAJOR ? blockIdx.x : blockIdx.y;
     const int b = RMAJOR ? blockIdx.y : blockIdx.z;
@@ -495,8 +495,8 @@ DecodeShape decode_shape(int64_t batch, int64_t n_kv_head, int64_t max_pages) {
     // page-units = (request, kv head, page) triples the grid is sized for
     const int64_t units = batch * n_kv_head * max_pages;
     DecodeShape sh{1, 4};                 // 4-page splits: few requests, short contexts
-    if (units > 2048) sh = {1, 8};        // 8-page splits (e.g. b16 x 3 kv heads x 2048)
-    if (units > 8192) sh = {2, 8};        // 16-page splits (e.g. b16 x 12 kv heads x 2048)
+    if (units > 2048) sh = {2, 8};        // 16-page splits (e.g. b16 x 3 kv heads x 2048)
+    if (units > 8192) sh = {4, 4};        // 16-page splits, 4 pages a wave (b16 x 12 x 2048)
     if (const char* env = std::getenv("CRUCIBLE_DECODE_PAGES")) {
         const int v = std::atoi(env);
         if (v == 1 || v == 2 || v == 4) sh.pages = v;
@@ -536,10 +536,9 @@ int launch_decode(DecodeArgs a, DecodeShape sh, bool q_f32, hipStream_t stream,
     CRUCIBLE_CHECK(a.n_splits > 0 && a.n_kv_head <= 65535 && a.batch <= 65535,
                    CRUCIBLE_ERR_INVALID, "%s: grid (%d, %d, %d) too large", what, a.n_splits,
                    a.n_kv_head, a.batch);
-    // Request-major order once the grid exceeds what stays resident at once (the 512-thread
-    // shapes hold 2-3 workgroups per CU by registers: at most 768 on 256 CUs). At or below
-    // that, the split-major order measures faster.
-    bool rmajor = (int64_t)a.n_splits * a.n_kv_head * a.batch > 3 * 256;
+    // Request-major order: every request's first splits are dispatched first (measured
+    // faster with the default shapes, most of all when the grid exceeds the resident set).
+    bool rmajor = true;
     if (const char* env = std::getenv("CRUCIBLE_DECODE_REQUEST_MAJOR")) rmajor = std::atoi(env) != 0;
     const dim3 grid = rmajor ? dim3((unsigned)a.n_kv_head, (unsigned)a.batch, (unsigned)a.n_splits)
                              : dim3((unsigned)a.n_splits, (unsigned)a.n_kv_head, (unsigned)a.batch);

@@ -108,6 +108,34 @@ struct PrefillArgs {
     float scale_log2;
 };
 
+// Row `local` of the grid tile: its packed row (-1 = none), owner (table) and absolute
+// position, by the entry point's row mode.
+__device__ __forceinline__ void tile_row(const PrefillArgs& a, int64_t local, int& row,
+                                         int& owner, int& pos) {
+    row = -1;
+    owner = 0;
+    pos = 0;
+    if (a.mode == kSegments) {
+        const int32_t* seg = a.segments + 4 * (int64_t)blockIdx.z;
+        if (local < seg[1]) {
+            row = (int)(seg[0] + local);
+            pos = (int)(seg[2] + local);
+            owner = seg[3];
+        }
+    } else if (local < a.rows) {
+        row = (int)local;
+        if (a.mode == kOwners) {
+            owner = a.owners[local];
+            pos = a.positions[local];
+        } else if (a.mode == kParams) {
+            pos = (int)(a.params[kParamPrefillPos] + local);
+        } else {
+            pos = (int)(a.pos_offset + local);
+        }
+    }
+    if (pos < 0 || pos >= a.max_seq) row = -1;  // outside the table: never read
+}
+
 // `tables` is passed on its own, read-only and unaliased, so the page-id loads of the
 // tile loop compile to scalar loads (lgkmcnt) that never wait on the in-flight tiles.
 // KB: LDS ring depth in key tiles (4 or 6): KB / 2 - 1 pairs of tiles load ahead.
@@ -146,26 +174,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
     // ---- rows of this tile: (packed row, owner, absolute position); -1 = none
     int row = -1, owner = 0, pos = 0;
     if (tid < R) {
-        const int64_t local = (int64_t)blockIdx.y * R + tid;
-        if (a.mode == kSegments) {
-            const int32_t* seg = a.segments + 4 * (int64_t)blockIdx.z;
-            if (local < seg[1]) {
-                row = (int)(seg[0] + local);
-                pos = (int)(seg[2] + local);
-                owner = seg[3];
-            }
-        } else if (local < a.rows) {
-            row = (int)local;
-            if (a.mode == kOwners) {
-                owner = a.owners[local];
-                pos = a.positions[local];
-            } else if (a.mode == kParams) {
-                pos = (int)(a.params[kParamPrefillPos] + local);
-            } else {
-                pos = (int)(a.pos_offset + local);
-            }
-        }
-        if (pos < 0 || pos >= a.max_seq) row = -1;  // outside the table: never read
+        tile_row(a, (int64_t)blockIdx.y * R + tid, row, owner, pos);
         s_row[tid] = row;
         s_owner[tid] = owner;
         s_pos[tid] = pos;
@@ -514,6 +523,254 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
     }
 }
 
+// ---------------------------------------------------------------- register-direct form
+//
+// Workgroup = 16 query rows of one head; its 8 waves split the causal key range, wave w
+// taking the 64-key tiles w, w + 8, ... Each wave loads its tile's K rows and V^T page
+// slices from the pool straight into MFMA operand registers (the decode kernel's operand
+// layout): no LDS staging and no barrier per tile, so the longest row block costs one
+// tile's chain per wave instead of one per tile. The 8 online-softmax states merge
+// through LDS once at the end. K/V tiles are read once per 16-row block (from L2 after
+// the first), against once per 64 rows in the LDS form: the direct form trades L2 reads
+// for parallelism, which pays while the LDS form's grid would leave CUs idle.
+constexpr int kDirectWaves = 8;
+
+template <bool QF32>
+__global__ __launch_bounds__(kDirectWaves * 64) void prefill_direct_kernel(
+    PrefillArgs a, const int32_t* __restrict__ tables) {
+    __shared__ int s_owner[16];
+    __shared__ int s_pos[16];
+    __shared__ int s_row[16];
+    __shared__ uint64_t s_mask;
+    __shared__ float s_m[kDirectWaves][16];
+    __shared__ float s_l[kDirectWaves][16];
+    __shared__ float4_t s_acc[kDirectWaves][4][64];
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int col = lane & 15;
+    const int grp = lane >> 4;
+    const int h = blockIdx.x;
+    const int g = h / a.n_rep;
+
+    int row = -1, owner = 0, pos = 0;
+    if (tid < 16) {
+        tile_row(a, (int64_t)blockIdx.y * 16 + tid, row, owner, pos);
+        s_row[tid] = row;
+        s_owner[tid] = owner;
+        s_pos[tid] = pos;
+    }
+    const uint64_t vmask = __ballot(tid < 16 && row >= 0);
+    if (wave == 0 && lane == 0) s_mask = vmask;
+    __syncthreads();
+    const uint64_t mask = s_mask;
+    if (mask == 0) return;  // uniform: no row of this tile is valid
+
+    const int my_row = s_row[col];
+    const int my_pos = s_pos[col];
+    const int64_t ld_q = (int64_t)a.n_head * kHeadDim;
+    half8_t qh0 = {}, qh1 = {}, ql0 = {}, ql1 = {};
+    if (my_row >= 0) {
+        const int64_t off = (int64_t)my_row * ld_q + (int64_t)h * kHeadDim + 8 * grp;
+        if constexpr (QF32) {
+            const float* qp = static_cast<const float*>(a.q) + off;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x0 = qp[j], x1 = qp[32 + j];
+                qh0[j] = (half_t)x0;
+                qh1[j] = (half_t)x1;
+                ql0[j] = (half_t)(x0 - (float)qh0[j]);
+                ql1[j] = (half_t)(x1 - (float)qh1[j]);
+            }
+        } else {
+            const half_t* qp = static_cast<const half_t*>(a.q) + off;
+            qh0 = *reinterpret_cast<const half8_t*>(qp);
+            qh1 = *reinterpret_cast<const half8_t*>(qp + 32);
+        }
+    }
+
+    float m = -INFINITY, l = 0.0f;
+    float4_t acc[4] = {};
+    const int kv_dim = a.addr.kv_dim;
+    const int first_valid = __builtin_ctzll(mask);
+    const int last_valid = 63 - __builtin_clzll(mask);
+    int r0 = a.mode == kOwners ? 0 : first_valid;
+    while (r0 < 16) {
+        int r1, owner_r, hist_end, wave_last;
+        if (a.mode != kOwners) {
+            r1 = last_valid + 1;
+            owner_r = s_owner[r0];
+            hist_end = s_pos[last_valid] + 1;
+            wave_last = s_pos[last_valid];
+        } else {
+            while (r0 < 16 && s_row[r0] < 0) ++r0;
+            if (r0 >= 16) break;
+            owner_r = s_owner[r0];
+            r1 = r0 + 1;
+            while (r1 < 16 && s_row[r1] >= 0 && s_owner[r1] == owner_r) ++r1;
+            hist_end = 0;
+            for (int r = r0; r < r1; ++r) hist_end = max(hist_end, s_pos[r] + 1);
+            wave_last = hist_end - 1;
+        }
+        r0 = __builtin_amdgcn_readfirstlane(r0);
+        r1 = __builtin_amdgcn_readfirstlane(r1);
+        owner_r = __builtin_amdgcn_readfirstlane(owner_r);
+        hist_end = __builtin_amdgcn_readfirstlane(hist_end);
+        wave_last = __builtin_amdgcn_readfirstlane(wave_last);
+        const bool in_run = my_row >= 0 && col >= r0 && col < r1;
+
+        typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+        const_i32_ptr table = tables ? (const_i32_ptr)(tables + (int64_t)owner_r * a.table_stride)
+                                     : nullptr;
+        const int n_tiles = (hist_end + kKeyTile - 1) / kKeyTile;
+        const int last_page = (hist_end - 1) >> kPageShift;
+
+        for (int t = wave; t < n_tiles; t += kDirectWaves) {
+            const int kbase = t * kKeyTile;
+            if (wave_last < kbase) break;  // later tiles lie above the diagonal too
+            int64_t pg[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int idx = min(t * 4 + j, last_page);  // clamped: in bounds, masked later
+                pg[j] = block_base(a.addr, table ? (int64_t)table[idx] : (int64_t)idx);
+            }
+            // K operand of key block kb: key 16 kb + col (page kb of the tile), channels
+            // 8 grp .. +7 and 32 + 8 grp .. +7; V^T operand of channel 16 db + col: slots
+            // 4 grp .. +3 of pages 2 ks and 2 ks + 1 (keys 32 ks + 4 grp .. and +16).
+            half8_t ka[4][2];
+            half4_t va[4][2][2];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const half_t* kp = a.k_pool + pg[kb] + (int64_t)col * kv_dim + g * kHeadDim + 8 * grp;
+                ka[kb][0] = *reinterpret_cast<const half8_t*>(kp);
+                ka[kb][1] = *reinterpret_cast<const half8_t*>(kp + 32);
+            }
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) {
+                        const half_t* vp = a.v_pool + pg[2 * ks + hf] +
+                                           (int64_t)(g * kHeadDim + 16 * db + col) * kPageTokens +
+                                           4 * grp;
+                        va[db][ks][hf] = *reinterpret_cast<const half4_t*>(vp);
+                    }
+
+            float4_t st[4];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                float4_t c = {0.f, 0.f, 0.f, 0.f};
+                c = mfma_16x16x32(ka[kb][0], qh0, c);
+                c = mfma_16x16x32(ka[kb][1], qh1, c);
+                if constexpr (QF32) {
+                    c = mfma_16x16x32(ka[kb][0], ql0, c);
+                    c = mfma_16x16x32(ka[kb][1], ql1, c);
+                }
+                st[kb] = c;
+            }
+            const bool full = __all(in_run && my_pos >= kbase + kKeyTile - 1);
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = kbase + 16 * kb + 4 * grp + r;
+                    const float x = st[kb][r] * a.scale_log2;
+                    st[kb][r] = (full || (in_run && key <= my_pos)) ? x : -INFINITY;
+                }
+            float tm = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) tm = fmaxf(tm, st[kb][r]);
+            tm = max_xor32(max_xor16(tm));
+            const bool grow = tm > m + kLazyLog2;
+            if (__any(grow)) {
+                const float alpha = grow ? fast_exp2(m - tm) : 1.0f;
+                if (grow) m = tm;
+                l *= alpha;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) acc[db] = acc[db] * alpha;
+            }
+            const float mu = (m == -INFINITY) ? 0.0f : m;
+            half8_t pb[2], pl[2];
+            float ps = 0.0f;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                float pf[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    pf[r] = fast_exp2(st[kb][r] - mu);
+                    ps += pf[r];
+                }
+                const half4_t hh = split_hi(pf);
+                const half4_t lo = split_lo(pf, hh);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    pb[kb >> 1][(kb & 1) * 4 + r] = hh[r];
+                    pl[kb >> 1][(kb & 1) * 4 + r] = lo[r];
+                }
+            }
+            l += ps;
+            const bool tail = kbase + kKeyTile > hist_end;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    half4_t v0 = va[db][ks][0], v1 = va[db][ks][1];
+                    if (tail) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if (kbase + 32 * ks + 4 * grp + r >= hist_end) v0[r] = (half_t)0.0f;
+                            if (kbase + 32 * ks + 16 + 4 * grp + r >= hist_end) v1[r] = (half_t)0.0f;
+                        }
+                    }
+                    const half8_t vv = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                    acc[db] = mfma_16x16x32(vv, pb[ks], acc[db]);
+                    acc[db] = mfma_16x16x32(vv, pl[ks], acc[db]);
+                }
+        }
+        if (a.mode != kOwners) break;  // a single run
+        r0 = r1;
+    }
+
+    // ---- merge the 8 waves' states (per column: m, l summed over the lane groups)
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (grp == 0) {
+        s_m[wave][col] = m;
+        s_l[wave][col] = l;
+    }
+#pragma unroll
+    for (int db = 0; db < 4; ++db) s_acc[wave][db][lane] = acc[db];
+    __syncthreads();
+    if (wave >= 4 || my_row < 0) return;
+    const int db = wave;  // waves 0..3 each finish one 16-dim block
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDirectWaves; ++w) M = fmaxf(M, s_m[w][col]);
+    float L = 0.0f;
+    float4_t o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kDirectWaves; ++w) {
+        const float lw = s_l[w][col];
+        if (lw > 0.0f) {
+            const float wt = fast_exp2(s_m[w][col] - M);
+            L += lw * wt;
+            o += s_acc[w][db][lane] * wt;
+        }
+    }
+    o = o * (1.0f / L);
+    const int64_t off = (int64_t)my_row * ld_q + (int64_t)h * kHeadDim + 16 * db + 4 * grp;
+    if (a.out_f16) {
+        const half4_t hv = {(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
+        *reinterpret_cast<half4_t*>(static_cast<half_t*>(a.out) + off) = hv;
+    } else {
+        *reinterpret_cast<float4_t*>(static_cast<float*>(a.out) + off) = o;
+    }
+}
+
 int heads_per_wg(int n_rep) { return (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1; }
 
 template <int HPW, int QB, bool QF32>
@@ -533,18 +790,53 @@ void launch_hq(const PrefillArgs& a, bool q_f32, int kb, dim3 grid, hipStream_t 
 }
 
 // tile_rows_total: rows spanned by grid.y (max_chunk or rows); z: requests.
-int launch_prefill(const PrefillArgs& a, int64_t tile_rows_total, int64_t z, bool q_f32,
-                   hipStream_t stream, const char* what) {
-    const int hpw = heads_per_wg(a.n_rep);
-    const int64_t gx = (int64_t)a.n_kv_head * (a.n_rep / hpw);
-    const int rs = 4 / hpw;
+// The LDS form's grid for these rows: (kv-head groups, row tiles of 64 * QB / HPW rows, z).
+struct LdsGrid {
+    int hpw, qb;
+    int64_t gx, gy;
+};
+
+LdsGrid lds_grid(const PrefillArgs& a, int64_t tile_rows_total, int64_t z) {
+    LdsGrid lg;
+    lg.hpw = heads_per_wg(a.n_rep);
+    lg.gx = (int64_t)a.n_kv_head * (a.n_rep / lg.hpw);
+    const int rs = 4 / lg.hpw;
     auto tiles = [&](int qb) { return (tile_rows_total + rs * 16 * qb - 1) / (rs * 16 * qb); };
-    int qb = (gx * tiles(2) * z * 4 >= 2048) ? 2 : 1;
+    lg.qb = (lg.gx * tiles(2) * z * 4 >= 2048) ? 2 : 1;
     if (const char* env = std::getenv("CRUCIBLE_PREFILL_QB")) {
         const int v = std::atoi(env);
-        if (v == 1 || v == 2) qb = v;
+        if (v == 1 || v == 2) lg.qb = v;
     }
-    const int64_t gy = tiles(qb);
+    lg.gy = tiles(lg.qb);
+    return lg;
+}
+
+constexpr int64_t kCUs = 256;  // MI355X
+
+int launch_prefill(const PrefillArgs& a, int64_t tile_rows_total, int64_t z, bool q_f32,
+                   hipStream_t stream, const char* what) {
+    const LdsGrid lg = lds_grid(a, tile_rows_total, z);
+    // The register-direct form when the LDS form would leave CUs without a workgroup
+    // (short prompts: config 1 is 96 workgroups); the LDS form, which reads each K/V tile
+    // once per 64 rows instead of once per 16, when its grid fills the chip.
+    int direct = lg.gx * lg.gy * z < kCUs;
+    if (const char* env = std::getenv("CRUCIBLE_PREFILL_DIRECT")) direct = std::atoi(env) != 0;
+    if (direct) {
+        const int64_t gy = (tile_rows_total + 15) / 16;
+        CRUCIBLE_CHECK(a.n_head <= INT32_MAX && gy <= 65535 && z <= 65535, CRUCIBLE_ERR_INVALID,
+                       "%s: grid (%d, %lld, %lld) too large", what, a.n_head, (long long)gy,
+                       (long long)z);
+        const dim3 grid((unsigned)a.n_head, (unsigned)gy, (unsigned)z);
+        if (q_f32)
+            hipLaunchKernelGGL((prefill_direct_kernel<true>), grid, dim3(kDirectWaves * 64), 0,
+                               stream, a, a.tables);
+        else
+            hipLaunchKernelGGL((prefill_direct_kernel<false>), grid, dim3(kDirectWaves * 64), 0,
+                               stream, a, a.tables);
+        return fail_launch(what);
+    }
+    const int hpw = lg.hpw, qb = lg.qb;
+    const int64_t gx = lg.gx, gy = lg.gy;
     // A grid that fits the chip at one workgroup per CU affords the deeper ring (96 KiB
     // of LDS); larger grids keep two workgroups per CU.
     int kb = (gx * gy * z <= 256) ? 6 : 4;

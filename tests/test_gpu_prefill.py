@@ -6,7 +6,8 @@ through every prefill entry point (segments, owners/positions, params, contiguou
 compared with the f64 oracle on every element (bar: max-abs 2e-3). Structural contracts are
 exact: future-page poison leaves outputs bit-identical (:597-632), descriptor composition,
 order and page reuse leave each request's bits unchanged (:639-682), and output rows outside
-the written range keep their sentinel (:23, :271-287).
+the written range keep their sentinel (:23, :271-287). Both prefill kernels (LDS-tiled and
+register-direct) run every test.
 """
 import numpy as np
 import pytest
@@ -18,6 +19,14 @@ import oracle
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
+
+
+@pytest.fixture(autouse=True, params=["lds", "direct"])
+def prefill_form(request, monkeypatch):
+    """Every test runs through both prefill kernels: the LDS-tiled form and the
+    register-direct form (the library picks one by grid size; the variable forces it)."""
+    monkeypatch.setenv("CRUCIBLE_PREFILL_DIRECT", "1" if request.param == "direct" else "0")
+    return request.param
 
 
 def _dev(a, dev):

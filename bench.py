@@ -223,8 +223,12 @@ def flush_llc(dev):
 
 # ---------------------------------------------------------------- prefill workloads
 
-def bench_prefill(gpu, dev, cfg, launches: int = 50):
-    """Time the segment-form prefill kernel (gpu.rs:1606-1751 path) on config 1 or 4."""
+def bench_prefill(gpu, dev, cfg, launches: int = 50, q_dtype=None):
+    """Time the segment-form prefill kernel (gpu.rs:1606-1751 path) on config 1 or 4:
+    `launches` back-to-back launches replayed from one HIP graph (us_per_launch, the
+    figure TFLOP/s uses, timed like the decode step), and eager launches each bracketed by
+    events (us_per_launch_eager). The query is fp16 (the kernel's MFMA input type) unless
+    q_dtype says otherwise."""
     import numpy as np
     import torch
 
@@ -237,7 +241,7 @@ def bench_prefill(gpu, dev, cfg, launches: int = 50):
     stride = cfg.tables.shape[1]
     k_pool = W.device_normal((pool_elems(cfg.n_pages, 1, kv_dim),), torch.float16, cfg.seed + 1, dev)
     v_pool = W.device_normal((pool_elems(cfg.n_pages, 1, kv_dim),), torch.float16, cfg.seed + 2, dev)
-    q = W.device_normal((rows, cfg.n_head * 64), torch.float16, cfg.seed + 3, dev)
+    q = W.device_normal((rows, cfg.n_head * 64), q_dtype or torch.float16, cfg.seed + 3, dev)
     out = torch.empty((rows, cfg.n_head * 64), dtype=torch.float32, device=dev)
     seg, max_chunk = segments_from_cu_seqlens(cfg.cu_seqlens)
     d_seg = torch.from_numpy(np.ascontiguousarray(seg)).to(dev)
@@ -252,6 +256,7 @@ def bench_prefill(gpu, dev, cfg, launches: int = 50):
         run()
     torch.cuda.synchronize(dev)
     stream = torch.cuda.current_stream(dev)
+    # eager: every launch bracketed by its own events (includes the launch path)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(launches)]
     for a, b in ev:
@@ -260,11 +265,34 @@ def bench_prefill(gpu, dev, cfg, launches: int = 50):
         b.record(stream)
     torch.cuda.synchronize(dev)
     ms = sorted(a.elapsed_time(b) for a, b in ev)
-    avg = sum(ms) / len(ms)
+    eager = sum(ms) / len(ms)
+    # graph replay of `launches` back-to-back launches, as the decode step is timed
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        run()
+    stream.wait_stream(side)
+    torch.cuda.synchronize(dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(launches):
+            run()
+    g.replay()
+    torch.cuda.synchronize(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(4):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    avg = e0.elapsed_time(e1) / (4 * launches)
+    del g
     tflops = cfg.flops() / (avg * 1e-3) / 1e12
     return {"workload": cfg.name, "n_head": cfg.n_head, "n_kv_head": cfg.n_kv_head,
+            "q_dtype": str(q.dtype).replace("torch.", ""),
             "seq_lens": [int(x) for x in cfg.seq_lens], "flops": cfg.flops(),
-            "us_per_launch": round(avg * 1e3, 3), "us_median": round(ms[len(ms) // 2] * 1e3, 3),
+            "us_per_launch": round(avg * 1e3, 3),
+            "us_per_launch_eager": round(eager * 1e3, 3), "us_median_eager": round(ms[len(ms) // 2] * 1e3, 3),
             "tflops": round(tflops, 3), "frac_of_mfma_f16_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 5)}
 
 

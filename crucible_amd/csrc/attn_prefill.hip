@@ -535,8 +535,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
 // for parallelism, which pays while the LDS form's grid would leave CUs idle.
 constexpr int kDirectWaves = 8;
 
+// At most 128 VGPRs (4 waves per SIMD): two 8-wave workgroups per CU, so a config-1 grid
+// (384 workgroups) is resident at once instead of in two rounds.
 template <bool QF32>
-__global__ __launch_bounds__(kDirectWaves * 64) void prefill_direct_kernel(
+__global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
     PrefillArgs a, const int32_t* __restrict__ tables) {
     __shared__ int s_owner[16];
     __shared__ int s_pos[16];

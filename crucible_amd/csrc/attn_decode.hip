@@ -79,6 +79,12 @@ struct DecodeArgs {
     int n_splits;
     int out_f16;
     float scale_log2;            // (1/sqrt(64)) * log2(e)
+    // fused RoPE (the qkv entry point): rotate q and the appended K row at positions[b]
+    const float* rope_cos;       // [rope_max_pos][32]
+    const float* rope_sin;
+    int rope_max_pos;
+    int kv_new_stride;           // elements between k_new (and v_new) rows
+    int out_row_stride;          // elements between output rows (n_head * 64)
 };
 
 __device__ __forceinline__ int request_len(const DecodeArgs& a, int b) {
@@ -150,7 +156,39 @@ __device__ __forceinline__ void combine_partials(const DecodeArgs& a, int b, int
         }
         M = mx;
     }
-    store_out4(a, (int64_t)b * a.q_row_stride + (int64_t)hh * kHeadDim + 4 * d4, o * (1.0f / L));
+    store_out4(a, (int64_t)b * a.out_row_stride + (int64_t)hh * kHeadDim + 4 * d4, o * (1.0f / L));
+}
+
+// RoPE of one (i, i + 32) pair (ops.rs:124-135): lo*c - hi*s, lo*s + hi*c, each product
+// and difference rounded on its own as in the reference (no contraction).
+__device__ __forceinline__ void rope_pair(float& lo, float& hi, float c, float s) {
+#pragma clang fp contract(off)
+    const float a = lo * c - hi * s;
+    const float b = lo * s + hi * c;
+    lo = a;
+    hi = b;
+}
+
+// cos / sin of channels 8*grp .. 8*grp+7 at position pos: the pairs this lane's query and
+// K operand slots hold (channel d and d + 32 sit in one lane).
+struct RopeCS {
+    float c[8], s[8];
+};
+
+__device__ __forceinline__ RopeCS load_rope(const DecodeArgs& a, int pos, int grp) {
+    RopeCS r;
+    const int p = min(max(pos, 0), a.rope_max_pos - 1);
+    const float4_t* cp = reinterpret_cast<const float4_t*>(a.rope_cos + (int64_t)p * 32 + 8 * grp);
+    const float4_t* sp = reinterpret_cast<const float4_t*>(a.rope_sin + (int64_t)p * 32 + 8 * grp);
+    const float4_t c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        r.c[j] = c0[j];
+        r.c[4 + j] = c1[j];
+        r.s[j] = s0[j];
+        r.s[4 + j] = s1[j];
+    }
+    return r;
 }
 
 // New K/V values of the appended row for this lane's operand slots, rounded to fp16
@@ -164,10 +202,11 @@ struct NewRow {
 
 // One uniform branch on the source dtype, then every load of the row is issued back to
 // back (vector loads for K, four scalar loads for V) before any conversion waits on them.
+template <bool ROPE>
 __device__ __forceinline__ NewRow load_new_row(const DecodeArgs& a, int b, int g, int col,
-                                               int grp, int slot) {
+                                               int grp, int slot, const RopeCS& rc) {
     NewRow r{};
-    const int64_t row = (int64_t)b * a.addr.kv_dim + g * kHeadDim;
+    const int64_t row = (int64_t)b * a.kv_new_stride + g * kHeadDim;
     const bool k_lane = col == slot;
     const bool v_lane = grp == (slot >> 2);
     if (a.kv_new_f16) {
@@ -195,6 +234,18 @@ __device__ __forceinline__ NewRow load_new_row(const DecodeArgs& a, int b, int g
         if (v_lane) {
 #pragma unroll
             for (int db = 0; db < 4; ++db) vf[db] = v[16 * db + col];
+        }
+        if constexpr (ROPE) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float lo0 = k4[0][j], hi0 = k4[2][j], lo1 = k4[1][j], hi1 = k4[3][j];
+                rope_pair(lo0, hi0, rc.c[j], rc.s[j]);
+                rope_pair(lo1, hi1, rc.c[4 + j], rc.s[4 + j]);
+                k4[0][j] = lo0;
+                k4[2][j] = hi0;
+                k4[1][j] = lo1;
+                k4[3][j] = hi1;
+            }
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -225,8 +276,10 @@ __device__ __forceinline__ void store_new_row(const DecodeArgs& a, const NewRow&
 }
 
 // RMAJOR: grid (kv head, request, split) instead of (split, kv head, request).
-template <int PAGES, int WAVES, bool QF32, bool APPEND, bool PAGED, bool RMAJOR>
+// ROPE (with QF32 and APPEND): rotate q and the appended K row at the append position.
+template <int PAGES, int WAVES, bool QF32, bool APPEND, bool PAGED, bool RMAJOR, bool ROPE>
 __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
+    static_assert(!ROPE || (QF32 && APPEND), "RoPE is fused for f32 rows with the append");
     __shared__ float4_t s_acc[WAVES][16][17];  // [wave][col][dim/4], padded
     __shared__ float s_m[WAVES][16];
     __shared__ float s_l[WAVES][16];
@@ -250,9 +303,17 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     // first: its address does not depend on anything loaded.
     const int h = g * a.n_rep + col;
     half8_t qh0 = {}, qh1 = {}, ql0 = {}, ql1 = {};
+    float qx0[8] = {}, qx1[8] = {};  // ROPE: f32 query channels d and d + 32, rotated later
     if (col < a.n_rep) {
         const int64_t qoff = (int64_t)b * a.q_row_stride + (int64_t)h * kHeadDim + 8 * grp;
-        if constexpr (QF32) {
+        if constexpr (ROPE) {
+            const float* qp = static_cast<const float*>(a.q) + qoff;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                qx0[j] = qp[j];
+                qx1[j] = qp[32 + j];
+            }
+        } else if constexpr (QF32) {
             const float* qp = static_cast<const float*>(a.q) + qoff;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -300,10 +361,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     const int aidx = (apos >= 0 && (apos >> kPageShift) >= wp0 && (apos >> kPageShift) < wp0 + PAGES)
                          ? (apos >> kPageShift) - wp0 : -1;
     const int aslot = apos & kPageMask;
+    // RoPE of this request's position: cos/sin of the lane's channel pairs (the query and
+    // the appended K row use the same ones)
+    RopeCS rc{};
+    if constexpr (ROPE) rc = load_rope(a, pos, grp);
     if (!attend) {
         // append only: the row lies past the attended length
         if (aidx >= 0) {
-            const NewRow nr = load_new_row(a, b, g, col, grp, aslot);
+            const NewRow nr = load_new_row<ROPE>(a, b, g, col, grp, aslot, rc);
 #pragma unroll
             for (int i = 0; i < PAGES; ++i)
                 if (i == aidx) store_new_row(a, nr, block_base(a.addr, page[i]), g, col, grp, aslot);
@@ -330,10 +395,21 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
                 va[i][db] = *reinterpret_cast<const half4_t*>(vp + db * 16 * kPageTokens);
         }
     }
+    if constexpr (ROPE) {
+        // rotate the query, then split it into fp16 hi + lo as the plain f32 path does
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            rope_pair(qx0[j], qx1[j], rc.c[j], rc.s[j]);
+            qh0[j] = (half_t)qx0[j];
+            qh1[j] = (half_t)qx1[j];
+            ql0[j] = (half_t)(qx0[j] - (float)qh0[j]);
+            ql1[j] = (half_t)(qx1[j] - (float)qh1[j]);
+        }
+    }
     if (APPEND && aidx >= 0) {
         // The appended row replaces what the page held in this wave's operands and is
         // written to the page for later steps.
-        const NewRow nr = load_new_row(a, b, g, col, grp, aslot);
+        const NewRow nr = load_new_row<ROPE>(a, b, g, col, grp, aslot, rc);
 #pragma unroll
         for (int i = 0; i < PAGES; ++i) {
             if (i == aidx) {
@@ -438,7 +514,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
             }
         }
         if (n_active == 1) {
-            store_out4(a, (int64_t)b * a.q_row_stride + (int64_t)hh * kHeadDim + 4 * d4, o * (1.0f / L));
+            store_out4(a, (int64_t)b * a.out_row_stride + (int64_t)hh * kHeadDim + 4 * d4, o * (1.0f / L));
         } else {
             const int64_t slot = ((int64_t)b * a.n_head + hh) * a.n_splits + s;
             __builtin_amdgcn_raw_buffer_store_b128(
@@ -508,16 +584,16 @@ DecodeShape decode_shape(int64_t batch, int64_t n_kv_head, int64_t max_pages) {
     return sh;
 }
 
-template <bool QF32, bool APPEND, bool PAGED>
+template <bool QF32, bool APPEND, bool PAGED, bool ROPE = false>
 bool launch_shape(const DecodeArgs& a, DecodeShape sh, bool rmajor, dim3 grid,
                   hipStream_t stream) {
 #define CRUCIBLE_DECODE_CASE(P, W)                                                             \
     if (sh.pages == P && sh.waves == W) {                                                       \
         if (rmajor)                                                                             \
-            hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, true>), grid,          \
+            hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, true, ROPE>), grid,    \
                                dim3(W * 64), 0, stream, a);                                     \
         else                                                                                    \
-            hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, false>), grid,         \
+            hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, false, ROPE>), grid,   \
                                dim3(W * 64), 0, stream, a);                                     \
         return true;                                                                            \
     }
@@ -543,7 +619,9 @@ int launch_decode(DecodeArgs a, DecodeShape sh, bool q_f32, hipStream_t stream,
     const dim3 grid = rmajor ? dim3((unsigned)a.n_kv_head, (unsigned)a.batch, (unsigned)a.n_splits)
                              : dim3((unsigned)a.n_splits, (unsigned)a.n_kv_head, (unsigned)a.batch);
     bool launched;
-    if (a.positions)  // the fused append exists for paged pools only
+    if (a.rope_cos)  // fused RoPE: f32 qkv rows with the append
+        launched = launch_shape<true, true, true, true>(a, sh, rmajor, grid, stream);
+    else if (a.positions)  // the fused append exists for paged pools only
         launched = q_f32 ? launch_shape<true, true, true>(a, sh, rmajor, grid, stream)
                          : launch_shape<false, true, true>(a, sh, rmajor, grid, stream);
     else if (a.tables)
@@ -613,6 +691,7 @@ DecodeArgs common_args(const void* q, const void* k, const void* v, void* out, i
     a.v_pool = static_cast<half_t*>(const_cast<void*>(v));
     a.out = out;
     a.q_row_stride = (int32_t)(n_head * kHeadDim);
+    a.out_row_stride = (int32_t)(n_head * kHeadDim);
     a.batch = (int)batch;
     a.n_head = (int)n_head;
     a.n_kv_head = (int)n_kv_head;
@@ -733,12 +812,67 @@ extern "C" int crucible_attention_decode_paged_append(
     a.k_new = k_new;
     a.v_new = v_new;
     a.kv_new_f16 = kv_dtype == CRUCIBLE_F16;
+    a.kv_new_stride = (int32_t)kv_dim;
     a.addr.kv_dim = (int32_t)kv_dim;
     a.addr.page_stride = n_layer * kPageTokens * kv_dim;
     a.addr.layer_off = layer * kPageTokens * kv_dim;
     a.table_stride = (int32_t)table_stride;
     return decode_with_workspace(a, q_dtype == CRUCIBLE_F32, workspace, workspace_bytes, stream,
                                  what);
+}
+
+extern "C" int crucible_attention_decode_qkv_paged_append(
+    const float* qkv, int64_t qkv_row_stride, const float* rope_cos, const float* rope_sin,
+    int64_t rope_max_pos, void* k_pool, void* v_pool, void* out, int out_dtype,
+    const int32_t* page_tables, const int32_t* positions, const int32_t* seq_lens, int64_t batch,
+    int64_t n_head, int64_t n_kv_head, int64_t head_dim, int64_t table_stride, int64_t n_layer,
+    int64_t layer, int64_t kv_dim, int64_t max_seq, void* workspace, size_t workspace_bytes,
+    crucible_stream_t stream) {
+    const char* what = "attention_decode_qkv_paged_append";
+    CRUCIBLE_CHECK(dtype_ok(out_dtype), CRUCIBLE_ERR_INVALID, "%s: bad dtype", what);
+    if (int rc = check_geometry(what, n_head, n_kv_head, head_dim, kv_dim)) return rc;
+    CRUCIBLE_CHECK(batch >= 0 && batch <= INT32_MAX, CRUCIBLE_ERR_INVALID, "%s: batch %lld",
+                   what, (long long)batch);
+    if (batch == 0) return CRUCIBLE_OK;
+    CRUCIBLE_CHECK(qkv && k_pool && v_pool && out && page_tables && positions && seq_lens,
+                   CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
+    CRUCIBLE_CHECK(qkv_row_stride >= n_head * head_dim + 2 * kv_dim && qkv_row_stride % 4 == 0 &&
+                       qkv_row_stride <= INT32_MAX,
+                   CRUCIBLE_ERR_INVALID,
+                   "%s: qkv_row_stride %lld must hold q, k and v and be a multiple of 4", what,
+                   (long long)qkv_row_stride);
+    CRUCIBLE_CHECK(n_layer > 0 && layer >= 0 && layer < n_layer, CRUCIBLE_ERR_INVALID,
+                   "%s: layer %lld outside n_layer %lld", what, (long long)layer,
+                   (long long)n_layer);
+    CRUCIBLE_CHECK(table_stride > 0 && table_stride <= INT32_MAX && max_seq > 0 &&
+                       max_seq <= table_stride * kPageTokens && max_seq <= INT32_MAX,
+                   CRUCIBLE_ERR_INVALID, "%s: max_seq %lld must be in 1..table_stride*16", what,
+                   (long long)max_seq);
+    CRUCIBLE_CHECK((rope_cos == nullptr) == (rope_sin == nullptr), CRUCIBLE_ERR_INVALID,
+                   "%s: rope_cos and rope_sin go together", what);
+    CRUCIBLE_CHECK(!rope_cos || (rope_max_pos >= max_seq && rope_max_pos <= INT32_MAX &&
+                                 aligned16(rope_cos) && aligned16(rope_sin)),
+                   CRUCIBLE_ERR_INVALID,
+                   "%s: rope tables must cover max_seq positions (16-byte aligned)", what);
+    DecodeArgs a = common_args(qkv, k_pool, v_pool, out, out_dtype, batch, n_head, n_kv_head,
+                               max_seq);
+    a.q_row_stride = (int32_t)qkv_row_stride;
+    a.tables = page_tables;
+    a.lens = seq_lens;
+    a.lens_stride = 1;
+    a.positions = positions;
+    a.k_new = qkv + n_head * head_dim;
+    a.v_new = qkv + n_head * head_dim + kv_dim;
+    a.kv_new_f16 = 0;
+    a.kv_new_stride = (int32_t)qkv_row_stride;
+    a.rope_cos = rope_cos;
+    a.rope_sin = rope_sin;
+    a.rope_max_pos = (int)rope_max_pos;
+    a.addr.kv_dim = (int32_t)kv_dim;
+    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
+    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    a.table_stride = (int32_t)table_stride;
+    return decode_with_workspace(a, true, workspace, workspace_bytes, stream, what);
 }
 
 extern "C" int crucible_attention_decode(const void* q, int q_dtype, const void* k_cache,

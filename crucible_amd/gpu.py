@@ -169,6 +169,33 @@ class Gpu:
             n_layer, layer, kv_dim, max_seq, _ptr(ws), ws.numel() * ws.element_size(),
             self._stream()))
 
+    def attention_decode_qkv_paged_append(self, qkv, rope_cos, rope_sin, k_pool, v_pool, out,
+                                          page_tables, positions, seq_lens, batch, n_head,
+                                          n_kv_head, head_dim, table_stride, n_layer, layer,
+                                          kv_dim, max_seq, workspace=None):
+        """The fused step fed from the fused q/k/v rows, with RoPE of q and k at positions[b]
+        (rope tables [max_pos][32] f32, or None for no rotation)."""
+        _need(qkv, "qkv", dtype=torch.float32)
+        row_stride = qkv.shape[1]
+        _need(qkv, "qkv", numel=batch * row_stride)
+        _need(out, "out", numel=batch * n_head * head_dim)
+        _need(k_pool, "k_pool", dtype=torch.float16)
+        _need(v_pool, "v_pool", dtype=torch.float16)
+        _need(page_tables, "page_tables", dtype=torch.int32, numel=batch * table_stride)
+        _need(positions, "positions", dtype=torch.int32, numel=batch)
+        _need(seq_lens, "seq_lens", dtype=torch.int32, numel=batch)
+        max_pos = 0
+        if rope_cos is not None:
+            _need(rope_cos, "rope_cos", dtype=torch.float32)
+            _need(rope_sin, "rope_sin", dtype=torch.float32, numel=rope_cos.numel())
+            max_pos = rope_cos.shape[0]
+        ws = workspace if workspace is not None else self.workspace(batch, n_head, max_seq)
+        _lib.check(self.lib.crucible_attention_decode_qkv_paged_append(
+            _ptr(qkv), row_stride, _ptr(rope_cos), _ptr(rope_sin), max_pos, _ptr(k_pool),
+            _ptr(v_pool), _ptr(out), _dtype(out, "out"), _ptr(page_tables), _ptr(positions),
+            _ptr(seq_lens), batch, n_head, n_kv_head, head_dim, table_stride, n_layer, layer,
+            kv_dim, max_seq, _ptr(ws), ws.numel() * ws.element_size(), self._stream()))
+
     def attention_decode(self, q, k_cache, v_cache, out, n_head, n_kv_head, head_dim, params,
                          max_seq, cache_stride, layer_base, workspace=None):
         """gpu.rs:762-817: contiguous cache, length params[3]."""

@@ -20,9 +20,10 @@ Projections run either as the reference's matvec contract (ops.rs:17-32: f32 ope
 f64 accumulation, f32 result; `precision="reference"`) or as plain f32 GEMMs
 (`precision="f32"`). In reference precision the decode step is this library's kernels
 end to end: f64-MFMA projections with RMSNorm, residual and SwiGLU fused
-(crucible_linear_f64acc, crucible_linear_swiglu_f64acc), RoPE + q/k/v split, the fused
-append + attention, RMSNorm and the vocabulary projection, then the device argmax. The
-prefill's projections are torch f64 GEMMs (the same contract) over the packed rows.
+(crucible_linear_f64acc, crucible_linear_swiglu_f64acc), RoPE of q and k fused with both
+appends and the attention (crucible_attention_decode_qkv_paged_append), RMSNorm and the
+vocabulary projection, then the device argmax. The prefill's projections are torch f64
+GEMMs (the same contract) over the packed rows.
 
 Paging is the reference allocator (crucible_amd.paged): every request reserves the
 pages it needs through its last generated token up front (prefill.rs:160-172), so the
@@ -288,7 +289,7 @@ class GpuModel:
         self._advance(st)
 
     def _decode_step_native(self, st):
-        """The step as this library's kernels (reference arithmetic), 8 launches a layer."""
+        """The step as this library's kernels (reference arithmetic), 5 launches a layer."""
         cfg, gpu = self.cfg, self.gpu
         b = st["batch"]
         eps = float(np.float32(cfg.norm_eps))
@@ -296,14 +297,14 @@ class GpuModel:
         torch.index_select(self.tok_emb, 0, st["tokens"], out=x)
         for layer_i, layer in enumerate(self.layers):
             gpu.linear_f64acc(x, layer["wqkv"], st["qkv"], norm_w=layer["attn_norm"], eps=eps)
-            gpu.rope_split_qkv(st["qkv"], st["q"], st["k"], st["v"], self.rope_cos, self.rope_sin,
-                               st["positions"], cfg.n_head, cfg.n_kv_head)
-            gpu.attention_decode_paged_append(st["q"], st["k"], st["v"], self.k_pool, self.v_pool,
-                                              st["attn"], st["tables"], st["positions"],
-                                              st["lens"], b, cfg.n_head, cfg.n_kv_head, 64,
-                                              self.table_stride, cfg.n_layer, layer_i,
-                                              cfg.kv_dim, self.capacity,
-                                              workspace=self.workspace)
+            # RoPE of q and k, both appends and attention: one launch on the fused rows
+            gpu.attention_decode_qkv_paged_append(st["qkv"], self.rope_cos, self.rope_sin,
+                                                  self.k_pool, self.v_pool, st["attn"],
+                                                  st["tables"], st["positions"], st["lens"], b,
+                                                  cfg.n_head, cfg.n_kv_head, 64,
+                                                  self.table_stride, cfg.n_layer, layer_i,
+                                                  cfg.kv_dim, self.capacity,
+                                                  workspace=self.workspace)
             gpu.linear_f64acc(st["attn"], layer["wo"], x, resid=x)
             gpu.linear_swiglu_f64acc(x, layer["wg"], layer["wu"], st["act"],
                                      norm_w=layer["mlp_norm"], eps=eps)

@@ -147,6 +147,23 @@ int crucible_attention_decode_paged_append(
     int64_t kv_dim, int64_t max_seq, void* workspace, size_t workspace_bytes,
     crucible_stream_t stream);
 
+/* The same fused step fed straight from the fused q/k/v projection, with the RoPE of
+ * the reference's decode step (rope_rows before the K append and on q, gpu_model.rs:1424-1444;
+ * RopeTable::apply, ops.rs:124-135) applied in the same launch (§8f rank 2). Row b of qkv
+ * (f32, row stride qkv_row_stride, a multiple of 4) holds q (n_head*64), k (kv_dim), v
+ * (kv_dim). q and k are rotated at positions[b] with rope_cos/rope_sin ([rope_max_pos][32]
+ * f32, 16-byte aligned, rope_max_pos >= max_seq; both NULL: no rotation), each product
+ * and difference rounded on its own. k and v are appended at positions[b] and attention
+ * runs over seq_lens[b] keys. Bit-identical to crucible_rope_split_qkv followed by
+ * crucible_attention_decode_paged_append. */
+int crucible_attention_decode_qkv_paged_append(
+    const float* qkv, int64_t qkv_row_stride, const float* rope_cos, const float* rope_sin,
+    int64_t rope_max_pos, void* k_pool, void* v_pool, void* out, int out_dtype,
+    const int32_t* page_tables, const int32_t* positions, const int32_t* seq_lens, int64_t batch,
+    int64_t n_head, int64_t n_kv_head, int64_t head_dim, int64_t table_stride, int64_t n_layer,
+    int64_t layer, int64_t kv_dim, int64_t max_seq, void* workspace, size_t workspace_bytes,
+    crucible_stream_t stream);
+
 /* Replaces Gpu::attention_decode (gpu.rs:762-817; kernels.cu:288-389): one
  * sequence in a contiguous cache, visible length params[CRUCIBLE_PARAM_SEQ]. */
 int crucible_attention_decode(const void* q, int q_dtype, const void* k_cache,

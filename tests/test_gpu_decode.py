@@ -345,3 +345,88 @@ def test_workspace_shared_across_batch_sizes(gpu, dev):
         assert np.abs(out.cpu().numpy() - want).max() <= TOL, batch
     # every counter is back to zero
     assert int(ws[:65536 * 4].view(torch.int32).abs().sum()) == 0
+
+
+@pytest.mark.parametrize("n_head,n_kv,pad", [(12, 3, 0), (12, 12, 4), (16, 4, 0), (12, 1, 8)])
+def test_qkv_rope_entry_equals_rope_split_then_fused_append(gpu, dev, n_head, n_kv, pad):
+    """crucible_attention_decode_qkv_paged_append (q/k/v straight from the fused projection
+    rows, RoPE in the same launch) gives the bytes of crucible_rope_split_qkv followed by
+    crucible_attention_decode_paged_append: pools and outputs bit for bit, including an
+    append off the last slot and an inactive request."""
+    from crucible_amd.gpu_model import rope_tables
+
+    rng = np.random.default_rng(n_head * 7 + n_kv + pad)
+    lens = [1, 16, 17, 0, 300, 1024, 40]
+    positions = [0, 15, 16, 5, 299, 1023, 100]
+    batch, kv, n_layer, layer = len(lens), n_kv * 64, 3, 2
+    stride = max(-(-max(max(lens), max(positions) + 1) // 16), 1)
+    need = [max(-(-max(n, 1) // 16), (p >> 4) + 1) for n, p in zip(lens, positions)]
+    n_pages = sum(need) + 3
+    kp, vp = random_pools(rng, n_pages, n_layer, kv)
+    tables = disjoint_tables(rng, n_pages, [16 * k for k in need], stride)
+    width = (n_head + 2 * n_kv) * 64
+    qkv = np.zeros((batch, width + pad), np.float32)
+    qkv[:, :width] = rng.standard_normal((batch, width)).astype(np.float32)
+    cos, sin = rope_tables(64, stride * 16, 10000.0)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    d_qkv, d_cos, d_sin = d(qkv), d(cos), d(sin)
+    d_tab, d_pos, d_len = d(tables), d(np.asarray(positions, np.int32)), d(np.asarray(lens, np.int32))
+    max_seq = stride * 16
+    # reference order: split + rotate, then the fused append + decode
+    q = torch.empty((batch, n_head * 64), device=dev)
+    k = torch.empty((batch, kv), device=dev)
+    v = torch.empty((batch, kv), device=dev)
+    gpu.rope_split_qkv(d_qkv[:, :width].contiguous(), q, k, v, d_cos, d_sin, d_pos, n_head, n_kv)
+    k1, v1 = _dev(kp, dev), _dev(vp, dev)
+    out1 = torch.full((batch, n_head * 64), SENTINEL, device=dev)
+    gpu.attention_decode_paged_append(q, k, v, k1, v1, out1, d_tab, d_pos, d_len, batch, n_head,
+                                      n_kv, 64, stride, n_layer, layer, kv, max_seq)
+    k2, v2 = _dev(kp, dev), _dev(vp, dev)
+    out2 = torch.full((batch, n_head * 64), SENTINEL, device=dev)
+    gpu.attention_decode_qkv_paged_append(d_qkv, d_cos, d_sin, k2, v2, out2, d_tab, d_pos, d_len,
+                                          batch, n_head, n_kv, 64, stride, n_layer, layer, kv,
+                                          max_seq)
+    torch.cuda.synchronize()
+    assert torch.equal(k1, k2) and torch.equal(v1, v2), "pool bytes differ"
+    o1, o2 = out1.cpu().numpy(), out2.cpu().numpy()
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32)), "outputs differ"
+    assert np.all(o2[3] == SENTINEL)
+    # and against the oracle: rotate on the host (exact f32 ops), append, attend
+    qr = qkv[:, :n_head * 64].reshape(batch, n_head, 64).copy()
+    c = cos[positions][:, None, :]
+    s = sin[positions][:, None, :]
+    lo, hi = qr[..., :32].copy(), qr[..., 32:].copy()
+    qr[..., :32], qr[..., 32:] = lo * c - hi * s, lo * s + hi * c
+    want = _oracle(qr.reshape(batch, -1), k1.cpu().numpy().view(np.uint16),
+                   v1.cpu().numpy().view(np.uint16), tables, lens, n_head, n_kv, n_layer, layer)
+    active = [b for b, n in enumerate(lens) if n > 0]
+    assert np.abs(o2[active] - want[active]).max() <= TOL
+
+
+def test_qkv_entry_without_rope_equals_plain_fused_append(gpu, dev):
+    """With no rope tables the qkv entry is the fused append + decode on strided rows."""
+    rng = np.random.default_rng(5)
+    lens = [33, 200, 7]
+    positions = [32, 199, 6]
+    n_head, n_kv, batch, kv, n_layer, layer, stride = 12, 3, 3, 192, 2, 0, 16
+    need = [-(-n // 16) for n in lens]
+    n_pages = sum(need) + 2
+    kp, vp = random_pools(rng, n_pages, n_layer, kv)
+    tables = disjoint_tables(rng, n_pages, [16 * k for k in need], stride)
+    width = (n_head + 2 * n_kv) * 64
+    qkv = rng.standard_normal((batch, width)).astype(np.float32)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    d_tab, d_pos, d_len = d(tables), d(np.asarray(positions, np.int32)), d(np.asarray(lens, np.int32))
+    k1, v1 = _dev(kp, dev), _dev(vp, dev)
+    out1 = torch.full((batch, n_head * 64), SENTINEL, device=dev)
+    gpu.attention_decode_paged_append(d(qkv[:, :768]), d(qkv[:, 768:960]), d(qkv[:, 960:]), k1, v1,
+                                      out1, d_tab, d_pos, d_len, batch, n_head, n_kv, 64, stride,
+                                      n_layer, layer, kv, stride * 16)
+    k2, v2 = _dev(kp, dev), _dev(vp, dev)
+    out2 = torch.full((batch, n_head * 64), SENTINEL, device=dev)
+    gpu.attention_decode_qkv_paged_append(d(qkv), None, None, k2, v2, out2, d_tab, d_pos, d_len,
+                                          batch, n_head, n_kv, 64, stride, n_layer, layer, kv,
+                                          stride * 16)
+    torch.cuda.synchronize()
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    assert torch.equal(out1, out2)

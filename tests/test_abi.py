@@ -82,3 +82,51 @@ def test_workspace_size_formula():
     assert lib.crucible_attention_decode_workspace_bytes(16, 12, 2048) == (
         65536 * 4 + 16 * 12 * 32 * 66 * 4)
     assert lib.crucible_attention_decode_workspace_bytes(0, 12, 2048) == 0
+
+
+def test_decode_step_glue_validates_before_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)  # 16-byte aligned, never dereferenced
+    odd = ctypes.c_void_p(0x1004)   # misaligned
+    # k_in must be a multiple of 32
+    rc = lib.crucible_linear_f64acc(fake, 100, None, 1e-6, fake, 64, 100, None, fake, 64, 4, None)
+    assert rc == _lib.ERR_UNSUPPORTED and "k_in" in _lib.last_error()[1]
+    # leading dimension below k_in
+    rc = lib.crucible_linear_f64acc(fake, 64, None, 1e-6, fake, 64, 128, None, fake, 64, 4, None)
+    assert rc == _lib.ERR_INVALID
+    # misaligned activations
+    rc = lib.crucible_linear_f64acc(odd, 128, None, 1e-6, fake, 64, 128, None, fake, 64, 4, None)
+    assert rc == _lib.ERR_INVALID and "aligned" in _lib.last_error()[1]
+    # SwiGLU needs its up rows
+    rc = lib.crucible_linear_swiglu_f64acc(fake, 128, None, 1e-6, fake, None, 64, 128, fake, 64,
+                                           4, None)
+    assert rc == _lib.ERR_INVALID
+    # zero rows: nothing to do
+    assert lib.crucible_linear_f64acc(fake, 128, None, 1e-6, fake, 64, 128, None, fake, 64, 0,
+                                      None) == 0
+    # RoPE split: head_dim 128 is outside this build, ld too small
+    rc = lib.crucible_rope_split_qkv(fake, 1152, fake, fake, fake, fake, fake, fake, 16, 12, 3,
+                                     128, 1024, None)
+    assert rc == _lib.ERR_UNSUPPORTED
+    rc = lib.crucible_rope_split_qkv(fake, 1000, fake, fake, fake, fake, fake, fake, 16, 12, 3,
+                                     64, 1024, None)
+    assert rc == _lib.ERR_INVALID
+
+
+def test_qkv_decode_entry_validates_before_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+    args = dict(out_dtype=0, batch=16, n_head=12, n_kv=3, hd=64, stride=128, n_layer=12,
+                layer=0, kv_dim=192, max_seq=2048)
+
+    def call(row_stride=1152, cos=fake, sin=fake, max_pos=2048, ws_bytes=1 << 22):
+        return lib.crucible_attention_decode_qkv_paged_append(
+            fake, row_stride, cos, sin, max_pos, fake, fake, fake, args["out_dtype"], fake, fake,
+            fake, args["batch"], args["n_head"], args["n_kv"], args["hd"], args["stride"],
+            args["n_layer"], args["layer"], args["kv_dim"], args["max_seq"], fake, ws_bytes, None)
+
+    assert call(row_stride=1150) == _lib.ERR_INVALID      # not a multiple of 4
+    assert call(row_stride=1100) == _lib.ERR_INVALID      # cannot hold q, k and v
+    assert call(cos=None) == _lib.ERR_INVALID             # cos without sin
+    assert call(max_pos=1024) == _lib.ERR_INVALID         # tables shorter than max_seq
+    assert call(ws_bytes=16) == _lib.ERR_WORKSPACE        # split-K workspace too small

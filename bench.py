@@ -326,6 +326,31 @@ def bench_e2e(gpu, reps: int = 2):
 
 # ---------------------------------------------------------------- CPU baseline
 
+def cpu_prefill(cfg, seconds: float):
+    """The reference CPU attention for a prefill config (one SDPA(is_causal) per sequence,
+    fp32), bounded to about `seconds`: GFLOP/s on the config's visible-pair FLOPs."""
+    from oracle import cpu_path
+
+    cores = cpu_path.threads()
+    cpu = cpu_path.PrefillCPU(cfg.seq_lens, cfg.n_head, cfg.n_kv_head, seed=3)
+    reps, s_per = cpu_path.time_bounded(cpu.step, seconds)
+    return {"ms": round(s_per * 1e3, 3), "gflops": round(cfg.flops() / s_per / 1e9, 2),
+            "cores": cores, "kind": "port", "sample": f"{reps} full launches of the config, torch "
+            "SDPA fp32 per sequence"}
+
+
+def cpu_decode_b1(seconds: float):
+    """Config 2 on the CPU: one 12-layer step of batch 1 at 1024 keys (gather + SDPA + the
+    row append), per-layer microseconds."""
+    from oracle import cpu_path
+
+    cores = cpu_path.threads()
+    cpu = cpu_path.DecodeBatchCPU([1024], 12, 12, 3, seed=2)
+    reps, s_per = cpu_path.time_bounded(cpu.step, seconds)
+    return {"us_per_layer": round(s_per * 1e6 / 12, 2), "cores": cores, "kind": "port",
+            "sample": f"{reps} 12-layer steps"}
+
+
 def cpu_baseline(bench: DecodeBench, seconds: float):
     from oracle import cpu_path
 
@@ -452,6 +477,14 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(b16, args.cpu_seconds)
         log(f"cpu baseline: {cpu}")
+        if not args.no_extras:
+            # the reference CPU path beside the other configs
+            extras["decode_b1_ctx1024"]["cpu"] = cpu_decode_b1(2.0)
+            extras["prefill_config1"]["cpu"] = cpu_prefill(W.config1_prefill(n_kv_head=12), 2.0)
+            extras["prefill_config1_gqa3"]["cpu"] = cpu_prefill(W.config1_prefill(n_kv_head=3), 2.0)
+            extras["packed_config4"]["cpu"] = cpu_prefill(W.config4_packed(), 2.0)
+            log("cpu beside the extras: " + str({k: v.get("cpu") for k, v in extras.items()
+                                                 if isinstance(v, dict) and "cpu" in v}))
 
     line = {
         "metric": METRIC,

@@ -61,28 +61,108 @@ constexpr float kLazyLog2 = 8.0f;  // running-max slack (log2 units) before a re
 // lane ends with v[L] in one operand and v[L ^ 16] (resp. v[L ^ 32]) in the other. It is
 // written as asm because this compiler's builtin returns the first operand in both halves
 // of its result. s_nop 1 covers the VALU-write -> permlane-read hazard.
+//
+// The maxima are asm as well: fmaxf on values the compiler cannot prove canonical (MFMA
+// results, asm outputs) costs an extra canonicalising v_max per operand, and these
+// scores are never signalling NaNs.
+__device__ __forceinline__ float vmax(float a, float b) {
+    float d;
+    asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float d;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
 __device__ __forceinline__ float max_xor16(float v) {
     float a = v, b = v;
     asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return fmaxf(a, b);
+    return vmax(a, b);
 }
 __device__ __forceinline__ float max_xor32(float v) {
     float a = v, b = v;
     asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return fmaxf(a, b);
+    return vmax(a, b);
 }
 
-// P = hi + lo in fp16: hi truncates (v_cvt_pkrtz), lo = RNE(p - hi), which is exact to
-// about 2^-22 relative.
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ half4_t split_hi(const float (&p)[4]) {
-    const half2_t a = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(p[0], p[1]));
-    const half2_t b = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(p[2], p[3]));
-    return half4_t{a[0], a[1], b[0], b[1]};
+// One lane's 16 scores of a 64-key tile, st[kb][r] = S^T[key 16 kb + 4 grp + r][q = col],
+// kept unscaled: the scale (> 0) is folded into the exponent, so the max needs none.
+
+// Causal mask: key 16 kb + 4 grp + r of the tile is visible iff 16 kb + r <= lim, where
+// lim = pos - kbase - 4 grp for a row in the run and -1 (nothing visible) otherwise.
+// Written as selects so that it compiles to a compare and a select per score.
+__device__ __forceinline__ void mask_tile(float4_t (&st)[4], int lim) {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st[kb][r] = (16 * kb + r <= lim) ? st[kb][r] : -INFINITY;
 }
-__device__ __forceinline__ half4_t split_lo(const float (&p)[4], half4_t h) {
-    return half4_t{(half_t)(p[0] - (float)h[0]), (half_t)(p[1] - (float)h[1]),
-                   (half_t)(p[2] - (float)h[2]), (half_t)(p[3] - (float)h[3])};
+
+// Column max of the tile (over the lane's 16 scores and its 4 lane groups), unscaled.
+__device__ __forceinline__ float tile_max(const float4_t (&st)[4]) {
+    float a = vmax3(st[0][0], st[0][1], st[0][2]);
+    float b = vmax3(st[1][0], st[1][1], st[1][2]);
+    a = vmax3(a, st[0][3], st[2][0]);
+    b = vmax3(b, st[1][3], st[3][0]);
+    a = vmax3(a, st[2][1], st[2][2]);
+    b = vmax3(b, st[3][1], st[3][2]);
+    return max_xor32(max_xor16(vmax3(a, b, vmax(st[2][3], st[3][3]))));
+}
+
+// P = exp2(s * scale - mu) (one FMA and one exp per score), split into fp16 P = hi + lo
+// (hi truncates, lo = RNE(p - hi): exact to about 2^-22 relative), as the hi/lo
+// operands of the PV product: pb/pl[0] hold keys 0..31 of the tile, [1] keys 32..63, in
+// the B-operand layout the S^T product leaves (lane group grp: keys 4 grp .. +3 of each
+// 16-key block). Returns the lane's sum of P.
+//
+// The split per pair of values: hi = v_cvt_pkrtz (round toward zero), and lo = RNE(p -
+// hi) from v_fma_mix{lo,hi}_f16, which take hi as an fp16 operand, form p - hi exactly in
+// f32 and round once to fp16 into one half of the packed result (one instruction per value
+// where the C form needs a convert, a subtract and half a pack).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint32_t split_lo2(float p0, float p1, uint32_t hi) {
+    uint32_t lo;
+    asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, %1, -1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "=&v"(lo)
+        : "v"(hi), "v"(p0), "v"(p1));
+    return lo;
+}
+__device__ __forceinline__ float tile_p(const float4_t (&st)[4], float scale, float mu,
+                                        half8_t (&pb)[2], half8_t (&pl)[2]) {
+    u32x4_t hw[2], lw[2];
+    float part[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        float pf[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pf[r] = fast_exp2(__builtin_fmaf(st[kb][r], scale, -mu));
+        part[kb] = (pf[0] + pf[1]) + (pf[2] + pf[3]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t h =
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pf[2 * j], pf[2 * j + 1]));
+            hw[kb >> 1][(kb & 1) * 2 + j] = h;
+            lw[kb >> 1][(kb & 1) * 2 + j] = split_lo2(pf[2 * j], pf[2 * j + 1], h);
+        }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        pb[ks] = __builtin_bit_cast(half8_t, hw[ks]);
+        pl[ks] = __builtin_bit_cast(half8_t, lw[ks]);
+    }
+    return (part[0] + part[1]) + (part[2] + part[3]);
+}
+
+// Zeroes the keys at or past the run's end in a V^T operand quarter: element r is key
+// k0 + r, kept iff k0 + r < hist_end. Only the last tile of a run needs it (the pages
+// there may hold anything, NaN included, and 0 * NaN would poison the product).
+__device__ __forceinline__ half4_t zero_tail(half4_t v, int k0, int hist_end) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        if (k0 + r >= hist_end) v[r] = (half_t)0.0f;
+    return v;
 }
 
 struct PrefillArgs {
@@ -320,6 +400,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
         // a slot runs half of the tiles and the two halves' softmax chains overlap.
         constexpr int PS = KB / 2;  // pair slots in the ring
         const int n_pairs = (n_tiles + 1) / 2;
+        // the pair holding the run's last tile when that tile is partial, else none
+        const int tail_pair = (hist_end % kKeyTile) ? (n_tiles - 1) / 2 : -1;
 #pragma unroll
         for (int p = 0; p < PS - 1; ++p)
             if (p < n_pairs) {
@@ -334,6 +416,24 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
             if (ahead >= 2) __builtin_amdgcn_s_waitcnt(kWaitVm8Lgkm0);
             else if (ahead == 1) __builtin_amdgcn_s_waitcnt(kWaitVm4Lgkm0);
             else __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+            // Keys past the run's end may hold anything, NaN included, and P = 0 there
+            // would still give 0 * NaN: in the run's last tile, each thread zeroes them in
+            // the V^T chunk it loaded (its own load has landed), before the barrier.
+            if (ip == tail_pair) {
+                const int t = n_tiles - 1;
+                const int d = 8 * wave + (lane >> 3);
+                const int c = (lane & 7) ^ (d & 7);  // keys 8c .. 8c + 7 of the tile
+                const int nv = hist_end - (t * kKeyTile + 8 * c);
+                if (nv < 8) {
+                    half8_t* chunk = reinterpret_cast<half8_t*>(&s_v[t % KB][8 * wave][0]) + lane;
+                    half8_t v = *chunk;
+#pragma unroll
+                    for (int r = 0; r < 8; ++r)
+                        if (r >= nv) v[r] = (half_t)0.0f;
+                    *chunk = v;
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            }
             __builtin_amdgcn_s_barrier();
             if (ip + PS - 1 < n_pairs) {
                 issue(2 * (ip + PS - 1));
@@ -364,33 +464,22 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                         st[qb][kb] = c;
                     }
                 }
-                // Scale to base 2 and mask; a tile that every row of the wave sees whole
-                // (below the diagonal, all rows in the run) needs no mask.
+                // Mask; a tile that every row of the wave sees whole (below the diagonal,
+                // all rows in the run) needs none.
                 bool lane_full = true;
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb)
                     lane_full = lane_full && in_run[qb] && my_pos[qb] >= kbase + kKeyTile - 1;
-                const bool full = __all(lane_full);
+                if (!__all(lane_full)) {
 #pragma unroll
-                for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int key = kbase + 16 * kb + 4 * grp + r;
-                            const float x = st[qb][kb][r] * a.scale_log2;
-                            st[qb][kb][r] = (full || (in_run[qb] && key <= my_pos[qb])) ? x : -INFINITY;
-                        }
+                    for (int qb = 0; qb < QB; ++qb)
+                        mask_tile(st[qb], in_run[qb] ? my_pos[qb] - kbase - 4 * grp : -1);
+                }
                 half8_t pb[QB][2];
                 half8_t pl[QB][2];  // P = hi + lo: the product keeps ~22 bits of P
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) {
-                    float tm = -INFINITY;
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) tm = fmaxf(tm, st[qb][kb][r]);
-                    tm = max_xor32(max_xor16(tm));
+                    const float tm = tile_max(st[qb]) * a.scale_log2;  // base-2 units
                     // Lazy rescale: the running max moves only when the tile's max exceeds
                     // it by more than kLazyLog2, so P stays <= 2^kLazyLog2 and most tiles
                     // skip rescaling the accumulators. out = acc / l is unchanged.
@@ -406,28 +495,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                         m[qb] = mn;
                     }
                     const float mu = (m[qb] == -INFINITY) ? 0.0f : m[qb];
-                    float ps = 0.0f;
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb) {
-                        float pf[4];
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            pf[r] = fast_exp2(st[qb][kb][r] - mu);
-                            ps += pf[r];
-                        }
-                        const half4_t h = split_hi(pf);
-                        const half4_t lo = split_lo(pf, h);
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            pb[qb][kb >> 1][(kb & 1) * 4 + r] = h[r];
-                            pl[qb][kb >> 1][(kb & 1) * 4 + r] = lo[r];
-                        }
-                    }
-                    l[qb] += ps;
+                    l[qb] += tile_p(st[qb], a.scale_log2, mu, pb[qb], pl[qb]);
                 }
-                // O^T[dim][q] += V^T[dim][32 keys] . P^T[32 keys][q], key halves ks = 0, 1.
-                // Keys past the run's end may hold anything (even NaN): zero them.
-                const bool tail = kbase + kKeyTile > hist_end;
+                // O^T[dim][q] += V^T[dim][32 keys] . P^T[32 keys][q], key halves ks = 0, 1
+                // (keys past the run's end were zeroed in LDS above).
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
                     const int d = 16 * db + col;
@@ -435,17 +506,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                     for (int ks = 0; ks < 2; ++ks) {
                         const int c1 = 4 * ks + (grp >> 1);
                         const int o = 4 * (grp & 1);
-                        half4_t v0 = *reinterpret_cast<const half4_t*>(
+                        const half4_t v0 = *reinterpret_cast<const half4_t*>(
                             &s_v[buf][d][8 * (c1 ^ (d & 7)) + o]);
-                        half4_t v1 = *reinterpret_cast<const half4_t*>(
+                        const half4_t v1 = *reinterpret_cast<const half4_t*>(
                             &s_v[buf][d][8 * ((c1 + 2) ^ (d & 7)) + o]);
-                        if (tail) {
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                if (kbase + 32 * ks + 4 * grp + r >= hist_end) v0[r] = (half_t)0.0f;
-                                if (kbase + 32 * ks + 16 + 4 * grp + r >= hist_end) v1[r] = (half_t)0.0f;
-                            }
-                        }
                         const half8_t va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
 #pragma unroll
                         for (int qb = 0; qb < QB; ++qb) {
@@ -672,21 +736,9 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
                 }
                 st[kb] = c;
             }
-            const bool full = __all(in_run && my_pos >= kbase + kKeyTile - 1);
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int key = kbase + 16 * kb + 4 * grp + r;
-                    const float x = st[kb][r] * a.scale_log2;
-                    st[kb][r] = (full || (in_run && key <= my_pos)) ? x : -INFINITY;
-                }
-            float tm = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) tm = fmaxf(tm, st[kb][r]);
-            tm = max_xor32(max_xor16(tm));
+            if (!__all(in_run && my_pos >= kbase + kKeyTile - 1))
+                mask_tile(st, in_run ? my_pos - kbase - 4 * grp : -1);
+            const float tm = tile_max(st) * a.scale_log2;  // base-2 units
             const bool grow = tm > m + kLazyLog2;
             if (__any(grow)) {
                 const float alpha = grow ? fast_exp2(m - tm) : 1.0f;
@@ -697,37 +749,22 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
             }
             const float mu = (m == -INFINITY) ? 0.0f : m;
             half8_t pb[2], pl[2];
-            float ps = 0.0f;
+            l += tile_p(st, a.scale_log2, mu, pb, pl);
+            if (kbase + kKeyTile > hist_end) {  // the run's last tile: zero keys past its end
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                float pf[4];
+                for (int db = 0; db < 4; ++db)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    pf[r] = fast_exp2(st[kb][r] - mu);
-                    ps += pf[r];
-                }
-                const half4_t hh = split_hi(pf);
-                const half4_t lo = split_lo(pf, hh);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    pb[kb >> 1][(kb & 1) * 4 + r] = hh[r];
-                    pl[kb >> 1][(kb & 1) * 4 + r] = lo[r];
-                }
+                    for (int ks = 0; ks < 2; ++ks) {
+                        va[db][ks][0] = zero_tail(va[db][ks][0], kbase + 32 * ks + 4 * grp, hist_end);
+                        va[db][ks][1] =
+                            zero_tail(va[db][ks][1], kbase + 32 * ks + 16 + 4 * grp, hist_end);
+                    }
             }
-            l += ps;
-            const bool tail = kbase + kKeyTile > hist_end;
 #pragma unroll
             for (int db = 0; db < 4; ++db)
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
-                    half4_t v0 = va[db][ks][0], v1 = va[db][ks][1];
-                    if (tail) {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            if (kbase + 32 * ks + 4 * grp + r >= hist_end) v0[r] = (half_t)0.0f;
-                            if (kbase + 32 * ks + 16 + 4 * grp + r >= hist_end) v1[r] = (half_t)0.0f;
-                        }
-                    }
+                    const half4_t v0 = va[db][ks][0], v1 = va[db][ks][1];
                     const half8_t vv = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
                     acc[db] = mfma_16x16x32(vv, pb[ks], acc[db]);
                     acc[db] = mfma_16x16x32(vv, pl[ks], acc[db]);

@@ -42,6 +42,8 @@ SIGNATURES = {
     "crucible_attention_prefill_tiled": ([_P, _I, _P, _P, _P, _P, _P, _I, _P, _P] + [_I64] * 9 + [_I, _I64, _P], _I),
     "crucible_attention_prefill": ([_P, _I, _P, _P, _P, _I] + [_I64] * 8 + [_P], _I),
     "crucible_argmax_rows": ([_P, _P, _I64, _I64, _P], _I),
+    "crucible_greedy_advance": ([_P, _I64, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _P,
+                                 _P, _P], _I),
     "crucible_linear_f64acc": ([_P, _I64, _P, ctypes.c_float, _P, _I64, _I64, _P, _P, _I64, _I64,
                                 _P], _I),
     "crucible_linear_swiglu_f64acc": ([_P, _I64, _P, ctypes.c_float, _P, _P, _I64, _I64, _P,

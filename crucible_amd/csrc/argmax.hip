@@ -12,7 +12,7 @@
 // where order() maps floats to unsigned integers with the same ordering (and maps -0.0
 // to +0.0). The maximum key is the highest value with the lowest index among ties, so a
 // plain max-reduction in any order gives the host's answer; the v[0]-is-NaN case is
-// checked once per row. One workgroup of 1024 threads per row; each thread keeps four
+// checked once per row. One workgroup of 1024 threads per row; each thread keeps eight
 // loads in flight.
 #include "common.hpp"
 
@@ -30,34 +30,75 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t i) {
 
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const float* __restrict__ x,
-                                                                   int32_t* __restrict__ out,
-                                                                   int64_t cols) {
+// Index of the row's maximum by the host rule, in thread 0 (other threads: unspecified).
+// Every thread keeps eight loads in flight per round.
+__device__ __forceinline__ int32_t row_argmax(const float* __restrict__ r, int64_t cols) {
     __shared__ uint64_t s_key[kArgmaxThreads / 64];
-    const float* r = x + (int64_t)blockIdx.x * cols;
     const int t = threadIdx.x;
     uint64_t best = 0;
     int64_t i = t;
-    for (; i + 3 * kArgmaxThreads < cols; i += 4 * kArgmaxThreads) {
-        const float v0 = r[i], v1 = r[i + kArgmaxThreads], v2 = r[i + 2 * kArgmaxThreads],
-                    v3 = r[i + 3 * kArgmaxThreads];
-        best = max_u64(best, argmax_key(v0, (uint32_t)i));
-        best = max_u64(best, argmax_key(v1, (uint32_t)(i + kArgmaxThreads)));
-        best = max_u64(best, argmax_key(v2, (uint32_t)(i + 2 * kArgmaxThreads)));
-        best = max_u64(best, argmax_key(v3, (uint32_t)(i + 3 * kArgmaxThreads)));
+    constexpr int kU = 8;
+    for (; i + (kU - 1) * kArgmaxThreads < cols; i += kU * kArgmaxThreads) {
+        float v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) v[u] = r[i + u * kArgmaxThreads];
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+            best = max_u64(best, argmax_key(v[u], (uint32_t)(i + u * kArgmaxThreads)));
     }
     for (; i < cols; i += kArgmaxThreads) best = max_u64(best, argmax_key(r[i], (uint32_t)i));
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) best = max_u64(best, __shfl_xor(best, off));
     if ((t & 63) == 0) s_key[t >> 6] = best;
     __syncthreads();
+    int32_t idx = 0;
     if (t == 0) {
         uint64_t k = s_key[0];
 #pragma unroll
         for (int w = 1; w < kArgmaxThreads / 64; ++w) k = max_u64(k, s_key[w]);
         const float v0 = r[0];
         // all-NaN rows (k == 0) and rows whose first element is NaN answer 0
-        out[blockIdx.x] = (k == 0 || v0 != v0) ? 0 : (int32_t)(0xffffffffu - (uint32_t)k);
+        idx = (k == 0 || v0 != v0) ? 0 : (int32_t)(0xffffffffu - (uint32_t)k);
+    }
+    return idx;
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const float* __restrict__ x,
+                                                                   int32_t* __restrict__ out,
+                                                                   int64_t cols) {
+    const int32_t idx = row_argmax(x + (int64_t)blockIdx.x * cols, cols);
+    if (threadIdx.x == 0) out[blockIdx.x] = idx;
+}
+
+// The greedy decode step's tail, one workgroup per row (see crucible_greedy_advance).
+__global__ __launch_bounds__(kArgmaxThreads) void greedy_advance_kernel(
+    const float* __restrict__ logits, int64_t cols, const float* __restrict__ emb,
+    int64_t n_embd, float* __restrict__ x, int64_t ldx, int32_t* __restrict__ tokens,
+    int32_t* __restrict__ history, int64_t* step, int64_t max_steps,
+    int32_t* __restrict__ positions, int32_t* __restrict__ lens, uint32_t* done, int rows) {
+    __shared__ int32_t s_tok;
+    const int row = blockIdx.x;
+    const int32_t tok = row_argmax(logits + (int64_t)row * cols, cols);
+    if (threadIdx.x == 0) {
+        s_tok = tok;
+        tokens[row] = tok;
+        const int64_t st = *step;  // read before this row is counted below
+        if (st >= 0 && st < max_steps) history[st * rows + row] = tok;
+        positions[row] += 1;
+        lens[row] += 1;
+    }
+    __syncthreads();
+    const float* src = emb + (int64_t)s_tok * n_embd;
+    float* dst = x + (int64_t)row * ldx;
+    for (int64_t k = threadIdx.x; k < n_embd; k += kArgmaxThreads) dst[k] = src[k];
+    if (threadIdx.x == 0) {
+        // the row that completes the step advances it; every row has read it by then
+        const uint32_t prev =
+            __hip_atomic_fetch_add(done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev == (uint32_t)(rows - 1)) {
+            __hip_atomic_store(step, *step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -76,5 +117,25 @@ extern "C" int crucible_argmax_rows(const float* x, int32_t* out, int64_t rows, 
     CRUCIBLE_CHECK(x && out, CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
     hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)rows), dim3(kArgmaxThreads), 0, stream,
                        x, out, cols);
+    return fail_launch(what);
+}
+
+extern "C" int crucible_greedy_advance(const float* logits, int64_t rows, int64_t cols,
+                                       const float* emb, int64_t n_embd, float* x, int64_t ldx,
+                                       int32_t* tokens, int32_t* history, int64_t* step,
+                                       int64_t max_steps, int32_t* positions, int32_t* lens,
+                                       uint32_t* done, crucible_stream_t stream) {
+    const char* what = "greedy_advance";
+    CRUCIBLE_CHECK(rows >= 0 && rows <= 65535 && cols > 0 && cols < 0x7fffffffLL &&
+                       n_embd > 0 && ldx >= n_embd && max_steps >= 0,
+                   CRUCIBLE_ERR_INVALID, "%s: rows=%lld cols=%lld n_embd=%lld ldx=%lld", what,
+                   (long long)rows, (long long)cols, (long long)n_embd, (long long)ldx);
+    if (rows == 0) return CRUCIBLE_OK;
+    CRUCIBLE_CHECK(logits && emb && x && tokens && step && positions && lens && done &&
+                       (history || max_steps == 0),
+                   CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
+    hipLaunchKernelGGL(greedy_advance_kernel, dim3((unsigned)rows), dim3(kArgmaxThreads), 0,
+                       stream, logits, cols, emb, n_embd, x, ldx, tokens, history, step,
+                       max_steps, positions, lens, done, (int)rows);
     return fail_launch(what);
 }

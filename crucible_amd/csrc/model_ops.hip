@@ -19,7 +19,9 @@
 // as the reference's do.
 #include "common.hpp"
 
+#include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #pragma clang fp contract(off)
 
@@ -33,6 +35,10 @@ constexpr int kLinThreads = 64 * kLinWaves;
 constexpr int kLinK = 32;                  // K per chunk: 8 per lane group, 8 MFMA steps
 constexpr int kLinBatch = 8;               // chunks whose loads are in flight together
                                            // (1 for the 4-block tiles: registers, occupancy)
+constexpr int kNormRegChunks = 4;          // fused-norm rows with at most this many chunks
+                                           // per wave take their sums of squares from the
+                                           // operand registers (no separate pass); 3 for
+                                           // the 4-block tiles (registers, occupancy)
 
 enum LinMode { kPlain = 0, kResidual = 1, kSwiGLU = 2 };
 
@@ -61,7 +67,9 @@ struct Chunk {
     half8_t w[NB];
 };
 
-// out tile = 16 rows x (16 * NB) columns (kSwiGLU: 16 columns of gate and of up).
+// out tile = 16 rows x (16 * NB) columns. kSwiGLU (NB = 1): 8 output columns, whose gate
+// rows fill MFMA columns 0..7 and whose up rows fill columns 8..15, so one 16-wide tile
+// carries both halves of SwiGLU at the cost of 8 columns of work.
 //
 // f64 MFMA 16x16x4 operand layout: lane l supplies A[l & 15][kslot] and B[kslot][l & 15]
 // with kslot = l >> 4, and holds D[(l >> 4) + 4 r][l & 15], r = 0..3. Lane group g
@@ -70,6 +78,7 @@ struct Chunk {
 template <bool NORM, int MODE, int NB>
 __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
     __shared__ double s_scale[16];
+    __shared__ double s_ss[kLinWaves][16];          // per-wave sums of squares by row
     __shared__ double s_red[kLinWaves][NB][4][64];  // [wave][block][r][lane]
 
     const int tid = threadIdx.x;
@@ -78,9 +87,15 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
     const int col = lane & 15;
     const int g = lane >> 4;
     const int m0 = blockIdx.y * 16;
-    const int n0 = blockIdx.x * 16 * (MODE == kSwiGLU ? 1 : NB);
+    static_assert(MODE != kSwiGLU || NB == 1, "SwiGLU tiles are one 16-column block");
+    const int n0 = blockIdx.x * (MODE == kSwiGLU ? 8 : 16 * NB);
+    const int nc = a.k_in / kLinK;  // 32-wide chunks of the K range
+    // Short rows (every wave holds at most RC chunks) take the norm's sums of squares
+    // from the operand registers; longer ones make a separate pass first.
+    constexpr int RC = NB >= 4 ? 3 : kNormRegChunks;
+    const bool reg_norm = NORM && nc <= kLinWaves * RC;
 
-    if constexpr (NORM) {
+    if (NORM && !reg_norm) {
         // sum of squares of row tid >> 5 over the float4s t, t + 32, ... of the row, in
         // f64; loads go out 8 at a time so their latencies overlap
         const int r = tid >> 5, t = tid & 31;
@@ -108,8 +123,7 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
         __syncthreads();
     }
 
-    // wave w takes chunks [w * nc / 8, (w + 1) * nc / 8) of the nc = k_in / 32 chunks
-    const int nc = a.k_in / kLinK;
+    // wave w takes chunks [w * nc / 8, (w + 1) * nc / 8) of the nc chunks
     const int c0 = wave * nc / kLinWaves, c1 = (wave + 1) * nc / kLinWaves;
     const int kw = (c1 - c0) * kLinK;
     const int kbeg = c0 * kLinK + 8 * g;
@@ -117,13 +131,12 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
     const bool row_ok = row < a.rows;
     const float* xp = a.x + (int64_t)(row_ok ? row : 0) * a.ldx + kbeg;
     const float* nwp = NORM ? a.norm_w + kbeg : nullptr;
-    const double scale = NORM ? s_scale[col] : 1.0;
     const half_t* wp[NB];
     bool n_ok[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-        const half_t* base = (MODE == kSwiGLU && j == 1) ? a.w2 : a.w;
-        const int n = n0 + col + (MODE == kSwiGLU ? 0 : 16 * j);
+        const half_t* base = (MODE == kSwiGLU && col >= 8) ? a.w2 : a.w;
+        const int n = MODE == kSwiGLU ? n0 + (col & 7) : n0 + col + 16 * j;
         n_ok[j] = n < a.n_out;
         wp[j] = base + (int64_t)(n_ok[j] ? n : 0) * a.k_in + kbeg;
     }
@@ -141,35 +154,75 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[j] = double4_t{0.0, 0.0, 0.0, 0.0};
 
-    // Up to kLinBatch chunks load at once (the weights stream from HBM once: their
-    // latency, not the MFMA, bounds these small-batch products), then feed the MFMA.
-    constexpr int BATCH = NB >= 4 ? 1 : kLinBatch;
-    for (int b0 = 0; b0 < kw; b0 += BATCH * kLinK) {
-        Chunk<NB> ch[BATCH];
+    // One chunk into the accumulators: the activations (normalised first under NORM)
+    // and the weights go to f64, 8 MFMA steps per column block.
+    auto feed = [&](const Chunk<NB>& ch, int k0, double scale) {
+        float xs[8] = {ch.x0[0], ch.x0[1], ch.x0[2], ch.x0[3], ch.x1[0], ch.x1[1], ch.x1[2], ch.x1[3]};
+        if constexpr (NORM) {
+            const float4_t w0 = *reinterpret_cast<const float4_t*>(nwp + k0);
+            const float4_t w1 = *reinterpret_cast<const float4_t*>(nwp + k0 + 4);
+            const float nw[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
 #pragma unroll
-        for (int c = 0; c < BATCH; ++c)
-            if (b0 + c * kLinK < kw) ch[c] = load(b0 + c * kLinK);
+            for (int i = 0; i < 8; ++i) xs[i] = (float)((double)xs[i] * scale) * nw[i];
+        }
 #pragma unroll
-        for (int c = 0; c < BATCH; ++c) {
-            if (b0 + c * kLinK >= kw) break;
-            const int k0 = b0 + c * kLinK;
-            float xs[8] = {ch[c].x0[0], ch[c].x0[1], ch[c].x0[2], ch[c].x0[3],
-                           ch[c].x1[0], ch[c].x1[1], ch[c].x1[2], ch[c].x1[3]};
-            if constexpr (NORM) {
-                const float4_t w0 = *reinterpret_cast<const float4_t*>(nwp + k0);
-                const float4_t w1 = *reinterpret_cast<const float4_t*>(nwp + k0 + 4);
-                const float nw[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+        for (int i = 0; i < 8; ++i) {
+            const double av = row_ok ? (double)xs[i] : 0.0;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) xs[i] = (float)((double)xs[i] * scale) * nw[i];
+            for (int j = 0; j < NB; ++j) {
+                const double bv = n_ok[j] ? (double)(float)ch.w[j][i] : 0.0;
+                acc[j] = mfma_f64(av, bv, acc[j]);
             }
+        }
+    };
+
+    if (reg_norm) {
+        // Every chunk of the wave loads at once; the row's sum of squares comes from
+        // those registers: per lane over its chunks, then over the 4 lane groups of the
+        // row, then over the waves in a fixed order.
+        Chunk<NB> ch[RC];
+        const int nch = c1 - c0;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const double av = row_ok ? (double)xs[i] : 0.0;
+        for (int c = 0; c < RC; ++c)
+            if (c < nch) ch[c] = load(c * kLinK);
+        double ss = 0.0;
 #pragma unroll
-                for (int j = 0; j < NB; ++j) {
-                    const double bv = n_ok[j] ? (double)(float)ch[c].w[j][i] : 0.0;
-                    acc[j] = mfma_f64(av, bv, acc[j]);
-                }
+        for (int c = 0; c < RC; ++c) {
+            if (c >= nch) break;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const double d0 = (double)ch[c].x0[i], d1 = (double)ch[c].x1[i];
+                ss += d0 * d0;
+                ss += d1 * d1;
+            }
+        }
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        if (g == 0) s_ss[wave][col] = ss;
+        __syncthreads();
+        double tot = 0.0;
+#pragma unroll
+        for (int w = 0; w < kLinWaves; ++w) tot += s_ss[w][col];
+        const double scale = 1.0 / sqrt(tot / (double)a.k_in + a.eps);
+#pragma unroll
+        for (int c = 0; c < RC; ++c) {
+            if (c >= nch) break;
+            feed(ch[c], c * kLinK, scale);
+        }
+    } else {
+        const double scale = NORM ? s_scale[col] : 1.0;
+        // Up to kLinBatch chunks load at once (the weights stream from HBM once: their
+        // latency, not the MFMA, bounds these small-batch products), then feed the MFMA.
+        constexpr int BATCH = NB >= 4 ? 1 : kLinBatch;
+        for (int b0 = 0; b0 < kw; b0 += BATCH * kLinK) {
+            Chunk<NB> ch[BATCH];
+#pragma unroll
+            for (int c = 0; c < BATCH; ++c)
+                if (b0 + c * kLinK < kw) ch[c] = load(b0 + c * kLinK);
+#pragma unroll
+            for (int c = 0; c < BATCH; ++c) {
+                if (b0 + c * kLinK >= kw) break;
+                feed(ch[c], b0 + c * kLinK, scale);
             }
         }
     }
@@ -181,7 +234,25 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
     __syncthreads();
 
     // fixed summation order over the waves: the result does not depend on scheduling
-    constexpr int kOut = 256 * (MODE == kSwiGLU ? 1 : NB);
+    if constexpr (MODE == kSwiGLU) {
+        // thread (row, c) of the 16 x 8 outputs: gate at tile column c, up at c + 8
+        if (tid < 128) {
+            const int orow = m0 + (tid >> 3), c = tid & 7;
+            const int l = 16 * ((tid >> 3) & 3) + c, r = tid >> 5;
+            if (orow < a.rows && n0 + c < a.n_out) {
+                double y = 0.0, u = 0.0;
+#pragma unroll
+                for (int w = 0; w < kLinWaves; ++w) {
+                    y += s_red[w][0][r][l];
+                    u += s_red[w][0][r][l + 8];
+                }
+                const float gf = (float)y;
+                a.out[(int64_t)orow * a.ldo + n0 + c] = gf / (1.0f + expf(-gf)) * (float)u;
+            }
+        }
+        return;
+    }
+    constexpr int kOut = 256 * NB;
     for (int o = tid; o < kOut; o += kLinThreads) {
         const int blk = o >> 8, rem = o & 255;
         const int l = rem & 63, r = rem >> 6;
@@ -192,17 +263,151 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
 #pragma unroll
         for (int w = 0; w < kLinWaves; ++w) y += s_red[w][blk][r][l];
         float* dst = a.out + (int64_t)orow * a.ldo + on;
-        if constexpr (MODE == kSwiGLU) {
-            double u = 0.0;
-#pragma unroll
-            for (int w = 0; w < kLinWaves; ++w) u += s_red[w][1][r][l];
-            const float gf = (float)y;
-            *dst = gf / (1.0f + expf(-gf)) * (float)u;
-        } else if constexpr (MODE == kResidual) {
+        if constexpr (MODE == kResidual) {
             *dst = a.resid[(int64_t)orow * a.ldo + on] + (float)y;
         } else {
             *dst = (float)y;
         }
+    }
+}
+
+// ---------------------------------------------------------------- wide projections
+
+constexpr int kCUs = 256;      // MI355X: one persistent workgroup per CU
+constexpr int kWideDepth = 4;  // weight tiles in flight per wave (even: see s_red)
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// The vocabulary projection: tens of thousands of output columns at <= 16 rows. A
+// persistent grid (one workgroup per CU and 16-row block) walks the 16-column tiles, tile
+// t on workgroup t mod gridDim.x, so the activations are loaded, normalised and converted
+// to f64 once per workgroup and stay in registers for every tile, and every CU gets the
+// same number of tiles to within one. Weights stream through a ring of kWideDepth tiles
+// in registers, kWideDepth - 1 tiles ahead of the MFMAs. Every load and store is a buffer
+// access whose range check does the masking (rows and columns past the end read zeros,
+// stores there are dropped), so none sits behind a branch and the compiler's wait before
+// each tile's MFMAs covers that tile's loads only. Same arithmetic, operand layout and
+// fixed wave order as linear_kernel. RC = chunks per wave (k_in <= 256 * RC).
+template <bool NORM, int RC>
+__global__ __launch_bounds__(kLinThreads) void linear_wide_kernel(LinArgs a) {
+    __shared__ double s_ss[kLinWaves][16];
+    __shared__ double s_red[2][kLinWaves][4][64];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int col = lane & 15;
+    const int g = lane >> 4;
+    const int m0 = blockIdx.y * 16;
+    const int nc = a.k_in / kLinK;
+    const int c0 = wave * nc / kLinWaves, c1 = (wave + 1) * nc / kLinWaves;
+    const int nch = c1 - c0;  // <= RC; chunks past it read as zeros
+    const int kbeg = c0 * kLinK + 8 * g;
+    const int row = m0 + col;
+    // Offsets are below 2^31 (the launcher checks); OR-ing in the sign bit of (limit - 1 -
+    // index) moves an index at or past its limit beyond every range. Arithmetic, not a
+    // select: a branch around a load would hide its count from the compiler's waits.
+    auto oob = [](int index, int limit) { return (uint32_t)(limit - 1 - index) & 0x80000000u; };
+
+    const __amdgpu_buffer_rsrc_t xr =
+        make_rsrc(a.x, (uint32_t)(((int64_t)(a.rows - 1) * a.ldx + a.k_in) * 4));
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, (uint32_t)((int64_t)a.n_out * a.k_in * 2));
+    const __amdgpu_buffer_rsrc_t orr =
+        make_rsrc(a.out, (uint32_t)(((int64_t)(a.rows - 1) * a.ldo + a.n_out) * 4));
+
+    float4_t xv[RC][2];
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+        const uint32_t off = ((uint32_t)(row * (int)a.ldx + kbeg + c * kLinK) * 4u) |
+                             oob(row, a.rows) | oob(c, nch);
+        xv[c][0] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+        xv[c][1] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0));
+    }
+    double scale = 1.0;
+    if constexpr (NORM) {
+        double ss = 0.0;
+#pragma unroll
+        for (int c = 0; c < RC; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const double d0 = (double)xv[c][0][i], d1 = (double)xv[c][1][i];
+                ss += d0 * d0;
+                ss += d1 * d1;
+            }
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        if (g == 0) s_ss[wave][col] = ss;
+        __syncthreads();
+        double tot = 0.0;
+#pragma unroll
+        for (int w = 0; w < kLinWaves; ++w) tot += s_ss[w][col];
+        scale = 1.0 / sqrt(tot / (double)a.k_in + a.eps);
+    }
+    double av[RC][8];
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+        float xs[8] = {xv[c][0][0], xv[c][0][1], xv[c][0][2], xv[c][0][3],
+                       xv[c][1][0], xv[c][1][1], xv[c][1][2], xv[c][1][3]};
+        if constexpr (NORM) {
+            const __amdgpu_buffer_rsrc_t nr = make_rsrc(a.norm_w, (uint32_t)(a.k_in * 4));
+            const uint32_t off = ((uint32_t)(kbeg + c * kLinK) * 4u) | oob(c, nch);
+            const float4_t w0 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(nr, off, 0, 0));
+            const float4_t w1 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(nr, off + 16, 0, 0));
+            const float nw[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xs[i] = (float)((double)xs[i] * scale) * nw[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) av[c][i] = (double)xs[i];
+    }
+
+    const int n_tiles = (a.n_out + 15) / 16;
+    // tile t's weights for this lane: row 16 t + col, this wave's chunks
+    auto wload = [&](int t, half8_t (&wv)[RC]) {
+        const int n = 16 * t + col;
+#pragma unroll
+        for (int c = 0; c < RC; ++c) {
+            const uint32_t off = ((uint32_t)(n * a.k_in + kbeg + c * kLinK) * 2u) |
+                                 oob(n, a.n_out) | oob(c, nch);
+            wv[c] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
+        }
+    };
+    half8_t wb[kWideDepth][RC];
+#pragma unroll
+    for (int j = 0; j < kWideDepth - 1; ++j) wload(blockIdx.x + j * gridDim.x, wb[j]);
+    // iteration i handles tile blockIdx.x + i * gridDim.x; its ring slot is i % depth, a
+    // constant inside the unrolled body. Loop exits are uniform across the workgroup.
+    for (int i0 = 0;; i0 += kWideDepth) {
+        bool done = false;
+#pragma unroll
+        for (int j = 0; j < kWideDepth; ++j) {
+            const int t = blockIdx.x + (i0 + j) * gridDim.x;
+            if (t >= n_tiles) {
+                done = true;
+                break;
+            }
+            wload(t + (kWideDepth - 1) * gridDim.x, wb[(j + kWideDepth - 1) % kWideDepth]);
+            double4_t acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int c = 0; c < RC; ++c)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc = mfma_f64(av[c][e], (double)(float)wb[j][c][e], acc);
+            double* red = &s_red[j & 1][0][0][0];  // kWideDepth is even: alternates
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[(wave * 4 + r) * 64 + lane] = acc[r];
+            __syncthreads();
+            // waves 0..3: output (row (l >> 4) + 4 r, column l & 15) of the tile
+            const int l = tid & 63, r = (tid >> 6) & 3;
+            double y = 0.0;
+#pragma unroll
+            for (int w = 0; w < kLinWaves; ++w) y += red[(w * 4 + r) * 64 + l];
+            const int orow = m0 + (l >> 4) + 4 * r;
+            const int on = 16 * t + (l & 15);
+            const uint32_t off = ((uint32_t)(orow * (int)a.ldo + on) * 4u) | oob(tid, 256) |
+                                 oob(orow, a.rows) | oob(on, a.n_out);
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, (float)y), orr, off, 0, 0);
+        }
+        if (done) break;
     }
 }
 
@@ -276,7 +481,7 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 template <bool NORM, int MODE, int NB>
 void launch_linear(const LinArgs& a, hipStream_t stream) {
-    const int cols = 16 * (MODE == kSwiGLU ? 1 : NB);
+    const int cols = MODE == kSwiGLU ? 8 : 16 * NB;
     const dim3 grid((unsigned)((a.n_out + cols - 1) / cols), (unsigned)((a.rows + 15) / 16));
     hipLaunchKernelGGL((linear_kernel<NORM, MODE, NB>), grid, dim3(kLinThreads), 0, stream, a);
 }
@@ -315,9 +520,36 @@ extern "C" int crucible_linear_f64acc(const float* x, int64_t ldx, const float* 
     LinArgs a{x, ldx, norm_w, (double)eps, static_cast<const half_t*>(w), nullptr, resid, out,
               ldo, (int)rows, (int)n_out, (int)k_in};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    // Wide outputs (the vocabulary projection) take 4 column blocks per workgroup so each
-    // activation fragment feeds 4 MFMAs; narrow ones keep more workgroups.
+    // Wide outputs (the vocabulary projection): the persistent tile walk when the K range
+    // fits its registers, else 4 column blocks per workgroup so each activation fragment
+    // feeds 4 MFMAs; narrow ones keep a workgroup per 16 columns.
     const bool wide = n_out >= 16 * 1024;
+    const int64_t wide_rc = (k_in / kLinK + kLinWaves - 1) / kLinWaves;
+    // the buffer ranges of the persistent walk are 32-bit
+    const bool wide_fits = (int64_t)n_out * k_in * 2 < (1LL << 31) &&
+                           ((rows - 1) * ldx + k_in) * 4 < (1LL << 31) &&
+                           ((rows - 1) * ldo + n_out) * 4 < (1LL << 31);
+    if (wide && !resid && wide_rc <= 4 && wide_fits) {
+        const int64_t row_blocks = (rows + 15) / 16;
+        const int64_t tiles = (n_out + 15) / 16;
+        const int64_t gx = std::max<int64_t>(1, std::min<int64_t>(tiles, kCUs / std::min<int64_t>(row_blocks, kCUs)));
+        const dim3 grid((unsigned)gx, (unsigned)row_blocks);
+        auto go = [&](auto norm_tag, auto rc_tag) {
+            hipLaunchKernelGGL((linear_wide_kernel<decltype(norm_tag)::value, decltype(rc_tag)::value>),
+                               grid, dim3(kLinThreads), 0, s, a);
+        };
+        auto by_rc = [&](auto norm_tag) {
+            switch (wide_rc) {
+                case 1: go(norm_tag, std::integral_constant<int, 1>{}); break;
+                case 2: go(norm_tag, std::integral_constant<int, 2>{}); break;
+                case 3: go(norm_tag, std::integral_constant<int, 3>{}); break;
+                default: go(norm_tag, std::integral_constant<int, 4>{}); break;
+            }
+        };
+        if (norm_w) by_rc(std::true_type{});
+        else by_rc(std::false_type{});
+        return fail_launch(what);
+    }
     if (resid) {
         if (norm_w) launch_linear<true, kResidual, 1>(a, s);
         else launch_linear<false, kResidual, 1>(a, s);
@@ -346,8 +578,8 @@ extern "C" int crucible_linear_swiglu_f64acc(const float* x, int64_t ldx, const 
               static_cast<const half_t*>(w_up), nullptr, out, ldo, (int)rows, (int)hidden,
               (int)k_in};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (norm_w) launch_linear<true, kSwiGLU, 2>(a, s);
-    else launch_linear<false, kSwiGLU, 2>(a, s);
+    if (norm_w) launch_linear<true, kSwiGLU, 1>(a, s);
+    else launch_linear<false, kSwiGLU, 1>(a, s);
     return fail_launch(what);
 }
 

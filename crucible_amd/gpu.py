@@ -341,3 +341,29 @@ class Gpu:
         _need(x, "x", dtype=torch.float32, numel=rows * cols)
         _need(out, "out", dtype=torch.int32, numel=rows)
         _lib.check(self.lib.crucible_argmax_rows(_ptr(x), _ptr(out), rows, cols, self._stream()))
+
+    def greedy_advance(self, logits, emb, x, tokens, history, step, positions, lens, done):
+        """The greedy step's tail on the device (argmax_rows at gpu_model.rs:1586, the
+        positions/lengths upload_batch sends, the next step's embed_batch at :1401):
+        tokens = argmax(logits) by the argmax_rows rule, history[step] = tokens,
+        positions += 1, lens += 1, x = emb[tokens], step += 1. logits [rows][cols] f32,
+        emb [cols][n_embd] f32, x [rows][n_embd] f32, history [max_steps][rows] int32,
+        step int64 [1], done int32/uint32 [1] (0 between calls)."""
+        rows, cols = logits.shape
+        n_embd = emb.shape[1]
+        _need(logits, "logits", dtype=torch.float32)
+        _need(emb, "emb", dtype=torch.float32, numel=cols * n_embd)
+        _need(x, "x", dtype=torch.float32, numel=rows * n_embd)
+        for t, nm in ((tokens, "tokens"), (positions, "positions"), (lens, "lens")):
+            _need(t, nm, dtype=torch.int32, numel=rows)
+        _need(history, "history", dtype=torch.int32)
+        if history.dim() != 2 or history.shape[1] != rows:
+            raise CrucibleError(_lib.ERR_INVALID, "history must be [max_steps][rows]")
+        _need(step, "step", dtype=torch.int64, numel=1)
+        _need(done, "done", numel=1)
+        if done.element_size() != 4:
+            raise CrucibleError(_lib.ERR_INVALID, "done must be a 4-byte counter")
+        _lib.check(self.lib.crucible_greedy_advance(
+            _ptr(logits), rows, cols, _ptr(emb), n_embd, _ptr(x), n_embd, _ptr(tokens),
+            _ptr(history), _ptr(step), history.shape[0], _ptr(positions), _ptr(lens), _ptr(done),
+            self._stream()))

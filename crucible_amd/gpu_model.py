@@ -286,15 +286,17 @@ class GpuModel:
             self._decode_step_native(st)
         else:
             self._decode_step_torch(st)
-        self._advance(st)
+            self._advance(st)
 
     def _decode_step_native(self, st):
-        """The step as this library's kernels (reference arithmetic), 5 launches a layer."""
+        """The step as this library's kernels (reference arithmetic), 5 launches a layer,
+        then the vocabulary projection (with the final norm) and the greedy tail. st["x"]
+        enters as the embedding of the token fed (the previous step's greedy tail, or the
+        caller, wrote it) and leaves as the next one's."""
         cfg, gpu = self.cfg, self.gpu
         b = st["batch"]
         eps = float(np.float32(cfg.norm_eps))
         x = st["x"]
-        torch.index_select(self.tok_emb, 0, st["tokens"], out=x)
         for layer_i, layer in enumerate(self.layers):
             gpu.linear_f64acc(x, layer["wqkv"], st["qkv"], norm_w=layer["attn_norm"], eps=eps)
             # RoPE of q and k, both appends and attention: one launch on the fused rows
@@ -309,8 +311,9 @@ class GpuModel:
             gpu.linear_swiglu_f64acc(x, layer["wg"], layer["wu"], st["act"],
                                      norm_w=layer["mlp_norm"], eps=eps)
             gpu.linear_f64acc(st["act"], layer["wd"], x, resid=x)
-        gpu.rmsnorm_rows(x, self.final_norm, st["h"], eps)
-        gpu.linear_f64acc(st["h"], self.lm_head, st["logits"])
+        gpu.linear_f64acc(x, self.lm_head, st["logits"], norm_w=self.final_norm, eps=eps)
+        gpu.greedy_advance(st["logits"], self.tok_emb, x, st["tokens"], st["history"],
+                           st["step"], st["positions"], st["lens"], st["done"])
 
     def _decode_step_torch(self, st):
         cfg, gpu = self.cfg, self.gpu
@@ -368,17 +371,16 @@ class GpuModel:
                 "lens": torch.from_numpy(lens + 1).to(dev),        # keys visible after append
                 "attn": torch.empty((batch, cfg.n_embd), dtype=torch.float32, device=dev),
                 "x": torch.empty((batch, cfg.n_embd), dtype=torch.float32, device=dev),
-                "h": torch.empty((batch, cfg.n_embd), dtype=torch.float32, device=dev),
                 "qkv": torch.empty((batch, cfg.n_embd + 2 * cfg.kv_dim), dtype=torch.float32,
                                    device=dev),
-                "q": torch.empty((batch, cfg.n_embd), dtype=torch.float32, device=dev),
-                "k": torch.empty((batch, cfg.kv_dim), dtype=torch.float32, device=dev),
-                "v": torch.empty((batch, cfg.kv_dim), dtype=torch.float32, device=dev),
                 "act": torch.empty((batch, cfg.hidden), dtype=torch.float32, device=dev),
                 "logits": torch.empty((batch, cfg.vocab_size), dtype=torch.float32, device=dev),
                 "history": torch.zeros((max(n_new - 1, 1), batch), dtype=torch.int32, device=dev),
                 "step": torch.zeros(1, dtype=torch.long, device=dev),
+                "done": torch.zeros(1, dtype=torch.int32, device=dev),
             }
+            if self.precision == "reference":  # the first step's input row
+                torch.index_select(self.tok_emb, 0, st["tokens"], out=st["x"])
             steps = n_new - 1
             if steps > 0 and graph:
                 g = self._capture(st)

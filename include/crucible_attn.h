@@ -242,6 +242,21 @@ int crucible_attention_prefill(const void* q, int q_dtype, const void* k_cache,
 int crucible_argmax_rows(const float* x, int32_t* out, int64_t rows, int64_t cols,
                          crucible_stream_t stream);
 
+/* The tail of a greedy batched decode step, kept on the device so the step replays as one
+ * graph. Replaces argmax_rows at the end of queue_decode_batch (gpu_model.rs:1586), the
+ * host's per-step upload of positions and lengths (upload_batch, gpu_model.rs:1088-1147)
+ * and the next step's embed_batch (gpu_model.rs:1401). For each row r < rows:
+ *   token = argmax(logits[r][0..cols)) by the argmax_rows rule; tokens[r] = token;
+ *   history[step * rows + r] = token when 0 <= step < max_steps;
+ *   positions[r] += 1; lens[r] += 1; x[r * ldx + k] = emb[token * n_embd + k], k < n_embd;
+ * then *step += 1. `done` is a caller-owned u32 that must read 0 before the first call;
+ * the call leaves it 0. Calls that overlap on the same buffers race. */
+int crucible_greedy_advance(const float* logits, int64_t rows, int64_t cols, const float* emb,
+                            int64_t n_embd, float* x, int64_t ldx, int32_t* tokens,
+                            int32_t* history, int64_t* step, int64_t max_steps,
+                            int32_t* positions, int32_t* lens, uint32_t* done,
+                            crucible_stream_t stream);
+
 /* ------------------------------------------------------------------ decode-step glue
  * The projections and row operations that surround attention in the reference's batched
  * decode step (gpu_model.rs:1393-1605 queue_decode_batch), with the reference CPU

@@ -113,6 +113,24 @@ def test_decode_step_glue_validates_before_launch():
     assert rc == _lib.ERR_INVALID
 
 
+def test_greedy_advance_validates_before_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced
+    args = lambda rows, cols, n_embd, ldx, hist, max_steps, done: (
+        fake, rows, cols, fake, n_embd, fake, ldx, fake, hist, fake, max_steps, fake, fake, done,
+        None)
+    # x rows narrower than the embedding
+    assert lib.crucible_greedy_advance(*args(16, 50257, 768, 700, fake, 8, fake)) == _lib.ERR_INVALID
+    # negative rows, empty vocabulary
+    assert lib.crucible_greedy_advance(*args(-1, 50257, 768, 768, fake, 8, fake)) == _lib.ERR_INVALID
+    assert lib.crucible_greedy_advance(*args(16, 0, 768, 768, fake, 8, fake)) == _lib.ERR_INVALID
+    # a history of max_steps > 0 rows must exist; the step counter's partner too
+    assert lib.crucible_greedy_advance(*args(16, 50257, 768, 768, None, 8, fake)) == _lib.ERR_INVALID
+    assert lib.crucible_greedy_advance(*args(16, 50257, 768, 768, fake, 8, None)) == _lib.ERR_INVALID
+    # zero rows: nothing to do
+    assert lib.crucible_greedy_advance(*args(0, 50257, 768, 768, fake, 8, fake)) == 0
+
+
 def test_qkv_decode_entry_validates_before_launch():
     lib = _lib.load()
     fake = ctypes.c_void_p(0x1000)

@@ -80,3 +80,58 @@ def test_argmax_batch16_logits(gpu, dev):
     gpu.argmax_rows(d_x, out, 16, VOCAB)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), [oracle.argmax(r) for r in x])
+
+
+def test_greedy_advance_matches_host_rule_and_bookkeeping(gpu, dev):
+    """The fused greedy tail: tokens by the host rule on the adversarial rows, history
+    row `step`, positions and lengths + 1, x = emb[token], step + 1, the counter back at
+    0; two calls in a row (the second sees the first's step)."""
+    rows_np = _rows(VOCAB)[:14]
+    rng = np.random.default_rng(11)
+    rows_np += [rng.standard_normal(VOCAB).astype(np.float32) for _ in range(2)]
+    n_embd, max_steps = 48, 3
+    emb = rng.standard_normal((VOCAB, n_embd)).astype(np.float32)
+    d_emb = torch.from_numpy(emb).to(dev)
+    rows = len(rows_np)
+    tokens = torch.full((rows,), -7, dtype=torch.int32, device=dev)
+    history = torch.full((max_steps, rows), -9, dtype=torch.int32, device=dev)
+    step = torch.zeros(1, dtype=torch.int64, device=dev)
+    positions = torch.arange(rows, dtype=torch.int32, device=dev) * 10
+    lens = positions + 1
+    done = torch.zeros(1, dtype=torch.int32, device=dev)
+    x = torch.full((rows, n_embd), np.nan, dtype=torch.float32, device=dev)
+    for call in range(2):
+        logits = np.stack(rows_np) if call == 0 else np.stack(rows_np[::-1])
+        want = np.array([oracle.argmax(r) for r in logits])
+        gpu.greedy_advance(torch.from_numpy(np.ascontiguousarray(logits)).to(dev), d_emb, x,
+                           tokens, history, step, positions, lens, done)
+        torch.cuda.synchronize()
+        assert np.array_equal(tokens.cpu().numpy(), want)
+        assert np.array_equal(history[call].cpu().numpy(), want)
+        assert np.array_equal(x.cpu().numpy(), emb[want])
+        assert int(step.item()) == call + 1
+        assert int(done.item()) == 0
+        base = np.arange(rows, dtype=np.int32) * 10 + call + 1
+        assert np.array_equal(positions.cpu().numpy(), base)
+        assert np.array_equal(lens.cpu().numpy(), base + 1)
+    assert np.all(history[2].cpu().numpy() == -9)
+
+
+def test_greedy_advance_past_history_end_skips_the_write(gpu, dev):
+    """A step at or past max_steps leaves the history alone (no write out of bounds)."""
+    rng = np.random.default_rng(12)
+    rows, vocab, n_embd = 4, 1000, 16
+    logits = torch.from_numpy(rng.standard_normal((rows, vocab)).astype(np.float32)).to(dev)
+    emb = torch.from_numpy(rng.standard_normal((vocab, n_embd)).astype(np.float32)).to(dev)
+    history = torch.full((1, rows), -9, dtype=torch.int32, device=dev)
+    step = torch.ones(1, dtype=torch.int64, device=dev)
+    tokens = torch.empty(rows, dtype=torch.int32, device=dev)
+    positions = torch.zeros(rows, dtype=torch.int32, device=dev)
+    lens = torch.ones(rows, dtype=torch.int32, device=dev)
+    done = torch.zeros(1, dtype=torch.int32, device=dev)
+    x = torch.empty((rows, n_embd), dtype=torch.float32, device=dev)
+    gpu.greedy_advance(logits, emb, x, tokens, history, step, positions, lens, done)
+    torch.cuda.synchronize()
+    assert np.all(history.cpu().numpy() == -9)
+    assert int(step.item()) == 2
+    assert np.array_equal(tokens.cpu().numpy(), logits.cpu().numpy().argmax(axis=1))

@@ -43,7 +43,7 @@ def _mat(rng, shape, std):
 
 @pytest.mark.parametrize("rows,n_out,k_in", [(1, 1152, 768), (16, 768, 768), (5, 200, 2048),
                                              (33, 768, 256), (16, 50257, 768), (4, 256, 704),
-                                             (2, 64, 96)])
+                                             (2, 64, 96), (33, 16400, 256), (3, 16400, 1056)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_linear_matches_f64_matvec(gpu, dev, rows, n_out, k_in, norm):
     rng = np.random.default_rng(rows * 7 + n_out + k_in + norm)
@@ -79,9 +79,9 @@ def test_linear_residual_in_place(gpu, dev):
     assert np.abs(got - want).max() <= 4 * np.abs(want).max() * 2.0 ** -24
 
 
-def test_swiglu_matches_reference_ops(gpu, dev):
-    rng = np.random.default_rng(9)
-    rows, hidden, k_in = 16, 2048, 768
+@pytest.mark.parametrize("rows,hidden,k_in", [(16, 2048, 768), (5, 2045, 96)])
+def test_swiglu_matches_reference_ops(gpu, dev, rows, hidden, k_in):
+    rng = np.random.default_rng(9 + hidden)
     x = rng.standard_normal((rows, k_in), dtype=np.float32)
     wg = _mat(rng, (hidden, k_in), 0.05)
     wu = _mat(rng, (hidden, k_in), 0.05)

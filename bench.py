@@ -49,6 +49,9 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true")
+    p.add_argument("--extras", default="decode,prefill,e2e",
+                   help="comma list of extra groups to run: decode (the other decode "
+                        "shapes), prefill (configs 1 and 4), e2e (config 5)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 256 MiB device copy (PMC traffic calibration)")
     return p.parse_args()
@@ -424,7 +427,8 @@ def main():
     del fused_graphs
 
     extras = {}
-    if not args.no_extras:
+    groups = set() if args.no_extras else {g.strip() for g in args.extras.split(",")}
+    if "decode" in groups:
         # the reference's three launches per layer, and attention alone, same batches
         for mode in ("separate", "decode"):
             graphs = b16.capture(mode)
@@ -457,13 +461,15 @@ def main():
                                          "bytes_per_launch": int(by / 12)}
             del graphs, mha
         torch.cuda.empty_cache()
+    if "prefill" in groups:
         extras["prefill_config1"] = bench_prefill(gpu, dev, W.config1_prefill(n_kv_head=12))
         extras["prefill_config1_gqa3"] = bench_prefill(gpu, dev, W.config1_prefill(n_kv_head=3))
         extras["packed_config4"] = bench_prefill(gpu, dev, W.config4_packed())
         torch.cuda.empty_cache()
+    if "e2e" in groups:
         extras["e2e_config5"] = bench_e2e(gpu)
-        for k, v in extras.items():
-            log(f"{k}: {v}")
+    for k, v in extras.items():
+        log(f"{k}: {v}")
 
     if args.copy_probe:
         src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
@@ -477,12 +483,14 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(b16, args.cpu_seconds)
         log(f"cpu baseline: {cpu}")
-        if not args.no_extras:
-            # the reference CPU path beside the other configs
+        # the reference CPU path beside the other configs
+        if "decode_b1_ctx1024" in extras:
             extras["decode_b1_ctx1024"]["cpu"] = cpu_decode_b1(2.0)
+        if "prefill_config1" in extras:
             extras["prefill_config1"]["cpu"] = cpu_prefill(W.config1_prefill(n_kv_head=12), 2.0)
             extras["prefill_config1_gqa3"]["cpu"] = cpu_prefill(W.config1_prefill(n_kv_head=3), 2.0)
             extras["packed_config4"]["cpu"] = cpu_prefill(W.config4_packed(), 2.0)
+        if extras:
             log("cpu beside the extras: " + str({k: v.get("cpu") for k, v in extras.items()
                                                  if isinstance(v, dict) and "cpu" in v}))
 

@@ -321,6 +321,20 @@ def test_decode_shapes_agree(gpu, dev, monkeypatch, order):
             assert np.abs(o2 - want).max() <= TOL, (pages, waves)
 
 
+def test_grid_orders_are_bit_identical(gpu, dev, monkeypatch):
+    """The grid order only places the workgroups: splits merge in split order whatever
+    order they finish in, so both orders give the same bits."""
+    lens = [1, 17, 256, 257, 700, 2048, 1999, 64, 0, 1024]
+    positions = [max(n - 1, 0) for n in lens]
+    outs = []
+    for order in ("0", "1"):
+        monkeypatch.setenv("CRUCIBLE_DECODE_REQUEST_MAJOR", order)
+        _, _, _, _, o2, o1, _, _ = _fused_vs_separate(gpu, dev, lens, positions, 12, 3, seed=5)
+        assert np.array_equal(o2.view(np.uint32), o1.view(np.uint32))
+        outs.append(o2.view(np.uint32))
+    assert np.array_equal(outs[0], outs[1])
+
+
 def test_workspace_shared_across_batch_sizes(gpu, dev):
     """One workspace (sized for the largest batch) serves decode calls whose batch size
     changes from call to call, as the engine's active count does step to step."""

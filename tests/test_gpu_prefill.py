@@ -107,6 +107,20 @@ def test_future_pages_do_not_affect_output(gpu, dev, case):
         assert np.array_equal(clean.view(np.uint32), p.result().view(np.uint32))
 
 
+def test_repeated_launches_are_bit_identical(gpu, dev):
+    """The same call twice gives the same bits: every reduction has a fixed order, and no
+    tile is read before it has landed or after it is reused."""
+    for case in [c for c in CASES if c.name in ("single-1024", "offset-255", "4x256", "ragged-profile-1")]:
+        fx = A.fixture(case)
+        d = Device(fx, dev)
+        run_segments(gpu, d)
+        first = d.result().copy()
+        for _ in range(3):
+            d.reset()
+            run_segments(gpu, d)
+            assert np.array_equal(d.result().view(np.uint32), first.view(np.uint32)), case.name
+
+
 def test_single_sequence_params_and_contiguous_forms(gpu, dev):
     """attention_prefill_paged (params[5] offset) and attention_prefill (contiguous)."""
     for case in [c for c in CASES if c.name in ("single-1024", "single-941", "offset-255")]:

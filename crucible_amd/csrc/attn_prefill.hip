@@ -55,35 +55,49 @@ constexpr int kWaitVm8Lgkm0 = 0x0078;
 constexpr int kThreads = 512;  // 8 waves: 4 row/head slots x 2 tile parities
 constexpr float kLazyLog2 = 8.0f;  // running-max slack (log2 units) before a rescale
 
-// Max over lanes L and L ^ 16 (resp. L ^ 32): two steps reduce the 4 lane groups of a
-// column. v_permlane16_swap a, b swaps the odd 16-lane rows of a with the even rows of b
-// (permlane32_swap: the upper half of a with the lower half of b), so from a = b = v each
-// lane ends with v[L] in one operand and v[L ^ 16] (resp. v[L ^ 32]) in the other. It is
-// written as asm because this compiler's builtin returns the first operand in both halves
-// of its result. s_nop 1 covers the VALU-write -> permlane-read hazard.
+// Hand-written instructions and the hazards the compiler cannot see. The compiler inserts
+// wait states after the instructions it emits, but an asm block is opaque to it: a block
+// that reads MFMA results, the result of a transcendental op, or writes what an MFMA reads
+// must supply the wait states itself. CDNA does not interlock MFMA results for VALU reads
+// (an 8-pass 16x16x32 result needs about 10 wait states), a VALU read of a v_exp_f32
+// result needs 1, a VALU write read by an MFMA needs 2, and v_permlane*_swap needs 2 around
+// its VALU neighbours. Missing ones do not fault: the read returns the register's previous
+// value, depending on how the other waves' issue fell, so results vary in the last bits
+// from launch to launch (a wrong running max only changes the softmax's rounding).
 //
-// The maxima are asm as well: fmaxf on values the compiler cannot prove canonical (MFMA
-// results, asm outputs) costs an extra canonicalising v_max per operand, and these
-// scores are never signalling NaNs.
-__device__ __forceinline__ float vmax(float a, float b) {
-    float d;
-    asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
-    return d;
-}
-__device__ __forceinline__ float vmax3(float a, float b, float c) {
-    float d;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-    return d;
-}
-__device__ __forceinline__ float max_xor16(float v) {
-    float a = v, b = v;
-    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return vmax(a, b);
-}
-__device__ __forceinline__ float max_xor32(float v) {
-    float a = v, b = v;
-    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return vmax(a, b);
+// Column max of a lane's 16 scores, then over its 4 lane groups (lanes L, L ^ 16, L ^ 32,
+// L ^ 48): v_max3 chains, then v_permlane16_swap / v_permlane32_swap of the value with
+// itself (one operand ends with v[L], the other with v[L ^ 16], resp. v[L ^ 32]) and a max.
+// It is asm because fmaxf on MFMA results costs a canonicalising v_max per operand, and
+// this compiler's permlane swap builtins return the first operand in both halves. The
+// block opens with 16 wait states for the MFMA results it reads.
+__device__ __forceinline__ float tile_max(const float4_t (&st)[4]) {
+    float r, t;
+    asm("s_nop 7\n\ts_nop 7\n\t"
+        "v_max3_f32 %0, %2, %3, %4\n\t"
+        "v_max3_f32 %0, %0, %5, %6\n\t"
+        "v_max3_f32 %0, %0, %7, %8\n\t"
+        "v_max3_f32 %0, %0, %9, %10\n\t"
+        "v_max3_f32 %0, %0, %11, %12\n\t"
+        "v_max3_f32 %0, %0, %13, %14\n\t"
+        "v_max3_f32 %0, %0, %15, %16\n\t"
+        "v_max_f32 %0, %0, %17\n\t"
+        "v_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\t"
+        "v_permlane16_swap_b32 %0, %1\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32 %0, %0, %1\n\t"
+        "v_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\t"
+        "v_permlane32_swap_b32 %0, %1\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32 %0, %0, %1"
+        : "=&v"(r), "=&v"(t)
+        : "v"(st[0][0]), "v"(st[0][1]), "v"(st[0][2]), "v"(st[0][3]), "v"(st[1][0]),
+          "v"(st[1][1]), "v"(st[1][2]), "v"(st[1][3]), "v"(st[2][0]), "v"(st[2][1]),
+          "v"(st[2][2]), "v"(st[2][3]), "v"(st[3][0]), "v"(st[3][1]), "v"(st[3][2]),
+          "v"(st[3][3]));
+    return r;
 }
 
 // One lane's 16 scores of a 64-key tile, st[kb][r] = S^T[key 16 kb + 4 grp + r][q = col],
@@ -99,17 +113,6 @@ __device__ __forceinline__ void mask_tile(float4_t (&st)[4], int lim) {
         for (int r = 0; r < 4; ++r) st[kb][r] = (16 * kb + r <= lim) ? st[kb][r] : -INFINITY;
 }
 
-// Column max of the tile (over the lane's 16 scores and its 4 lane groups), unscaled.
-__device__ __forceinline__ float tile_max(const float4_t (&st)[4]) {
-    float a = vmax3(st[0][0], st[0][1], st[0][2]);
-    float b = vmax3(st[1][0], st[1][1], st[1][2]);
-    a = vmax3(a, st[0][3], st[2][0]);
-    b = vmax3(b, st[1][3], st[3][0]);
-    a = vmax3(a, st[2][1], st[2][2]);
-    b = vmax3(b, st[3][1], st[3][2]);
-    return max_xor32(max_xor16(vmax3(a, b, vmax(st[2][3], st[3][3]))));
-}
-
 // P = exp2(s * scale - mu) (one FMA and one exp per score), split into fp16 P = hi + lo
 // (hi truncates, lo = RNE(p - hi): exact to about 2^-22 relative), as the hi/lo
 // operands of the PV product: pb/pl[0] hold keys 0..31 of the tile, [1] keys 32..63, in
@@ -120,14 +123,20 @@ __device__ __forceinline__ float tile_max(const float4_t (&st)[4]) {
 // hi) from v_fma_mix{lo,hi}_f16, which take hi as an fp16 operand, form p - hi exactly in
 // f32 and round once to fp16 into one half of the packed result (one instruction per value
 // where the C form needs a convert, a subtract and half a pack).
+//
+// It reads v_exp_f32 results (1 wait state) and an MFMA reads what it writes (2 wait
+// states): the block opens with s_nop 0 and ends with s_nop 1.
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint32_t split_lo2(float p0, float p1, uint32_t hi) {
-    uint32_t lo;
-    asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]\n\t"
-        "v_fma_mixhi_f16 %0, %1, -1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-        : "=&v"(lo)
-        : "v"(hi), "v"(p0), "v"(p1));
-    return lo;
+__device__ __forceinline__ void split_lo4(const float (&p)[4], uint32_t h01, uint32_t h23,
+                                          uint32_t& lo01, uint32_t& lo23) {
+    asm("s_nop 0\n\t"
+        "v_fma_mixlo_f16 %0, %2, -1.0, %4 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, %2, -1.0, %5 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixlo_f16 %1, %3, -1.0, %6 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %1, %3, -1.0, %7 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "s_nop 1"
+        : "=&v"(lo01), "=&v"(lo23)
+        : "v"(h01), "v"(h23), "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]));
 }
 __device__ __forceinline__ float tile_p(const float4_t (&st)[4], float scale, float mu,
                                         half8_t (&pb)[2], half8_t (&pl)[2]) {
@@ -139,13 +148,14 @@ __device__ __forceinline__ float tile_p(const float4_t (&st)[4], float scale, fl
 #pragma unroll
         for (int r = 0; r < 4; ++r) pf[r] = fast_exp2(__builtin_fmaf(st[kb][r], scale, -mu));
         part[kb] = (pf[0] + pf[1]) + (pf[2] + pf[3]);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t h =
-                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pf[2 * j], pf[2 * j + 1]));
-            hw[kb >> 1][(kb & 1) * 2 + j] = h;
-            lw[kb >> 1][(kb & 1) * 2 + j] = split_lo2(pf[2 * j], pf[2 * j + 1], h);
-        }
+        const uint32_t h01 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pf[0], pf[1]));
+        const uint32_t h23 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pf[2], pf[3]));
+        uint32_t lo01, lo23;
+        split_lo4(pf, h01, h23, lo01, lo23);
+        hw[kb >> 1][(kb & 1) * 2] = h01;
+        hw[kb >> 1][(kb & 1) * 2 + 1] = h23;
+        lw[kb >> 1][(kb & 1) * 2] = lo01;
+        lw[kb >> 1][(kb & 1) * 2 + 1] = lo23;
     }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {

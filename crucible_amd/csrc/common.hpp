@@ -79,9 +79,10 @@ constexpr int kPolicyCoherent = 16;
 // must be wave-uniform). Issued through inline asm so the compiler does not track the
 // LDS write: the caller orders it with its own s_waitcnt vmcnt + s_barrier, which lets
 // several tiles stay in flight while earlier ones are read (the compiler would otherwise
-// wait for every outstanding load before each LDS read).
+// wait for every outstanding load before each LDS read). An SALU write of M0 needs one
+// wait state before a load with LDS reads it (s_nop 0); the compiler adds none inside asm.
 __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :
                  : "v"(src), "s"(lds_base)
                  : "memory", "m0");

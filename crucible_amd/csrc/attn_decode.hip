@@ -113,7 +113,10 @@ __device__ __forceinline__ float load_coherent(const float* p) {
 }
 
 // Merge the partials of splits [0, n_active) for query head hh, dims 4*d4 .. 4*d4+3.
-// Loads are issued eight splits at a time so the merge costs n_active / 8 round trips.
+// Loads are issued CW splits at a time so the merge costs n_active / CW round trips. CW is
+// 16 for launches with more than 8 splits (batch 1 at ctx 1024: 16 splits, one round trip
+// instead of two) and 8 otherwise: the wider form's registers slow the common case.
+template <int CW>
 __device__ __forceinline__ void combine_partials(const DecodeArgs& a, int b, int hh, int d4,
                                                  int n_active) {
     const int64_t slot0 = ((int64_t)b * a.n_head + hh) * a.n_splits;
@@ -121,11 +124,11 @@ __device__ __forceinline__ void combine_partials(const DecodeArgs& a, int b, int
     float M = -INFINITY;
     float L = 0.0f;
     float4_t o = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < n_active; s0 += 8) {
-        float mv[8], lv[8];
-        float4_t ov[8];
+    for (int s0 = 0; s0 < n_active; s0 += CW) {
+        float mv[CW], lv[CW];
+        float4_t ov[CW];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < CW; ++j) {
             if (s0 + j < n_active) {
                 const int64_t slot = slot0 + s0 + j;
                 mv[j] = load_coherent(a.pm + slot);
@@ -142,12 +145,12 @@ __device__ __forceinline__ void combine_partials(const DecodeArgs& a, int b, int
         }
         float mx = M;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, mv[j]);
+        for (int j = 0; j < CW; ++j) mx = fmaxf(mx, mv[j]);
         const float sc = fast_exp2(M - mx);  // M = -inf on the first pass: sc = 0, L = o = 0
         L *= sc;
         o = o * sc;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < CW; ++j) {
             if (lv[j] > 0.0f) {
                 const float w = fast_exp2(mv[j] - mx);
                 L += lv[j] * w;
@@ -277,7 +280,9 @@ __device__ __forceinline__ void store_new_row(const DecodeArgs& a, const NewRow&
 
 // RMAJOR: grid (kv head, request, split) instead of (split, kv head, request).
 // ROPE (with QF32 and APPEND): rotate q and the appended K row at the append position.
-template <int PAGES, int WAVES, bool QF32, bool APPEND, bool PAGED, bool RMAJOR, bool ROPE>
+// CW: splits merged per round trip by the combining workgroup (combine_partials).
+template <int PAGES, int WAVES, bool QF32, bool APPEND, bool PAGED, bool RMAJOR, bool ROPE,
+          int CW = 8>
 __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     static_assert(!ROPE || (QF32 && APPEND), "RoPE is fused for f32 rows with the append");
     __shared__ float4_t s_acc[WAVES][16][17];  // [wave][col][dim/4], padded
@@ -542,7 +547,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     }
     __syncthreads();
     if (!s_last) return;
-    if (owner) combine_partials(a, b, hh, d4, n_active);
+    if (owner) combine_partials<CW>(a, b, hh, d4, n_active);
 }
 
 // Second-pass combine for callers that own the partials without a counter
@@ -557,7 +562,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
     if (n_active <= 1) return;
     const int ccol = threadIdx.x >> 4;
     if (ccol >= a.n_rep) return;
-    combine_partials(a, b, g * a.n_rep + ccol, threadIdx.x & 15, n_active);
+    combine_partials<8>(a, b, g * a.n_rep + ccol, threadIdx.x & 15, n_active);
 }
 
 struct DecodeShape {
@@ -589,7 +594,10 @@ bool launch_shape(const DecodeArgs& a, DecodeShape sh, bool rmajor, dim3 grid,
                   hipStream_t stream) {
 #define CRUCIBLE_DECODE_CASE(P, W)                                                             \
     if (sh.pages == P && sh.waves == W) {                                                       \
-        if (rmajor)                                                                             \
+        if (rmajor && a.n_splits > 8)                                                           \
+            hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, true, ROPE, 16>), grid,\
+                               dim3(W * 64), 0, stream, a);                                     \
+        else if (rmajor)                                                                        \
             hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, true, ROPE>), grid,    \
                                dim3(W * 64), 0, stream, a);                                     \
         else                                                                                    \

@@ -12,7 +12,7 @@
 // where order() maps floats to unsigned integers with the same ordering (and maps -0.0
 // to +0.0). The maximum key is the highest value with the lowest index among ties, so a
 // plain max-reduction in any order gives the host's answer; the v[0]-is-NaN case is
-// checked once per row. One workgroup of 1024 threads per row; each thread keeps eight
+// checked once per row. One workgroup of 1024 threads per row; each thread keeps up to 50
 // loads in flight.
 #include "common.hpp"
 
@@ -31,22 +31,39 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t i) {
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
 // Index of the row's maximum by the host rule, in thread 0 (other threads: unspecified).
-// Every thread keeps eight loads in flight per round.
+// Each thread scans its columns in increasing order keeping (value, index) of its first
+// maximum: a strict `>` never takes a NaN, keeps the earlier of equal values and treats
+// -0.0 and +0.0 as equal, which is the host rule within the thread (a compare and two
+// selects per element, where a 64-bit key per element costs about ten instructions and
+// made one row's scan VALU-bound on its CU). The threads' winners then meet as 64-bit
+// keys. Each pass issues all of a thread's loads at once (50: one pass covers 51,200
+// columns, the 50,257-word vocabulary included, within 105 VGPRs); loads past the row end
+// are predicated off.
 __device__ __forceinline__ int32_t row_argmax(const float* __restrict__ r, int64_t cols) {
     __shared__ uint64_t s_key[kArgmaxThreads / 64];
     const int t = threadIdx.x;
-    uint64_t best = 0;
-    int64_t i = t;
-    constexpr int kU = 8;
-    for (; i + (kU - 1) * kArgmaxThreads < cols; i += kU * kArgmaxThreads) {
+    const int n = (int)cols;  // < 2^31 (the launchers check)
+    float bv = -INFINITY;
+    int bi = -1;  // no candidate yet
+    constexpr int kU = 50;
+    for (int i0 = t; i0 < n; i0 += kU * kArgmaxThreads) {
         float v[kU];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) v[u] = r[i + u * kArgmaxThreads];
+        for (int u = 0; u < kU; ++u) {
+            const int i = i0 + u * kArgmaxThreads;
+            v[u] = i < n ? r[i] : -INFINITY;
+        }
 #pragma unroll
-        for (int u = 0; u < kU; ++u)
-            best = max_u64(best, argmax_key(v[u], (uint32_t)(i + u * kArgmaxThreads)));
+        for (int u = 0; u < kU; ++u) {
+            const bool take = v[u] > bv;
+            bv = take ? v[u] : bv;
+            bi = take ? i0 + u * kArgmaxThreads : bi;
+        }
     }
-    for (; i < cols; i += kArgmaxThreads) best = max_u64(best, argmax_key(r[i], (uint32_t)i));
+    // A thread that saw nothing above -inf offers no candidate: under the host rule a -inf
+    // (or NaN) element never displaces index 0, so a row whose maximum is -inf answers 0,
+    // as an empty key set does below.
+    uint64_t best = bi < 0 ? 0 : argmax_key(bv, (uint32_t)bi);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) best = max_u64(best, __shfl_xor(best, off));
     if ((t & 63) == 0) s_key[t >> 6] = best;
@@ -92,9 +109,12 @@ __global__ __launch_bounds__(kArgmaxThreads) void greedy_advance_kernel(
     float* dst = x + (int64_t)row * ldx;
     for (int64_t k = threadIdx.x; k < n_embd; k += kArgmaxThreads) dst[k] = src[k];
     if (threadIdx.x == 0) {
-        // the row that completes the step advances it; every row has read it by then
+        // The row that completes the step advances it. Every row has read the step by then:
+        // its value was used for the history store before this atomic issued. Relaxed
+        // order suffices (what this launch writes reaches the next one at the kernel
+        // boundary); acquire-release would write back and invalidate the whole L2 here.
         const uint32_t prev =
-            __hip_atomic_fetch_add(done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (prev == (uint32_t)(rows - 1)) {
             __hip_atomic_store(step, *step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -110,7 +130,7 @@ using namespace crucible;
 extern "C" int crucible_argmax_rows(const float* x, int32_t* out, int64_t rows, int64_t cols,
                                     crucible_stream_t stream) {
     const char* what = "argmax_rows";
-    CRUCIBLE_CHECK(rows >= 0 && rows <= INT32_MAX && cols > 0 && cols < 0xffffffffLL,
+    CRUCIBLE_CHECK(rows >= 0 && rows <= INT32_MAX && cols > 0 && cols < 0x7fffffffLL,
                    CRUCIBLE_ERR_INVALID, "%s: rows=%lld cols=%lld", what, (long long)rows,
                    (long long)cols);
     if (rows == 0) return CRUCIBLE_OK;

@@ -274,7 +274,8 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
 // ---------------------------------------------------------------- wide projections
 
 constexpr int kCUs = 256;      // MI355X: one persistent workgroup per CU
-constexpr int kWideDepth = 4;  // weight tiles in flight per wave (even: see s_red)
+constexpr int kWideDepth = 4;  // weight tiles in flight per wave
+constexpr int kWideMaxIters = 16;  // tiles per workgroup (the walk is fully unrolled)
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -315,14 +316,39 @@ __global__ __launch_bounds__(kLinThreads) void linear_wide_kernel(LinArgs a) {
     const __amdgpu_buffer_rsrc_t orr =
         make_rsrc(a.out, (uint32_t)(((int64_t)(a.rows - 1) * a.ldo + a.n_out) * 4));
 
-    float4_t xv[RC][2];
+    float4_t xv[RC][2], nv[RC][2];
 #pragma unroll
     for (int c = 0; c < RC; ++c) {
         const uint32_t off = ((uint32_t)(row * (int)a.ldx + kbeg + c * kLinK) * 4u) |
                              oob(row, a.rows) | oob(c, nch);
         xv[c][0] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
         xv[c][1] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0));
+        if constexpr (NORM) {
+            const __amdgpu_buffer_rsrc_t nr = make_rsrc(a.norm_w, (uint32_t)(a.k_in * 4));
+            const uint32_t noff = ((uint32_t)(kbeg + c * kLinK) * 4u) | oob(c, nch);
+            nv[c][0] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(nr, noff, 0, 0));
+            nv[c][1] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(nr, noff + 16, 0, 0));
+        }
     }
+
+    const int n_tiles = (a.n_out + 15) / 16;
+    // tile t's weights for this lane: row 16 t + col, this wave's chunks
+    auto wload = [&](int t, half8_t (&wv)[RC]) {
+        const int n = 16 * t + col;
+#pragma unroll
+        for (int c = 0; c < RC; ++c) {
+            const uint32_t off = ((uint32_t)(n * a.k_in + kbeg + c * kLinK) * 2u) |
+                                 oob(n, a.n_out) | oob(c, nch);
+            wv[c] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
+        }
+    };
+    // The first weight tiles are requested before the activations are normalised, so their
+    // latency overlaps that work (one workgroup per CU: registers are not the limit).
+    half8_t wb[kWideDepth][RC];
+#pragma unroll
+    for (int j = 0; j < kWideDepth - 1; ++j) wload(blockIdx.x + j * gridDim.x, wb[j]);
+    __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the wait for the activations
+
     double scale = 1.0;
     if constexpr (NORM) {
         double ss = 0.0;
@@ -349,11 +375,8 @@ __global__ __launch_bounds__(kLinThreads) void linear_wide_kernel(LinArgs a) {
         float xs[8] = {xv[c][0][0], xv[c][0][1], xv[c][0][2], xv[c][0][3],
                        xv[c][1][0], xv[c][1][1], xv[c][1][2], xv[c][1][3]};
         if constexpr (NORM) {
-            const __amdgpu_buffer_rsrc_t nr = make_rsrc(a.norm_w, (uint32_t)(a.k_in * 4));
-            const uint32_t off = ((uint32_t)(kbeg + c * kLinK) * 4u) | oob(c, nch);
-            const float4_t w0 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(nr, off, 0, 0));
-            const float4_t w1 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(nr, off + 16, 0, 0));
-            const float nw[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+            const float nw[8] = {nv[c][0][0], nv[c][0][1], nv[c][0][2], nv[c][0][3],
+                                 nv[c][1][0], nv[c][1][1], nv[c][1][2], nv[c][1][3]};
 #pragma unroll
             for (int i = 0; i < 8; ++i) xs[i] = (float)((double)xs[i] * scale) * nw[i];
         }
@@ -361,53 +384,36 @@ __global__ __launch_bounds__(kLinThreads) void linear_wide_kernel(LinArgs a) {
         for (int i = 0; i < 8; ++i) av[c][i] = (double)xs[i];
     }
 
-    const int n_tiles = (a.n_out + 15) / 16;
-    // tile t's weights for this lane: row 16 t + col, this wave's chunks
-    auto wload = [&](int t, half8_t (&wv)[RC]) {
-        const int n = 16 * t + col;
+    // Iteration i handles tile blockIdx.x + i * gridDim.x from ring slot i % depth. The walk
+    // is unrolled whole (the launcher keeps it within kWideMaxIters tiles a workgroup):
+    // straight-line code lets the compiler's wait before each tile's MFMAs count exactly
+    // the loads still in flight, where a loop's back edge made it drain them all. The exit
+    // is uniform across the workgroup.
 #pragma unroll
-        for (int c = 0; c < RC; ++c) {
-            const uint32_t off = ((uint32_t)(n * a.k_in + kbeg + c * kLinK) * 2u) |
-                                 oob(n, a.n_out) | oob(c, nch);
-            wv[c] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
-        }
-    };
-    half8_t wb[kWideDepth][RC];
+    for (int i = 0; i < kWideMaxIters; ++i) {
+        const int t = blockIdx.x + i * gridDim.x;
+        if (t >= n_tiles) break;
+        wload(t + (kWideDepth - 1) * gridDim.x, wb[(i + kWideDepth - 1) % kWideDepth]);
+        double4_t acc = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-    for (int j = 0; j < kWideDepth - 1; ++j) wload(blockIdx.x + j * gridDim.x, wb[j]);
-    // iteration i handles tile blockIdx.x + i * gridDim.x; its ring slot is i % depth, a
-    // constant inside the unrolled body. Loop exits are uniform across the workgroup.
-    for (int i0 = 0;; i0 += kWideDepth) {
-        bool done = false;
+        for (int c = 0; c < RC; ++c)
 #pragma unroll
-        for (int j = 0; j < kWideDepth; ++j) {
-            const int t = blockIdx.x + (i0 + j) * gridDim.x;
-            if (t >= n_tiles) {
-                done = true;
-                break;
-            }
-            wload(t + (kWideDepth - 1) * gridDim.x, wb[(j + kWideDepth - 1) % kWideDepth]);
-            double4_t acc = {0.0, 0.0, 0.0, 0.0};
+            for (int e = 0; e < 8; ++e)
+                acc = mfma_f64(av[c][e], (double)(float)wb[i % kWideDepth][c][e], acc);
+        double* red = &s_red[i & 1][0][0][0];
 #pragma unroll
-            for (int c = 0; c < RC; ++c)
+        for (int r = 0; r < 4; ++r) red[(wave * 4 + r) * 64 + lane] = acc[r];
+        __syncthreads();
+        // waves 0..3: output (row (l >> 4) + 4 r, column l & 15) of the tile
+        const int l = tid & 63, r = (tid >> 6) & 3;
+        double y = 0.0;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc = mfma_f64(av[c][e], (double)(float)wb[j][c][e], acc);
-            double* red = &s_red[j & 1][0][0][0];  // kWideDepth is even: alternates
-#pragma unroll
-            for (int r = 0; r < 4; ++r) red[(wave * 4 + r) * 64 + lane] = acc[r];
-            __syncthreads();
-            // waves 0..3: output (row (l >> 4) + 4 r, column l & 15) of the tile
-            const int l = tid & 63, r = (tid >> 6) & 3;
-            double y = 0.0;
-#pragma unroll
-            for (int w = 0; w < kLinWaves; ++w) y += red[(w * 4 + r) * 64 + l];
-            const int orow = m0 + (l >> 4) + 4 * r;
-            const int on = 16 * t + (l & 15);
-            const uint32_t off = ((uint32_t)(orow * (int)a.ldo + on) * 4u) | oob(tid, 256) |
-                                 oob(orow, a.rows) | oob(on, a.n_out);
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, (float)y), orr, off, 0, 0);
-        }
-        if (done) break;
+        for (int w = 0; w < kLinWaves; ++w) y += red[(w * 4 + r) * 64 + l];
+        const int orow = m0 + (l >> 4) + 4 * r;
+        const int on = 16 * t + (l & 15);
+        const uint32_t off = ((uint32_t)(orow * (int)a.ldo + on) * 4u) | oob(tid, 256) |
+                             oob(orow, a.rows) | oob(on, a.n_out);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, (float)y), orr, off, 0, 0);
     }
 }
 
@@ -532,7 +538,11 @@ extern "C" int crucible_linear_f64acc(const float* x, int64_t ldx, const float* 
     if (wide && !resid && wide_rc <= 4 && wide_fits) {
         const int64_t row_blocks = (rows + 15) / 16;
         const int64_t tiles = (n_out + 15) / 16;
-        const int64_t gx = std::max<int64_t>(1, std::min<int64_t>(tiles, kCUs / std::min<int64_t>(row_blocks, kCUs)));
+        // one workgroup per CU (and row block), or more when a CU would need more than
+        // kWideMaxIters tiles
+        const int64_t per_cu = std::max<int64_t>(1, kCUs / std::min<int64_t>(row_blocks, kCUs));
+        const int64_t gx = std::min<int64_t>(
+            tiles, std::max<int64_t>(per_cu, (tiles + kWideMaxIters - 1) / kWideMaxIters));
         const dim3 grid((unsigned)gx, (unsigned)row_blocks);
         auto go = [&](auto norm_tag, auto rc_tag) {
             hipLaunchKernelGGL((linear_wide_kernel<decltype(norm_tag)::value, decltype(rc_tag)::value>),

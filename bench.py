@@ -416,7 +416,7 @@ def main():
     bytes_per_launch = step_bytes / b16.n_layer
     achieved = bytes_per_launch / (launch_us * 1e-6) / 1e9
     log(f"fused decode launch: {launch_us:.2f} us avg, {achieved:.1f} GB/s")
-    kernel = "decode_kernel<2, 8, false, true, true, true, false, 8>"
+    kernel = "decode_kernel<2, 8, false, true, true, 2, false, 8>"
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": pmc_traffic(kernel),

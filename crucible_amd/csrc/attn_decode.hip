@@ -42,6 +42,7 @@
 
 #include <cmath>
 #include <cstdlib>
+#include <cstring>
 
 namespace crucible {
 namespace {
@@ -278,10 +279,18 @@ __device__ __forceinline__ void store_new_row(const DecodeArgs& a, const NewRow&
     }
 }
 
-// RMAJOR: grid (kv head, request, split) instead of (split, kv head, request).
+constexpr int kOrderSplit = 0;
+constexpr int kOrderRequest = 1;
+constexpr int kOrderCompact = 2;
+constexpr int kCompactMaxBatch = 64;  // one lane per request
+constexpr int64_t kDecodeCUs = 256;   // MI355X
+
+// ORDER: how workgroup ids map to (split, kv head, request): kOrderSplit, grid (split,
+// kv head, request); kOrderRequest, grid (kv head, request, split); kOrderCompact, a 1-D
+// grid over the units that have work, found from the lengths (batch <= 64).
 // ROPE (with QF32 and APPEND): rotate q and the appended K row at the append position.
 // CW: splits merged per round trip by the combining workgroup (combine_partials).
-template <int PAGES, int WAVES, bool QF32, bool APPEND, bool PAGED, bool RMAJOR, bool ROPE,
+template <int PAGES, int WAVES, bool QF32, bool APPEND, bool PAGED, int ORDER, bool ROPE,
           int CW = 8>
 __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     static_assert(!ROPE || (QF32 && APPEND), "RoPE is fused for f32 rows with the append");
@@ -295,17 +304,77 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     const int col = lane & 15;
     const int grp = lane >> 4;
 
-    // Grid (kv head, request, split), request-major (the default): every request's first
-    // splits are dispatched before any later split, and the later ones (often past the
-    // request's end) queue last; or (split, kv head, request). Either way, no integer
-    // division on the way to the loads.
-    const int s = RMAJOR ? blockIdx.z : blockIdx.x;
-    const int g = RMAJOR ? blockIdx.x : blockIdx.y;
-    const int b = RMAJOR ? blockIdx.y : blockIdx.z;
+    // Which (split s, kv head g, request b) this workgroup serves, its page ids, the
+    // request's length and its append position.
+    int s, g, b, len, pos = -1;
+    int gathered = 0;  // lanes < PAGES: this wave's page ids
+    if constexpr (ORDER == kOrderCompact) {
+        // Units: split k < n_active of every (request, kv head) that attends, plus one
+        // append-only unit where the appended row lies in a split past the attended ones.
+        // Workgroup i serves the i-th unit in (k, request, kv head) order, so the units
+        // take the lowest workgroup ids and a launch whose units fit the CUs gets one CU
+        // per unit; the ids past the last unit return at once. The lengths and positions
+        // of all requests (lane = request, batch <= 64) come in one vector load; the page
+        // ids follow in a second round trip.
+        int lv = 0, pv = -1;
+        if (lane < a.batch) {
+            lv = a.lens[lane * a.lens_stride + a.lens_off];
+            if constexpr (APPEND) pv = a.positions[lane];
+        }
+        const int lc = lv < a.max_seq ? lv : a.max_seq;  // never index past the table
+        const int np = lc > 0 ? (lc + kPageMask) >> kPageShift : 0;
+        const int na = (np + (1 << a.split_shift) - 1) >> a.split_shift;
+        const int sap = (APPEND && pv >= 0 && pv < (a.max_pages << kPageShift))
+                            ? pv >> (kPageShift + a.split_shift) : -1;
+        const int units = na + (sap >= na ? 1 : 0);
+        int k = 0, base = 0;
+        uint64_t mask;
+        for (;;) {  // at most n_splits + 1 rounds: a request has at most n_splits units
+            mask = __ballot(units > k);
+            const int cnt = __popcll(mask) * a.n_kv_head;
+            if (cnt == 0 || k > a.n_splits) return;  // uniform: no unit for this workgroup
+            if ((int)blockIdx.x < base + cnt) break;
+            base += cnt;
+            ++k;
+        }
+        const int j = (int)blockIdx.x - base;
+        const int r = j / a.n_kv_head;  // rank of the request among those with a unit k
+        g = j - r * a.n_kv_head;
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
+            (uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+        b = __builtin_ctzll(__ballot(((mask >> lane) & 1) && (int)rank == r));
+        len = __builtin_amdgcn_readlane(lc, b);
+        if constexpr (APPEND) pos = __builtin_amdgcn_readlane(pv, b);
+        s = k < __builtin_amdgcn_readlane(na, b) ? k : __builtin_amdgcn_readlane(sap, b);
+        if (PAGED && lane < PAGES)
+            gathered = a.tables[(int64_t)b * a.table_stride +
+                                min((s << a.split_shift) + wave * PAGES + lane, a.max_pages - 1)];
+    } else {
+        // Grid (kv head, request, split), request-major: every request's first splits are
+        // dispatched before any later split, and the later ones (often past the request's
+        // end) queue last; or (split, kv head, request). No integer division on the way to
+        // the loads. The page ids, the length and the append position come from ONE vector
+        // load (lane i < PAGES: page id i; lane PAGES: length; lane PAGES + 1: append
+        // position) and are broadcast with readlane, so no compiler scheduling can split
+        // them into dependent scalar loads. Table indices are clamped into the table, so
+        // every lane's address is in bounds (ids of pages past the request's end are never
+        // used).
+        s = ORDER == kOrderRequest ? blockIdx.z : blockIdx.x;
+        g = ORDER == kOrderRequest ? blockIdx.x : blockIdx.y;
+        b = ORDER == kOrderRequest ? blockIdx.y : blockIdx.z;
+        const int32_t* src = a.lens + b * a.lens_stride + a.lens_off;
+        if (PAGED && lane < PAGES)
+            src = a.tables + (int64_t)b * a.table_stride +
+                  min((s << a.split_shift) + wave * PAGES + lane, a.max_pages - 1);
+        if (APPEND && lane == PAGES + 1) src = a.positions + b;
+        gathered = *src;
+        const int len_raw = __builtin_amdgcn_readlane(gathered, PAGES);
+        len = len_raw < a.max_seq ? len_raw : a.max_seq;  // never index past the table
+        if constexpr (APPEND) pos = __builtin_amdgcn_readlane(gathered, PAGES + 1);
+    }
     const int bg = b * a.n_kv_head + g;
 
-    // Query operand: B[k = channel][col = head], 8 channels per lane per MFMA. Issued
-    // first: its address does not depend on anything loaded.
+    // Query operand: B[k = channel][col = head], 8 channels per lane per MFMA.
     const int h = g * a.n_rep + col;
     half8_t qh0 = {}, qh1 = {}, ql0 = {}, ql1 = {};
     float qx0[8] = {}, qx1[8] = {};  // ROPE: f32 query channels d and d + 32, rotated later
@@ -335,29 +404,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
         }
     }
 
-    // First round trip: the page ids, the length and the append position come from ONE
-    // vector load (lane i < PAGES: page id i; lane PAGES: length; lane PAGES + 1: append
-    // position) and are broadcast with readlane, so no compiler scheduling can split them
-    // into dependent scalar loads. Table indices are clamped into the table, so every
-    // lane's address is in bounds (ids of pages past the request's end are never used).
     const int wp0 = (s << a.split_shift) + wave * PAGES;
-    const int32_t* src = a.lens + b * a.lens_stride + a.lens_off;
-    if (PAGED && lane < PAGES)
-        src = a.tables + (int64_t)b * a.table_stride + min(wp0 + lane, a.max_pages - 1);
-    if (APPEND && lane == PAGES + 1) src = a.positions + b;
-    const int gathered = *src;
     int64_t page[PAGES];
 #pragma unroll
     for (int i = 0; i < PAGES; ++i)
         page[i] = PAGED ? (int64_t)__builtin_amdgcn_readlane(gathered, i) : (int64_t)(wp0 + i);
-    const int len_raw = __builtin_amdgcn_readlane(gathered, PAGES);
-    const int len = len_raw < a.max_seq ? len_raw : a.max_seq;  // never index past the table
-    const int pos = APPEND ? __builtin_amdgcn_readlane(gathered, PAGES + 1) : -1;
     int apos = -1;  // position of the row this workgroup appends, or -1
     if (APPEND && pos >= 0 && pos < (a.max_pages << kPageShift) &&
         (pos >> (kPageShift + a.split_shift)) == s)
         apos = pos;
-
     const int n_pages = len > 0 ? (len + kPageMask) >> kPageShift : 0;
     const int p_begin = s << a.split_shift;
     const bool attend = p_begin < n_pages;
@@ -590,19 +645,26 @@ DecodeShape decode_shape(int64_t batch, int64_t n_kv_head, int64_t max_pages) {
 }
 
 template <bool QF32, bool APPEND, bool PAGED, bool ROPE = false>
-bool launch_shape(const DecodeArgs& a, DecodeShape sh, bool rmajor, dim3 grid,
+bool launch_shape(const DecodeArgs& a, DecodeShape sh, int order, dim3 grid,
                   hipStream_t stream) {
+    // The 16-wide combine only where a launch can have more than 8 splits.
+#define CRUCIBLE_DECODE_ORDER(P, W, O)                                                         \
+    if (a.n_splits > 8)                                                                         \
+        hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, O, ROPE, 16>), grid,       \
+                           dim3(W * 64), 0, stream, a);                                         \
+    else                                                                                        \
+        hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, O, ROPE>), grid,           \
+                           dim3(W * 64), 0, stream, a);
 #define CRUCIBLE_DECODE_CASE(P, W)                                                             \
     if (sh.pages == P && sh.waves == W) {                                                       \
-        if (rmajor && a.n_splits > 8)                                                           \
-            hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, true, ROPE, 16>), grid,\
-                               dim3(W * 64), 0, stream, a);                                     \
-        else if (rmajor)                                                                        \
-            hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, true, ROPE>), grid,    \
-                               dim3(W * 64), 0, stream, a);                                     \
-        else                                                                                    \
-            hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, false, ROPE>), grid,   \
-                               dim3(W * 64), 0, stream, a);                                     \
+        if (order == kOrderCompact) {                                                           \
+            CRUCIBLE_DECODE_ORDER(P, W, kOrderCompact)                                          \
+        } else if (order == kOrderRequest) {                                                    \
+            CRUCIBLE_DECODE_ORDER(P, W, kOrderRequest)                                          \
+        } else {                                                                                \
+            hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, kOrderSplit, ROPE>),   \
+                               grid, dim3(W * 64), 0, stream, a);                               \
+        }                                                                                       \
         return true;                                                                            \
     }
     CRUCIBLE_DECODE_CASE(1, 4)
@@ -612,6 +674,7 @@ bool launch_shape(const DecodeArgs& a, DecodeShape sh, bool rmajor, dim3 grid,
     CRUCIBLE_DECODE_CASE(2, 8)
     CRUCIBLE_DECODE_CASE(4, 8)
 #undef CRUCIBLE_DECODE_CASE
+#undef CRUCIBLE_DECODE_ORDER
     return false;
 }
 
@@ -620,24 +683,39 @@ int launch_decode(DecodeArgs a, DecodeShape sh, bool q_f32, hipStream_t stream,
     CRUCIBLE_CHECK(a.n_splits > 0 && a.n_kv_head <= 65535 && a.batch <= 65535,
                    CRUCIBLE_ERR_INVALID, "%s: grid (%d, %d, %d) too large", what, a.n_splits,
                    a.n_kv_head, a.batch);
-    // Request-major order: every request's first splits are dispatched first (measured
-    // faster with the default shapes, most of all when the grid exceeds the resident set).
-    bool rmajor = true;
-    if (const char* env = std::getenv("CRUCIBLE_DECODE_REQUEST_MAJOR")) rmajor = std::atoi(env) != 0;
-    const dim3 grid = rmajor ? dim3((unsigned)a.n_kv_head, (unsigned)a.batch, (unsigned)a.n_splits)
-                             : dim3((unsigned)a.n_splits, (unsigned)a.n_kv_head, (unsigned)a.batch);
+    // When the grid is larger than the chip (more workgroups than CUs), the compact order:
+    // the units with work take the lowest workgroup ids, so while they fit each gets a CU
+    // of its own instead of sharing one with an early split of another request. It costs
+    // a second round trip before the pages (lengths first, then the page ids), so a grid
+    // that fits the CUs keeps the request-major order: every request's first splits are
+    // dispatched first (measured faster than split-major with the default shapes).
+    // CRUCIBLE_DECODE_ORDER = split | request | compact overrides the choice; compact needs
+    // batch <= 64 (one lane per request) and falls back to request-major past it.
+    const int64_t units = (int64_t)a.n_splits * a.n_kv_head * a.batch;
+    int order = (units > kDecodeCUs && a.batch <= kCompactMaxBatch) ? kOrderCompact : kOrderRequest;
+    if (const char* env = std::getenv("CRUCIBLE_DECODE_ORDER")) {
+        if (!std::strcmp(env, "split")) order = kOrderSplit;
+        if (!std::strcmp(env, "request")) order = kOrderRequest;
+        if (!std::strcmp(env, "compact") && a.batch <= kCompactMaxBatch) order = kOrderCompact;
+    }
+    CRUCIBLE_CHECK(units <= 0x7fffffff, CRUCIBLE_ERR_INVALID, "%s: grid of %lld too large", what,
+                   (long long)units);
+    const dim3 grid = order == kOrderCompact ? dim3((unsigned)units)
+                      : order == kOrderRequest
+                          ? dim3((unsigned)a.n_kv_head, (unsigned)a.batch, (unsigned)a.n_splits)
+                          : dim3((unsigned)a.n_splits, (unsigned)a.n_kv_head, (unsigned)a.batch);
     bool launched;
     if (a.rope_cos)  // fused RoPE: f32 qkv rows with the append
-        launched = launch_shape<true, true, true, true>(a, sh, rmajor, grid, stream);
+        launched = launch_shape<true, true, true, true>(a, sh, order, grid, stream);
     else if (a.positions)  // the fused append exists for paged pools only
-        launched = q_f32 ? launch_shape<true, true, true>(a, sh, rmajor, grid, stream)
-                         : launch_shape<false, true, true>(a, sh, rmajor, grid, stream);
+        launched = q_f32 ? launch_shape<true, true, true>(a, sh, order, grid, stream)
+                         : launch_shape<false, true, true>(a, sh, order, grid, stream);
     else if (a.tables)
-        launched = q_f32 ? launch_shape<true, false, true>(a, sh, rmajor, grid, stream)
-                         : launch_shape<false, false, true>(a, sh, rmajor, grid, stream);
+        launched = q_f32 ? launch_shape<true, false, true>(a, sh, order, grid, stream)
+                         : launch_shape<false, false, true>(a, sh, order, grid, stream);
     else
-        launched = q_f32 ? launch_shape<true, false, false>(a, sh, rmajor, grid, stream)
-                         : launch_shape<false, false, false>(a, sh, rmajor, grid, stream);
+        launched = q_f32 ? launch_shape<true, false, false>(a, sh, order, grid, stream)
+                         : launch_shape<false, false, false>(a, sh, order, grid, stream);
     CRUCIBLE_CHECK(launched, CRUCIBLE_ERR_INVALID, "%s: bad decode shape %d x %d", what,
                    sh.pages, sh.waves);
     if (int rc = fail_launch(what)) return rc;

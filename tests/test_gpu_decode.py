@@ -12,6 +12,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = 2e-3  # max-abs 2e-3 against the fp32 reference
 SENTINEL = -12345.25
+ORDERS = ["split", "request", "compact"]  # CRUCIBLE_DECODE_ORDER values
 
 
 def _dev(a, dev):
@@ -287,11 +288,14 @@ def test_fused_append_decode_equals_separate_calls(gpu, dev, n_head, n_kv, kv_dt
     assert np.abs(o2 - want).max() <= TOL
 
 
-def test_fused_append_off_the_last_slot_and_inactive_rows(gpu, dev):
-    """Rows appended inside the attended range, past it (a later page), and for inactive
-    requests (len 0) give the same pools and outputs as the separate calls."""
-    lens = [40, 40, 0, 300, 17, 129]
-    positions = [20, 100, 5, 299, 16, 128]
+@pytest.mark.parametrize("order", ORDERS)
+def test_fused_append_off_the_last_slot_and_inactive_rows(gpu, dev, monkeypatch, order):
+    """Rows appended inside the attended range, past it (a later page, and a later split:
+    a unit of its own in the compact order), and for inactive requests (len 0) give the
+    same pools and outputs as the separate calls."""
+    monkeypatch.setenv("CRUCIBLE_DECODE_ORDER", order)
+    lens = [40, 40, 0, 300, 17, 129, 0]
+    positions = [20, 100, 5, 299, 16, 128, 700]
     for rep in range(3):  # repeated launches reuse the workspace counters
         k2, v2, k1, v1, o2, o1, _, _ = _fused_vs_separate(gpu, dev, lens, positions, 12, 3,
                                                           seed=70 + rep)
@@ -301,14 +305,14 @@ def test_fused_append_off_the_last_slot_and_inactive_rows(gpu, dev):
         assert np.all(o2[2] == SENTINEL)
 
 
-@pytest.mark.parametrize("order", ["0", "1"])
+@pytest.mark.parametrize("order", ORDERS)
 def test_decode_shapes_agree(gpu, dev, monkeypatch, order):
     """Every split shape (pages per wave x waves per workgroup) gives the oracle's answer,
-    with the fused and plain entries, on lengths that exercise 1..many splits, in both
-    grid orders (split-major and request-major)."""
+    with the fused and plain entries, on lengths that exercise 1..many splits, in every
+    grid order (split-major, request-major, and the compact list of units with work)."""
     lens = [3, 64, 65, 500, 1023, 2048, 1500, 16]
     positions = [n - 1 for n in lens]
-    monkeypatch.setenv("CRUCIBLE_DECODE_REQUEST_MAJOR", order)
+    monkeypatch.setenv("CRUCIBLE_DECODE_ORDER", order)
     for pages in ("1", "2", "4"):
         for waves in ("4", "8"):
             monkeypatch.setenv("CRUCIBLE_DECODE_PAGES", pages)
@@ -323,16 +327,29 @@ def test_decode_shapes_agree(gpu, dev, monkeypatch, order):
 
 def test_grid_orders_are_bit_identical(gpu, dev, monkeypatch):
     """The grid order only places the workgroups: splits merge in split order whatever
-    order they finish in, so both orders give the same bits."""
+    order they finish in, so every order gives the same bits."""
     lens = [1, 17, 256, 257, 700, 2048, 1999, 64, 0, 1024]
     positions = [max(n - 1, 0) for n in lens]
     outs = []
-    for order in ("0", "1"):
-        monkeypatch.setenv("CRUCIBLE_DECODE_REQUEST_MAJOR", order)
+    for order in ORDERS:
+        monkeypatch.setenv("CRUCIBLE_DECODE_ORDER", order)
         _, _, _, _, o2, o1, _, _ = _fused_vs_separate(gpu, dev, lens, positions, 12, 3, seed=5)
         assert np.array_equal(o2.view(np.uint32), o1.view(np.uint32))
         outs.append(o2.view(np.uint32))
-    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+def test_batch_past_the_compact_limit(gpu, dev):
+    """Batches above 64 requests (one lane per request in the compact order's search) use
+    the request-major grid; the answer is the oracle's either way."""
+    lens = [int(x) for x in np.random.default_rng(44).integers(0, 300, 70)]
+    lens[3] = 0
+    q, k_pool, v_pool, tables, stride = _case(45, lens, 12, 3)
+    got = _run_decode(gpu, dev, q, k_pool, v_pool, tables, lens, 12, 3, 3, 1, stride * 16)
+    want = _oracle(q, k_pool, v_pool, tables, lens, 12, 3, 3, 1)
+    active = np.asarray(lens) > 0
+    assert np.abs(got[active] - want[active]).max() <= TOL
+    assert np.all(got[~active] == SENTINEL)
 
 
 def test_workspace_shared_across_batch_sizes(gpu, dev):

@@ -113,6 +113,47 @@ __device__ __forceinline__ float load_coherent(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Max and sum of a value over a lane's 4 lane groups (lanes L, L ^ 16, L ^ 32, L ^ 48):
+// v_permlane16_swap / v_permlane32_swap of the value with a copy of itself (one operand
+// ends with v[L], the other with v[L ^ 16], resp. v[L ^ 32]), then a max or an add. The
+// shuffles they replace go through LDS (ds_bpermute). The swap needs 2 wait states around
+// its VALU neighbours; the block opens with 1 for a v_exp_f32 result it may read. The sum
+// adds the same pairs in the same grouping as two xor shuffles, (x + x^16) + (x^32 + x^48),
+// so its bits do not change.
+__device__ __forceinline__ float group_max4(float x) {
+    float t;
+    asm("s_nop 0\n\t"
+        "v_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\t"
+        "v_permlane16_swap_b32 %0, %1\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32 %0, %0, %1\n\t"
+        "v_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\t"
+        "v_permlane32_swap_b32 %0, %1\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32 %0, %0, %1"
+        : "+v"(x), "=&v"(t));
+    return x;
+}
+
+__device__ __forceinline__ float group_sum4(float x) {
+    float t;
+    asm("s_nop 0\n\t"
+        "v_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\t"
+        "v_permlane16_swap_b32 %0, %1\n\t"
+        "s_nop 1\n\t"
+        "v_add_f32 %0, %0, %1\n\t"
+        "v_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\t"
+        "v_permlane32_swap_b32 %0, %1\n\t"
+        "s_nop 1\n\t"
+        "v_add_f32 %0, %0, %1"
+        : "+v"(x), "=&v"(t));
+    return x;
+}
+
 // Merge the partials of splits [0, n_active) for query head hh, dims 4*d4 .. 4*d4+3.
 // Loads are issued CW splits at a time so the merge costs n_active / CW round trips. CW is
 // 16 for launches with more than 8 splits (batch 1 at ctx 1024: 16 splits, one round trip
@@ -508,8 +549,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) sv[r] = (tok0 + r < len) ? st[r] * a.scale_log2 : -INFINITY;
             float tm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-            tm = fmaxf(tm, __shfl_xor(tm, 16));
-            tm = fmaxf(tm, __shfl_xor(tm, 32));
+            tm = group_max4(tm);
             const float mn = fmaxf(m, tm);
             const float alpha = fast_exp2(m - mn);
             float pv[4];
@@ -542,8 +582,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
             }
         }
     }
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    l = group_sum4(l);
 
     // Merge the waves' states: acc[db][r] = O^T[16*db + 4*grp + r][col].
     if (grp == 0) {
@@ -565,13 +604,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
         for (int w = 0; w < WAVES; ++w) M = fmaxf(M, s_m[w][ccol]);
         float L = 0.0f;
         float4_t o = {};
+        // Branch-free, so all the LDS reads issue together: a wave without pages has
+        // m = -inf, l = 0 and acc = 0, so its weight is 0 and it adds exact zeros (wave 0
+        // holds the split's first page, so M is finite).
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) {
-            if (s_l[w][ccol] > 0.0f) {
-                const float wgt = fast_exp2(s_m[w][ccol] - M);
-                L += s_l[w][ccol] * wgt;
-                o += s_acc[w][ccol][d4] * wgt;
-            }
+            const float wgt = fast_exp2(s_m[w][ccol] - M);
+            L += s_l[w][ccol] * wgt;
+            o += s_acc[w][ccol][d4] * wgt;
         }
         if (n_active == 1) {
             store_out4(a, (int64_t)b * a.out_row_stride + (int64_t)hh * kHeadDim + 4 * d4, o * (1.0f / L));

@@ -113,47 +113,6 @@ __device__ __forceinline__ float load_coherent(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Max and sum of a value over a lane's 4 lane groups (lanes L, L ^ 16, L ^ 32, L ^ 48):
-// v_permlane16_swap / v_permlane32_swap of the value with a copy of itself (one operand
-// ends with v[L], the other with v[L ^ 16], resp. v[L ^ 32]), then a max or an add. The
-// shuffles they replace go through LDS (ds_bpermute). The swap needs 2 wait states around
-// its VALU neighbours; the block opens with 1 for a v_exp_f32 result it may read. The sum
-// adds the same pairs in the same grouping as two xor shuffles, (x + x^16) + (x^32 + x^48),
-// so its bits do not change.
-__device__ __forceinline__ float group_max4(float x) {
-    float t;
-    asm("s_nop 0\n\t"
-        "v_mov_b32 %1, %0\n\t"
-        "s_nop 1\n\t"
-        "v_permlane16_swap_b32 %0, %1\n\t"
-        "s_nop 1\n\t"
-        "v_max_f32 %0, %0, %1\n\t"
-        "v_mov_b32 %1, %0\n\t"
-        "s_nop 1\n\t"
-        "v_permlane32_swap_b32 %0, %1\n\t"
-        "s_nop 1\n\t"
-        "v_max_f32 %0, %0, %1"
-        : "+v"(x), "=&v"(t));
-    return x;
-}
-
-__device__ __forceinline__ float group_sum4(float x) {
-    float t;
-    asm("s_nop 0\n\t"
-        "v_mov_b32 %1, %0\n\t"
-        "s_nop 1\n\t"
-        "v_permlane16_swap_b32 %0, %1\n\t"
-        "s_nop 1\n\t"
-        "v_add_f32 %0, %0, %1\n\t"
-        "v_mov_b32 %1, %0\n\t"
-        "s_nop 1\n\t"
-        "v_permlane32_swap_b32 %0, %1\n\t"
-        "s_nop 1\n\t"
-        "v_add_f32 %0, %0, %1"
-        : "+v"(x), "=&v"(t));
-    return x;
-}
-
 // Merge the partials of splits [0, n_active) for query head hh, dims 4*d4 .. 4*d4+3.
 // Loads are issued CW splits at a time so the merge costs n_active / CW round trips. CW is
 // 16 for launches with more than 8 splits (batch 1 at ctx 1024: 16 splits, one round trip

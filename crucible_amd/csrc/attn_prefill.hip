@@ -578,9 +578,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
     // ---- normalise and write: lane (q = col, grp) holds dims 16*db + 4*grp .. +3
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-        float lt = l[qb];
-        lt += __shfl_xor(lt, 16);
-        lt += __shfl_xor(lt, 32);
+        const float lt = group_sum4(l[qb]);
         if (my_row[qb] < 0) continue;
         const float inv = 1.0f / lt;
         const int64_t off = (int64_t)my_row[qb] * ld_q + (int64_t)h * kHeadDim + 4 * grp;
@@ -785,8 +783,7 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
     }
 
     // ---- merge the 8 waves' states (per column: m, l summed over the lane groups)
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    l = group_sum4(l);
     if (grp == 0) {
         s_m[wave][col] = m;
         s_l[wave][col] = l;
@@ -801,14 +798,14 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
     for (int w = 0; w < kDirectWaves; ++w) M = fmaxf(M, s_m[w][col]);
     float L = 0.0f;
     float4_t o = {0.f, 0.f, 0.f, 0.f};
+    // Branch-free, so all the LDS reads issue together. A wave whose keys this row cannot
+    // see has m = -inf, l = 0 and acc = 0: its weight is 0 and it adds exact zeros (wave
+    // 0 holds the row's first key, so M is finite).
 #pragma unroll
     for (int w = 0; w < kDirectWaves; ++w) {
-        const float lw = s_l[w][col];
-        if (lw > 0.0f) {
-            const float wt = fast_exp2(s_m[w][col] - M);
-            L += lw * wt;
-            o += s_acc[w][db][lane] * wt;
-        }
+        const float wt = fast_exp2(s_m[w][col] - M);
+        L += s_l[w][col] * wt;
+        o += s_acc[w][db][lane] * wt;
     }
     o = o * (1.0f / L);
     const int64_t off = (int64_t)my_row * ld_q + (int64_t)h * kHeadDim + 16 * db + 4 * grp;

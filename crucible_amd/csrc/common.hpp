@@ -53,6 +53,47 @@ __device__ __forceinline__ int64_t block_base(const PoolAddr& a, int64_t page) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Max and sum of a value over a lane's 4 lane groups (lanes L, L ^ 16, L ^ 32, L ^ 48):
+// v_permlane16_swap / v_permlane32_swap of the value with a copy of itself (one operand
+// ends with v[L], the other with v[L ^ 16], resp. v[L ^ 32]), then a max or an add. The
+// shuffles they replace go through LDS (ds_bpermute). The swap needs 2 wait states around
+// its VALU neighbours; the block opens with 1 for a v_exp_f32 result it may read. The sum
+// adds the same pairs in the same grouping as two xor shuffles, (x + x^16) + (x^32 + x^48),
+// so its bits do not change.
+__device__ __forceinline__ float group_max4(float x) {
+    float t;
+    asm("s_nop 0\n\t"
+        "v_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\t"
+        "v_permlane16_swap_b32 %0, %1\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32 %0, %0, %1\n\t"
+        "v_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\t"
+        "v_permlane32_swap_b32 %0, %1\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32 %0, %0, %1"
+        : "+v"(x), "=&v"(t));
+    return x;
+}
+
+__device__ __forceinline__ float group_sum4(float x) {
+    float t;
+    asm("s_nop 0\n\t"
+        "v_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\t"
+        "v_permlane16_swap_b32 %0, %1\n\t"
+        "s_nop 1\n\t"
+        "v_add_f32 %0, %0, %1\n\t"
+        "v_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\t"
+        "v_permlane32_swap_b32 %0, %1\n\t"
+        "s_nop 1\n\t"
+        "v_add_f32 %0, %0, %1"
+        : "+v"(x), "=&v"(t));
+    return x;
+}
+
 __device__ __forceinline__ float4_t mfma_16x16x32(half8_t a, half8_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

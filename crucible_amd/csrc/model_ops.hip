@@ -123,6 +123,25 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
         __syncthreads();
     }
 
+    // The residual each output thread adds is requested now, so its round trip overlaps
+    // the product instead of following it (out may alias resid: only this thread touches
+    // the element).
+    constexpr int kOut = 256 * NB;
+    constexpr int kOutPer = (kOut + kLinThreads - 1) / kLinThreads;
+    float rv[kOutPer];
+    if constexpr (MODE == kResidual) {
+#pragma unroll
+        for (int i = 0; i < kOutPer; ++i) {
+            const int o = tid + i * kLinThreads;
+            const int blk = o >> 8, rem = o & 255;
+            const int l = rem & 63, r = rem >> 6;
+            const int orow = m0 + (l >> 4) + 4 * r;
+            const int on = n0 + 16 * blk + (l & 15);
+            rv[i] = (o < kOut && orow < a.rows && on < a.n_out)
+                        ? a.resid[(int64_t)orow * a.ldo + on] : 0.0f;
+        }
+    }
+
     // wave w takes chunks [w * nc / 8, (w + 1) * nc / 8) of the nc chunks
     const int c0 = wave * nc / kLinWaves, c1 = (wave + 1) * nc / kLinWaves;
     const int kw = (c1 - c0) * kLinK;
@@ -252,8 +271,10 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
         }
         return;
     }
-    constexpr int kOut = 256 * NB;
-    for (int o = tid; o < kOut; o += kLinThreads) {
+#pragma unroll
+    for (int i = 0; i < kOutPer; ++i) {
+        const int o = tid + i * kLinThreads;
+        if (o >= kOut) break;
         const int blk = o >> 8, rem = o & 255;
         const int l = rem & 63, r = rem >> 6;
         const int orow = m0 + (l >> 4) + 4 * r;
@@ -264,7 +285,7 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
         for (int w = 0; w < kLinWaves; ++w) y += s_red[w][blk][r][l];
         float* dst = a.out + (int64_t)orow * a.ldo + on;
         if constexpr (MODE == kResidual) {
-            *dst = a.resid[(int64_t)orow * a.ldo + on] + (float)y;
+            *dst = rv[i] + (float)y;
         } else {
             *dst = (float)y;
         }

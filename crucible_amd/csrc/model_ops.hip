@@ -20,6 +20,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cmath>
 #include <type_traits>
 
@@ -292,6 +293,193 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- 4-column tiles
+
+// f64 MFMA 4x4x4 (four 4x4 blocks) operand layout, measured on gfx950: lane l supplies
+// A[l & 15][kslot] (the 16 rows are the four blocks of 4 rows) and B[kslot][l & 3] with
+// kslot = l >> 4 (the blocks share B: lanes that differ only in bits 2-3 hold the same
+// weight), and holds D[4 ((l >> 2) & 3) + (l >> 4)][l & 3]. It issues every 16 cycles,
+// the MAC rate of the 16x16x4 form, for a quarter of the columns: a 16-row product
+// spreads over four times the workgroups.
+__device__ __forceinline__ double mfma4_f64(double a, double b, double c) {
+    return __builtin_amdgcn_mfma_f64_4x4x4f64(a, b, c, 0, 0, 0);
+}
+
+// out tile = 16 rows x 4 columns; in kSwiGLU mode the gate rows and the up rows of those 4
+// columns are two weight groups. Same K split over the waves, chunk loads, fused norm and
+// f64 contract as linear_kernel; two accumulators per group (even and odd MFMA steps)
+// keep two independent chains in flight, summed in a fixed order at the end.
+// At most 128 VGPRs (4 waves per SIMD): two workgroups per CU, so grids of up to 512
+// workgroups (the decode step's 288 for qkv, 512 for gate/up) run in one round.
+template <bool NORM, int MODE>
+__global__ __launch_bounds__(kLinThreads, 4) void linear4_kernel(LinArgs a) {
+    constexpr int G = MODE == kSwiGLU ? 2 : 1;  // weight groups of 4 columns
+    __shared__ double s_scale[16];
+    __shared__ double s_ss[kLinWaves][16];
+    __shared__ double s_red[kLinWaves][G][64];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int col = lane & 15;  // A row within the tile
+    const int g = lane >> 4;
+    const int m0 = blockIdx.y * 16;
+    const int n0 = blockIdx.x * 4;
+    const int nc = a.k_in / kLinK;
+    constexpr int RC = 3;  // chunks held for the register-sourced norm (k_in <= 768)
+    const bool reg_norm = NORM && nc <= kLinWaves * RC;
+
+    // Output element of threads 0..63 (the D layout); the residual is requested now.
+    const int orow = m0 + 4 * ((lane >> 2) & 3) + (lane >> 4);
+    const int ocol = n0 + (lane & 3);
+    const bool out_ok = tid < 64 && orow < a.rows && ocol < a.n_out;
+    float rv = 0.0f;
+    if constexpr (MODE == kResidual)
+        if (out_ok) rv = a.resid[(int64_t)orow * a.ldo + ocol];
+
+    if (NORM && !reg_norm) {
+        const int r = tid >> 5, t = tid & 31;
+        double ss = 0.0;
+        if (m0 + r < a.rows) {
+            const float4_t* xr = reinterpret_cast<const float4_t*>(a.x + (int64_t)(m0 + r) * a.ldx);
+            const int n4 = a.k_in / 4;
+            for (int i0 = t; i0 < n4; i0 += 32 * 8) {
+                float4_t v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    v[i] = (i0 + 32 * i < n4) ? xr[i0 + 32 * i] : float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const double d = (double)v[i][e];
+                        ss += d * d;
+                    }
+            }
+        }
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 32);
+        if (t == 0) s_scale[r] = 1.0 / sqrt(ss / (double)a.k_in + a.eps);
+        __syncthreads();
+    }
+
+    const int c0 = wave * nc / kLinWaves, c1 = (wave + 1) * nc / kLinWaves;
+    const int kw = (c1 - c0) * kLinK;
+    const int kbeg = c0 * kLinK + 8 * g;
+    const int row = m0 + col;
+    const bool row_ok = row < a.rows;
+    const float* xp = a.x + (int64_t)(row_ok ? row : 0) * a.ldx + kbeg;
+    const float* nwp = NORM ? a.norm_w + kbeg : nullptr;
+    const int wn = n0 + (lane & 3);
+    const bool wn_ok = wn < a.n_out;
+    const half_t* wp[G];
+    wp[0] = a.w + (int64_t)(wn_ok ? wn : 0) * a.k_in + kbeg;
+    if constexpr (G == 2) wp[1] = a.w2 + (int64_t)(wn_ok ? wn : 0) * a.k_in + kbeg;
+
+    auto load = [&](int k0) {
+        Chunk<G> c;
+        c.x0 = *reinterpret_cast<const float4_t*>(xp + k0);
+        c.x1 = *reinterpret_cast<const float4_t*>(xp + k0 + 4);
+#pragma unroll
+        for (int j = 0; j < G; ++j) c.w[j] = *reinterpret_cast<const half8_t*>(wp[j] + k0);
+        return c;
+    };
+
+    double acc[G][2];
+#pragma unroll
+    for (int j = 0; j < G; ++j) acc[j][0] = acc[j][1] = 0.0;
+
+    auto feed = [&](const Chunk<G>& ch, int k0, double scale) {
+        float xs[8] = {ch.x0[0], ch.x0[1], ch.x0[2], ch.x0[3], ch.x1[0], ch.x1[1], ch.x1[2], ch.x1[3]};
+        if constexpr (NORM) {
+            const float4_t w0 = *reinterpret_cast<const float4_t*>(nwp + k0);
+            const float4_t w1 = *reinterpret_cast<const float4_t*>(nwp + k0 + 4);
+            const float nw[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xs[i] = (float)((double)xs[i] * scale) * nw[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const double av = row_ok ? (double)xs[i] : 0.0;
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+                const double bv = wn_ok ? (double)(float)ch.w[j][i] : 0.0;
+                acc[j][i & 1] = mfma4_f64(av, bv, acc[j][i & 1]);
+            }
+        }
+    };
+
+    if (reg_norm) {
+        Chunk<G> ch[RC];
+        const int nch = c1 - c0;
+#pragma unroll
+        for (int c = 0; c < RC; ++c)
+            if (c < nch) ch[c] = load(c * kLinK);
+        double ss = 0.0;
+#pragma unroll
+        for (int c = 0; c < RC; ++c) {
+            if (c >= nch) break;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const double d0 = (double)ch[c].x0[i], d1 = (double)ch[c].x1[i];
+                ss += d0 * d0;
+                ss += d1 * d1;
+            }
+        }
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        if (g == 0) s_ss[wave][col] = ss;
+        __syncthreads();
+        double tot = 0.0;
+#pragma unroll
+        for (int w = 0; w < kLinWaves; ++w) tot += s_ss[w][col];
+        const double scale = 1.0 / sqrt(tot / (double)a.k_in + a.eps);
+#pragma unroll
+        for (int c = 0; c < RC; ++c) {
+            if (c >= nch) break;
+            feed(ch[c], c * kLinK, scale);
+        }
+    } else {
+        const double scale = NORM ? s_scale[col] : 1.0;
+        // 8 chunks in flight for the plain products (down: all of a wave's K at once);
+        // the norm and SwiGLU forms keep 3 to stay within 128 registers
+        constexpr int BATCH = (NORM || G == 2) ? 3 : kLinBatch;
+        for (int b0 = 0; b0 < kw; b0 += BATCH * kLinK) {
+            Chunk<G> ch[BATCH];
+#pragma unroll
+            for (int c = 0; c < BATCH; ++c)
+                if (b0 + c * kLinK < kw) ch[c] = load(b0 + c * kLinK);
+#pragma unroll
+            for (int c = 0; c < BATCH; ++c) {
+                if (b0 + c * kLinK >= kw) break;
+                feed(ch[c], b0 + c * kLinK, scale);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int j = 0; j < G; ++j) s_red[wave][j][lane] = acc[j][0] + acc[j][1];
+    __syncthreads();
+    if (!out_ok) return;
+    // fixed summation order over the waves
+    double y[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        y[j] = 0.0;
+#pragma unroll
+        for (int w = 0; w < kLinWaves; ++w) y[j] += s_red[w][j][lane];
+    }
+    float* dst = a.out + (int64_t)orow * a.ldo + ocol;
+    if constexpr (MODE == kSwiGLU) {
+        const float gf = (float)y[0];
+        *dst = gf / (1.0f + expf(-gf)) * (float)y[G - 1];
+    } else if constexpr (MODE == kResidual) {
+        *dst = rv + (float)y[0];
+    } else {
+        *dst = (float)y[0];
+    }
+}
+
 // ---------------------------------------------------------------- wide projections
 
 constexpr int kCUs = 256;      // MI355X: one persistent workgroup per CU
@@ -513,6 +701,22 @@ void launch_linear(const LinArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((linear_kernel<NORM, MODE, NB>), grid, dim3(kLinThreads), 0, stream, a);
 }
 
+template <bool NORM, int MODE>
+void launch_linear4(const LinArgs& a, hipStream_t stream) {
+    const dim3 grid((unsigned)((a.n_out + 3) / 4), (unsigned)((a.rows + 15) / 16));
+    hipLaunchKernelGGL((linear4_kernel<NORM, MODE>), grid, dim3(kLinThreads), 0, stream, a);
+}
+
+// 4-column tiles where 16-column tiles would leave CUs without a workgroup and no norm is
+// fused (the decode step's o and down projections: 5.16 -> 4.84 and 10.2 -> 8.9 us).
+// With a fused norm every workgroup loads and normalises the whole rows, and four times
+// the workgroups made it slower (qkv 6.9 -> 8.8 us, gate/up 7.4 -> 11.6 us), so those keep
+// 16 columns. CRUCIBLE_LINEAR_TILE = 4 | 16 overrides the choice.
+bool use_tile4(int64_t n_out, int64_t rows, int cols16, bool norm) {
+    if (const char* env = std::getenv("CRUCIBLE_LINEAR_TILE")) return std::atoi(env) == 4;
+    return !norm && ((n_out + cols16 - 1) / cols16) * ((rows + 15) / 16) < kCUs;
+}
+
 int check_linear(const char* what, const float* x, int64_t ldx, const float* norm_w,
                  const void* w, int64_t n_out, int64_t k_in, const float* out, int64_t ldo,
                  int64_t rows) {
@@ -581,7 +785,15 @@ extern "C" int crucible_linear_f64acc(const float* x, int64_t ldx, const float* 
         else by_rc(std::false_type{});
         return fail_launch(what);
     }
-    if (resid) {
+    if (!wide && use_tile4(n_out, rows, 16, norm_w != nullptr)) {
+        if (resid) {
+            if (norm_w) launch_linear4<true, kResidual>(a, s);
+            else launch_linear4<false, kResidual>(a, s);
+        } else {
+            if (norm_w) launch_linear4<true, kPlain>(a, s);
+            else launch_linear4<false, kPlain>(a, s);
+        }
+    } else if (resid) {
         if (norm_w) launch_linear<true, kResidual, 1>(a, s);
         else launch_linear<false, kResidual, 1>(a, s);
     } else if (norm_w) {
@@ -609,8 +821,14 @@ extern "C" int crucible_linear_swiglu_f64acc(const float* x, int64_t ldx, const 
               static_cast<const half_t*>(w_up), nullptr, out, ldo, (int)rows, (int)hidden,
               (int)k_in};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (norm_w) launch_linear<true, kSwiGLU, 1>(a, s);
-    else launch_linear<false, kSwiGLU, 1>(a, s);
+    if (use_tile4(hidden, rows, 8, norm_w != nullptr)) {
+        if (norm_w) launch_linear4<true, kSwiGLU>(a, s);
+        else launch_linear4<false, kSwiGLU>(a, s);
+    } else if (norm_w) {
+        launch_linear<true, kSwiGLU, 1>(a, s);
+    } else {
+        launch_linear<false, kSwiGLU, 1>(a, s);
+    }
     return fail_launch(what);
 }
 

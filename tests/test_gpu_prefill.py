@@ -121,6 +121,23 @@ def test_repeated_launches_are_bit_identical(gpu, dev):
             assert np.array_equal(d.result().view(np.uint32), first.view(np.uint32)), case.name
 
 
+def test_grid_orders_are_bit_identical(gpu, dev, monkeypatch):
+    """The longest-first grid (the last row tiles of every request dispatched first, the
+    default) and the plain (x, row tile, request) grid only place the workgroups: the
+    outputs are the same bits."""
+    for case in [c for c in CASES if c.name in ("4x256", "ragged-profile-2", "offset-255")]:
+        fx = A.fixture(case)
+        outs = []
+        for order in ("1", "0"):
+            monkeypatch.setenv("CRUCIBLE_PREFILL_HEAVY_FIRST", order)
+            for runner in (run_segments, run_owners):
+                d = Device(fx, dev)
+                runner(gpu, d)
+                outs.append(d.result().copy())
+        assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32)), case.name
+        assert np.array_equal(outs[1].view(np.uint32), outs[3].view(np.uint32)), case.name
+
+
 def test_single_sequence_params_and_contiguous_forms(gpu, dev):
     """attention_prefill_paged (params[5] offset) and attention_prefill (contiguous)."""
     for case in [c for c in CASES if c.name in ("single-1024", "single-941", "offset-255")]:

@@ -51,7 +51,9 @@ def parse_args():
     p.add_argument("--no-extras", action="store_true")
     p.add_argument("--extras", default="decode,prefill,e2e",
                    help="comma list of extra groups to run: decode (the other decode "
-                        "shapes), prefill (configs 1 and 4), e2e (config 5)")
+                        "shapes), prefill (configs 1 and 4), e2e (config 5), scale (the "
+                        "fused decode at batch 32..256, config 3's length distribution; "
+                        "not in the default set)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 256 MiB device copy (PMC traffic calibration)")
     return p.parse_args()
@@ -461,6 +463,25 @@ def main():
                                          "bytes_per_launch": int(by / 12)}
             del graphs, mha
         torch.cuda.empty_cache()
+    if "scale" in groups:
+        # the same kernel and length distribution with more bytes per launch: where the
+        # bandwidth goes once a launch is no longer latency-bound
+        scale = {}
+        for kv, batches in ((3, (32, 64, 128, 256)), (12, (32, 64))):
+            for batch in batches:
+                sb = DecodeBench(gpu, dev, batch=batch, n_head=12, n_kv_head=kv, n_layer=12,
+                                 n_pages=batch * 3 * 140, max_seq=2048, rotations=3,
+                                 seed=W.BASE_SEED + 2)
+                graphs = sb.capture("fused")
+                ms, ev, by = sb.time_steps(graphs, 60, 10)
+                gbs = by / (ev * 1e-3) / 1e9
+                scale[f"b{batch}_kv{kv}"] = {"us_per_launch": round(ev * 1e3 / 12, 2),
+                                             "mb_per_launch": round(by / 12 / 1e6, 1),
+                                             "gbs": round(gbs, 1),
+                                             "frac": round(gbs / HBM_PEAK_GBS, 4)}
+                del graphs, sb
+                torch.cuda.empty_cache()
+        extras["decode_scale"] = scale
     if "prefill" in groups:
         extras["prefill_config1"] = bench_prefill(gpu, dev, W.config1_prefill(n_kv_head=12))
         extras["prefill_config1_gqa3"] = bench_prefill(gpu, dev, W.config1_prefill(n_kv_head=3))

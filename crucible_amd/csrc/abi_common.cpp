@@ -2,6 +2,7 @@
 // cu_seqlens -> segment helper used by packed prefill callers.
 #include "common.hpp"
 
+#include <atomic>
 #include <cstring>
 
 namespace crucible {
@@ -17,6 +18,25 @@ void set_error(int status, const char* fmt, ...) {
     va_start(ap, fmt);
     std::vsnprintf(g_last_message, sizeof(g_last_message), fmt, ap);
     va_end(ap);
+}
+
+int device_cu_count() {
+    constexpr int kMaxDevices = 64;
+    constexpr int kFallback = 256;  // MI355X
+    static std::atomic<int> cache[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();  // a failed query must not read as a later launch failure
+        return kFallback;
+    }
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        n = kFallback;
+    }
+    cache[dev].store(n, std::memory_order_relaxed);
+    return n;
 }
 
 int fail_launch(const char* what) {

@@ -283,7 +283,6 @@ constexpr int kOrderSplit = 0;
 constexpr int kOrderRequest = 1;
 constexpr int kOrderCompact = 2;
 constexpr int kCompactMaxBatch = 64;  // one lane per request
-constexpr int64_t kDecodeCUs = 256;   // MI355X
 
 // ORDER: how workgroup ids map to (split, kv head, request): kOrderSplit, grid (split,
 // kv head, request); kOrderRequest, grid (kv head, request, split); kOrderCompact, a 1-D
@@ -691,7 +690,8 @@ int launch_decode(DecodeArgs a, DecodeShape sh, bool q_f32, hipStream_t stream,
     // CRUCIBLE_DECODE_ORDER = split | request | compact overrides the choice; compact needs
     // batch <= 64 (one lane per request) and falls back to request-major past it.
     const int64_t units = (int64_t)a.n_splits * a.n_kv_head * a.batch;
-    int order = (units > kDecodeCUs && a.batch <= kCompactMaxBatch) ? kOrderCompact : kOrderRequest;
+    int order = (units > device_cu_count() && a.batch <= kCompactMaxBatch) ? kOrderCompact
+                                                                            : kOrderRequest;
     if (const char* env = std::getenv("CRUCIBLE_DECODE_ORDER")) {
         if (!std::strcmp(env, "split")) order = kOrderSplit;
         if (!std::strcmp(env, "request")) order = kOrderRequest;

@@ -888,7 +888,6 @@ LdsGrid lds_grid(const PrefillArgs& a, int64_t tile_rows_total, int64_t z) {
     return lg;
 }
 
-constexpr int64_t kCUs = 256;  // MI355X
 
 int launch_prefill(const PrefillArgs& a_in, int64_t tile_rows_total, int64_t z, bool q_f32,
                    hipStream_t stream, const char* what) {
@@ -911,7 +910,7 @@ int launch_prefill(const PrefillArgs& a_in, int64_t tile_rows_total, int64_t z, 
     // The register-direct form when the LDS form would leave CUs without a workgroup
     // (short prompts: config 1 is 96 workgroups); the LDS form, which reads each K/V tile
     // once per 64 rows instead of once per 16, when its grid fills the chip.
-    int direct = lg.gx * lg.gy * z < kCUs;
+    int direct = lg.gx * lg.gy * z < device_cu_count();
     if (const char* env = std::getenv("CRUCIBLE_PREFILL_DIRECT")) direct = std::atoi(env) != 0;
     if (direct) {
         const int64_t gy = (tile_rows_total + 15) / 16;

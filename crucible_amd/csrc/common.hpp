@@ -140,6 +140,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 void set_error(int status, const char* fmt, ...);
 int fail_launch(const char* what);
+// CUs of the current device (256 on MI355X), queried once per device: the launch-shape
+// choices compare grids against it.
+int device_cu_count();
 inline bool dtype_ok(int d) { return d == CRUCIBLE_F32 || d == CRUCIBLE_F16; }
 inline bool kind_ok(int k) { return k == CRUCIBLE_POOL_K || k == CRUCIBLE_POOL_V; }
 

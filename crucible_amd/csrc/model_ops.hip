@@ -482,7 +482,6 @@ __global__ __launch_bounds__(kLinThreads, 4) void linear4_kernel(LinArgs a) {
 
 // ---------------------------------------------------------------- wide projections
 
-constexpr int kCUs = 256;      // MI355X: one persistent workgroup per CU
 constexpr int kWideDepth = 4;  // weight tiles in flight per wave
 constexpr int kWideMaxIters = 16;  // tiles per workgroup (the walk is fully unrolled)
 
@@ -714,7 +713,7 @@ void launch_linear4(const LinArgs& a, hipStream_t stream) {
 // 16 columns. CRUCIBLE_LINEAR_TILE = 4 | 16 overrides the choice.
 bool use_tile4(int64_t n_out, int64_t rows, int cols16, bool norm) {
     if (const char* env = std::getenv("CRUCIBLE_LINEAR_TILE")) return std::atoi(env) == 4;
-    return !norm && ((n_out + cols16 - 1) / cols16) * ((rows + 15) / 16) < kCUs;
+    return !norm && ((n_out + cols16 - 1) / cols16) * ((rows + 15) / 16) < device_cu_count();
 }
 
 int check_linear(const char* what, const float* x, int64_t ldx, const float* norm_w,
@@ -765,7 +764,8 @@ extern "C" int crucible_linear_f64acc(const float* x, int64_t ldx, const float* 
         const int64_t tiles = (n_out + 15) / 16;
         // one workgroup per CU (and row block), or more when a CU would need more than
         // kWideMaxIters tiles
-        const int64_t per_cu = std::max<int64_t>(1, kCUs / std::min<int64_t>(row_blocks, kCUs));
+        const int64_t cus = device_cu_count();
+        const int64_t per_cu = std::max<int64_t>(1, cus / std::min<int64_t>(row_blocks, cus));
         const int64_t gx = std::min<int64_t>(
             tiles, std::max<int64_t>(per_cu, (tiles + kWideMaxIters - 1) / kWideMaxIters));
         const dim3 grid((unsigned)gx, (unsigned)row_blocks);

@@ -100,13 +100,37 @@ __device__ __forceinline__ float tile_max(const float4_t (&st)[4]) {
     return r;
 }
 
-// One lane's 16 scores of a 64-key tile, st[kb][r] = S^T[key 16 kb + 4 grp + r][q = col],
+// Key order of the LDS form's S^T products. Row m of key block kb (the MFMA's M index, lane group
+// m >> 2 holds rows 4 (m >> 2) .. +3) is key
+//   key(kb, m) = 32 (kb >> 1) + 8 (m >> 2) + 4 (kb & 1) + (m & 3)
+// of the 64-key tile, so after blocks 2 ks and 2 ks + 1 the lanes of group grp hold the
+// scores of keys 32 ks + 8 grp .. +7: eight consecutive keys, which is the k range that
+// lane group supplies to the PV product (k = 8 grp .. +7 of a 32-key step). Its V^T
+// operand is then 16 contiguous bytes of a channel row, one read instead of two 8-byte
+// halves joined by register moves. The softmax does not depend on the order of keys.
+__device__ __forceinline__ int tile_key(int kb, int m) {
+    return 32 * (kb >> 1) + 8 * (m >> 2) + 4 * (kb & 1) + (m & 3);
+}
+
+// One lane's 16 scores of a 64-key tile, st[kb][r] = S^T[key(kb, 4 grp + r)][q = col],
 // kept unscaled: the scale (> 0) is folded into the exponent, so the max needs none.
 
-// Causal mask: key 16 kb + 4 grp + r of the tile is visible iff 16 kb + r <= lim, where
-// lim = pos - kbase - 4 grp for a row in the run and -1 (nothing visible) otherwise.
-// Written as selects so that it compiles to a compare and a select per score.
+// Causal mask: key(kb, 4 grp + r) = 8 grp + 32 (kb >> 1) + 4 (kb & 1) + r of the tile is
+// visible iff 32 (kb >> 1) + 4 (kb & 1) + r <= lim, where lim = pos - kbase - 8 grp for a
+// row in the run and -1 (nothing visible) otherwise. Written as selects so that it
+// compiles to a compare and a select per score.
 __device__ __forceinline__ void mask_tile(float4_t (&st)[4], int lim) {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            st[kb][r] = (32 * (kb >> 1) + 4 * (kb & 1) + r <= lim) ? st[kb][r] : -INFINITY;
+}
+
+// The same mask in the plain block order of the register-direct form, whose K rows come
+// from global memory page by page (key block kb = page kb of the tile, st[kb][r] = key
+// 16 kb + 4 grp + r): visible iff 16 kb + r <= lim, lim = pos - kbase - 4 grp.
+__device__ __forceinline__ void mask_tile_blocks(float4_t (&st)[4], int lim) {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -116,8 +140,9 @@ __device__ __forceinline__ void mask_tile(float4_t (&st)[4], int lim) {
 // P = exp2(s * scale - mu) (one FMA and one exp per score), split into fp16 P = hi + lo
 // (hi truncates, lo = RNE(p - hi): exact to about 2^-22 relative), as the hi/lo
 // operands of the PV product: pb/pl[0] hold keys 0..31 of the tile, [1] keys 32..63, in
-// the B-operand layout the S^T product leaves (lane group grp: keys 4 grp .. +3 of each
-// 16-key block). Returns the lane's sum of P.
+// the B-operand layout the S^T product leaves (lane group grp: keys 32 ks + 8 grp .. +7
+// in the LDS form, see tile_key; keys 4 grp .. +3 of each 16-key block in the direct
+// form). Returns the lane's sum of P.
 //
 // The split per pair of values: hi = v_cvt_pkrtz (round toward zero), and lo = RNE(p -
 // hi) from v_fma_mix{lo,hi}_f16, which take hi as an fp16 operand, form p - hi exactly in
@@ -483,11 +508,11 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
             const int kbase = t * kKeyTile;
             if (t < n_tiles && wave_last >= kbase) {
                 const int buf = t % KB;
-                // S^T blocks: st[qb][kb] = S^T[kbase + 16*kb + 4*grp + r][q = col]
+                // S^T blocks: st[qb][kb] = S^T[kbase + key(kb, 4 grp + r)][q = col]
                 float4_t st[QB][4];
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb) {
-                    const int row = 16 * kb + col;
+                    const int row = tile_key(kb, col);
                     const half8_t a0 = *reinterpret_cast<const half8_t*>(
                         &s_k[buf][row][8 * (grp ^ (row & 7))]);
                     const half8_t a1 = *reinterpret_cast<const half8_t*>(
@@ -513,7 +538,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                 if (!__all(lane_full)) {
 #pragma unroll
                     for (int qb = 0; qb < QB; ++qb)
-                        mask_tile(st[qb], in_run[qb] ? my_pos[qb] - kbase - 4 * grp : -1);
+                        mask_tile(st[qb], in_run[qb] ? my_pos[qb] - kbase - 8 * grp : -1);
                 }
                 half8_t pb[QB][2];
                 half8_t pl[QB][2];  // P = hi + lo: the product keeps ~22 bits of P
@@ -544,13 +569,9 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                     const int d = 16 * db + col;
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) {
-                        const int c1 = 4 * ks + (grp >> 1);
-                        const int o = 4 * (grp & 1);
-                        const half4_t v0 = *reinterpret_cast<const half4_t*>(
-                            &s_v[buf][d][8 * (c1 ^ (d & 7)) + o]);
-                        const half4_t v1 = *reinterpret_cast<const half4_t*>(
-                            &s_v[buf][d][8 * ((c1 + 2) ^ (d & 7)) + o]);
-                        const half8_t va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                        // keys 32 ks + 8 grp .. +7: 16-byte chunk 4 ks + grp of the row
+                        const half8_t va = *reinterpret_cast<const half8_t*>(
+                            &s_v[buf][d][8 * ((4 * ks + grp) ^ (d & 7))]);
 #pragma unroll
                         for (int qb = 0; qb < QB; ++qb) {
                             acc[qb][db] = mfma_16x16x32(va, pb[qb][ks], acc[qb][db]);
@@ -776,7 +797,7 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
                 st[kb] = c;
             }
             if (!__all(in_run && my_pos >= kbase + kKeyTile - 1))
-                mask_tile(st, in_run ? my_pos - kbase - 4 * grp : -1);
+                mask_tile_blocks(st, in_run ? my_pos - kbase - 4 * grp : -1);
             const float tm = tile_max(st) * a.scale_log2;  // base-2 units
             const bool grow = tm > m + kLazyLog2;
             if (__any(grow)) {

@@ -52,8 +52,9 @@ def parse_args():
     p.add_argument("--extras", default="decode,prefill,e2e",
                    help="comma list of extra groups to run: decode (the other decode "
                         "shapes), prefill (configs 1 and 4), e2e (config 5), scale (the "
-                        "fused decode at batch 32..256, config 3's length distribution; "
-                        "not in the default set)")
+                        "fused decode at batch 32..256 with config 3's length "
+                        "distribution, and prefill of 2k..8k-token sequences; not in the "
+                        "default set)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 256 MiB device copy (PMC traffic calibration)")
     return p.parse_args()
@@ -482,6 +483,15 @@ def main():
                 del graphs, sb
                 torch.cuda.empty_cache()
         extras["decode_scale"] = scale
+        # prefill with longer sequences: the MFMA rate once a launch is compute-heavy
+        pscale = {}
+        for name, lens, nh, nkv in (("seq2048_12h", [2048], 12, 12), ("seq4096_12h", [4096], 12, 12),
+                                    ("seq8192_12h", [8192], 12, 12),
+                                    ("packed8x2048_16h4kv", [2048] * 8, 16, 4)):
+            r = bench_prefill(gpu, dev, W.prefill_sequences(name, lens, nh, nkv), launches=10)
+            pscale[name] = {k: r[k] for k in ("us_per_launch", "tflops", "frac_of_mfma_f16_peak")}
+            torch.cuda.empty_cache()
+        extras["prefill_scale"] = pscale
     if "prefill" in groups:
         extras["prefill_config1"] = bench_prefill(gpu, dev, W.config1_prefill(n_kv_head=12))
         extras["prefill_config1_gqa3"] = bench_prefill(gpu, dev, W.config1_prefill(n_kv_head=3))

@@ -175,6 +175,17 @@ def config4_packed(seed: int = BASE_SEED + 3) -> PrefillConfig:
     return cfg
 
 
+def prefill_sequences(name: str, seq_lens, n_head: int, n_kv_head: int,
+                      seed: int = BASE_SEED + 5) -> PrefillConfig:
+    """Causal prefill of the given sequences (packed when more than one), for the scaling
+    measurements beside configs 1 and 4."""
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(seq_lens, np.int32)
+    cfg = PrefillConfig(name, n_head, n_kv_head, lens, seed=seed)
+    cfg.tables, cfg.n_pages = _prefill_tables(rng, lens)
+    return cfg
+
+
 def device_normal(shape, dtype, seed: int, device) -> torch.Tensor:
     """N(0,1) on the device from a seeded generator, cast (RNE) to dtype."""
     gen = torch.Generator(device=device)

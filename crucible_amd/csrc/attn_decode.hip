@@ -630,7 +630,8 @@ DecodeShape decode_shape(int64_t batch, int64_t n_kv_head, int64_t max_pages) {
     const int64_t units = batch * n_kv_head * max_pages;
     DecodeShape sh{1, 8};                 // 8-page splits: few requests, short contexts
     if (units > 2048) sh = {2, 8};        // 16-page splits (e.g. b16 x 3 kv heads x 2048)
-    if (units > 8192) sh = {4, 4};        // 16-page splits, 4 pages a wave (b16 x 12 x 2048)
+    if (units > 8192) sh = {4, 8};        // 32-page splits, 4 pages a wave (b16 x 12 x 2048)
+    if (units > 32768) sh = {4, 4};       // 16-page splits, 4 pages a wave (b64 x 12 x 2048)
     if (const char* env = std::getenv("CRUCIBLE_DECODE_PAGES")) {
         const int v = std::atoi(env);
         if (v == 1 || v == 2 || v == 4) sh.pages = v;

@@ -339,11 +339,14 @@ def test_grid_orders_are_bit_identical(gpu, dev, monkeypatch):
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
 
 
-def test_batch_past_the_compact_limit(gpu, dev):
-    """Batches above 64 requests (one lane per request in the compact order's search) use
-    the request-major grid; the answer is the oracle's either way."""
-    lens = [int(x) for x in np.random.default_rng(44).integers(0, 300, 70)]
+@pytest.mark.parametrize("batch", [64, 70])
+def test_batch_at_and_past_the_compact_limit(gpu, dev, batch):
+    """64 requests is the compact order's largest batch (one lane per request in its
+    search); above it the launch falls back to the request-major grid. The answer is the
+    oracle's either way, and inactive requests keep their output."""
+    lens = [int(x) for x in np.random.default_rng(44 + batch).integers(0, 700, batch)]
     lens[3] = 0
+    lens[batch - 1] = 0
     q, k_pool, v_pool, tables, stride = _case(45, lens, 12, 3)
     got = _run_decode(gpu, dev, q, k_pool, v_pool, tables, lens, 12, 3, 3, 1, stride * 16)
     want = _oracle(q, k_pool, v_pool, tables, lens, 12, 3, 3, 1)

@@ -282,11 +282,93 @@ __device__ __forceinline__ void store_new_row(const DecodeArgs& a, const NewRow&
 constexpr int kOrderSplit = 0;
 constexpr int kOrderRequest = 1;
 constexpr int kOrderCompact = 2;
-constexpr int kCompactMaxBatch = 64;  // one lane per request
+constexpr int kCompactPerLane = 4;    // requests per lane in the compact order's search
+constexpr int kCompactMaxBatch = 64 * kCompactPerLane;
+
+// The compact order's search: the unit workgroup blockIdx.x serves. Units are split k <
+// n_active of every (request, kv head) that attends, plus one append-only unit where the
+// appended row lies in a split past the attended ones, numbered in (k, request, kv head)
+// order. Lane L holds requests L + 64 q, q < NQ (batch <= 64 NQ): their lengths and
+// positions come in one round of vector loads. Returns false (uniformly) when the id is
+// past the last unit.
+struct CompactUnit {
+    int k, g, lane, set, len, pos, n_active, split_append;
+};
+
+template <int NQ, bool APPEND>
+__device__ __forceinline__ bool compact_find(const DecodeArgs& a, int lane, CompactUnit& u) {
+    int lc[NQ], na[NQ], sap[NQ], un[NQ], pv[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int rq = lane + 64 * q;
+        int lv = 0;
+        pv[q] = -1;
+        if (rq < a.batch) {
+            lv = a.lens[rq * a.lens_stride + a.lens_off];
+            if constexpr (APPEND) pv[q] = a.positions[rq];
+        }
+        lc[q] = lv < a.max_seq ? lv : a.max_seq;  // never index past the table
+        const int np = lc[q] > 0 ? (lc[q] + kPageMask) >> kPageShift : 0;
+        na[q] = (np + (1 << a.split_shift) - 1) >> a.split_shift;
+        sap[q] = (APPEND && pv[q] >= 0 && pv[q] < (a.max_pages << kPageShift))
+                     ? pv[q] >> (kPageShift + a.split_shift) : -1;
+        un[q] = na[q] + (sap[q] >= na[q] ? 1 : 0);
+    }
+    int k = 0, base = 0;
+    uint64_t mask[NQ];
+    for (;;) {  // at most n_splits + 1 rounds: a request has at most n_splits units
+        int cnt = 0;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            mask[q] = __ballot(un[q] > k);
+            cnt += __popcll(mask[q]);
+        }
+        cnt *= a.n_kv_head;
+        if (cnt == 0 || k > a.n_splits) return false;
+        if ((int)blockIdx.x < base + cnt) break;
+        base += cnt;
+        ++k;
+    }
+    const int j = (int)blockIdx.x - base;
+    int r = j / a.n_kv_head;  // rank of the request among those with a unit k
+    u.k = k;
+    u.g = j - r * a.n_kv_head;
+    // the r-th set bit over the masks in request order: mask q covers requests 64 q ..
+    int qs = 0;
+#pragma unroll
+    for (int q = 0; q < NQ - 1; ++q) {
+        const int c = __popcll(mask[q]);
+        if (qs == q && r >= c) {
+            r -= c;
+            qs = q + 1;
+        }
+    }
+    uint64_t mq = mask[0];
+    int lcq = lc[0], pvq = pv[0], naq = na[0], sapq = sap[0];
+#pragma unroll
+    for (int q = 1; q < NQ; ++q)
+        if (qs == q) {
+            mq = mask[q];
+            lcq = lc[q];
+            pvq = pv[q];
+            naq = na[q];
+            sapq = sap[q];
+        }
+    const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
+        (uint32_t)(mq >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mq, 0u));
+    const int bl = __builtin_ctzll(__ballot(((mq >> lane) & 1) && (int)rank == r));
+    u.lane = bl;
+    u.set = qs;
+    u.len = __builtin_amdgcn_readlane(lcq, bl);
+    u.pos = __builtin_amdgcn_readlane(pvq, bl);
+    u.n_active = __builtin_amdgcn_readlane(naq, bl);
+    u.split_append = __builtin_amdgcn_readlane(sapq, bl);
+    return true;
+}
 
 // ORDER: how workgroup ids map to (split, kv head, request): kOrderSplit, grid (split,
 // kv head, request); kOrderRequest, grid (kv head, request, split); kOrderCompact, a 1-D
-// grid over the units that have work, found from the lengths (batch <= 64).
+// grid over the units that have work, found from the lengths (batch <= 256).
 // ROPE (with QF32 and APPEND): rotate q and the appended K row at the append position.
 // CW: splits merged per round trip by the combining workgroup (combine_partials).
 template <int PAGES, int WAVES, bool QF32, bool APPEND, bool PAGED, int ORDER, bool ROPE,
@@ -308,43 +390,22 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     int s, g, b, len, pos = -1;
     int gathered = 0;  // lanes < PAGES: this wave's page ids
     if constexpr (ORDER == kOrderCompact) {
-        // Units: split k < n_active of every (request, kv head) that attends, plus one
-        // append-only unit where the appended row lies in a split past the attended ones.
-        // Workgroup i serves the i-th unit in (k, request, kv head) order, so the units
-        // take the lowest workgroup ids and a launch whose units fit the CUs gets one CU
-        // per unit; the ids past the last unit return at once. The lengths and positions
-        // of all requests (lane = request, batch <= 64) come in one vector load; the page
-        // ids follow in a second round trip.
-        int lv = 0, pv = -1;
-        if (lane < a.batch) {
-            lv = a.lens[lane * a.lens_stride + a.lens_off];
-            if constexpr (APPEND) pv = a.positions[lane];
-        }
-        const int lc = lv < a.max_seq ? lv : a.max_seq;  // never index past the table
-        const int np = lc > 0 ? (lc + kPageMask) >> kPageShift : 0;
-        const int na = (np + (1 << a.split_shift) - 1) >> a.split_shift;
-        const int sap = (APPEND && pv >= 0 && pv < (a.max_pages << kPageShift))
-                            ? pv >> (kPageShift + a.split_shift) : -1;
-        const int units = na + (sap >= na ? 1 : 0);
-        int k = 0, base = 0;
-        uint64_t mask;
-        for (;;) {  // at most n_splits + 1 rounds: a request has at most n_splits units
-            mask = __ballot(units > k);
-            const int cnt = __popcll(mask) * a.n_kv_head;
-            if (cnt == 0 || k > a.n_splits) return;  // uniform: no unit for this workgroup
-            if ((int)blockIdx.x < base + cnt) break;
-            base += cnt;
-            ++k;
-        }
-        const int j = (int)blockIdx.x - base;
-        const int r = j / a.n_kv_head;  // rank of the request among those with a unit k
-        g = j - r * a.n_kv_head;
-        const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
-            (uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-        b = __builtin_ctzll(__ballot(((mask >> lane) & 1) && (int)rank == r));
-        len = __builtin_amdgcn_readlane(lc, b);
-        if constexpr (APPEND) pos = __builtin_amdgcn_readlane(pv, b);
-        s = k < __builtin_amdgcn_readlane(na, b) ? k : __builtin_amdgcn_readlane(sap, b);
+        // Workgroup i serves the i-th unit (compact_find), so the units take the lowest
+        // workgroup ids and a launch whose units fit the CUs gets one CU per unit; the ids
+        // past the last unit return at once. The page ids follow the lengths in a second
+        // round trip. One request per lane up to batch 64 keeps the search short there.
+        CompactUnit u;
+        const bool found = a.batch <= 64 ? compact_find<1, APPEND>(a, lane, u)
+                                         : compact_find<kCompactPerLane, APPEND>(a, lane, u);
+        if (!found) return;  // uniform: no unit for this workgroup
+        const int bl = u.lane;
+        const int qs = u.set;
+        const int k = u.k;
+        g = u.g;
+        b = bl + 64 * qs;
+        len = u.len;
+        if constexpr (APPEND) pos = u.pos;
+        s = k < u.n_active ? k : u.split_append;
         if (PAGED && lane < PAGES)
             gathered = a.tables[(int64_t)b * a.table_stride +
                                 min((s << a.split_shift) + wave * PAGES + lane, a.max_pages - 1)];
@@ -689,7 +750,7 @@ int launch_decode(DecodeArgs a, DecodeShape sh, bool q_f32, hipStream_t stream,
     // that fits the CUs keeps the request-major order: every request's first splits are
     // dispatched first (measured faster than split-major with the default shapes).
     // CRUCIBLE_DECODE_ORDER = split | request | compact overrides the choice; compact needs
-    // batch <= 64 (one lane per request) and falls back to request-major past it.
+    // batch <= 256 (four requests per lane) and falls back to request-major past it.
     const int64_t units = (int64_t)a.n_splits * a.n_kv_head * a.batch;
     int order = (units > device_cu_count() && a.batch <= kCompactMaxBatch) ? kOrderCompact
                                                                             : kOrderRequest;

@@ -339,11 +339,12 @@ def test_grid_orders_are_bit_identical(gpu, dev, monkeypatch):
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
 
 
-@pytest.mark.parametrize("batch", [64, 70])
+@pytest.mark.parametrize("batch", [64, 70, 256, 260])
 def test_batch_at_and_past_the_compact_limit(gpu, dev, batch):
-    """64 requests is the compact order's largest batch (one lane per request in its
-    search); above it the launch falls back to the request-major grid. The answer is the
-    oracle's either way, and inactive requests keep their output."""
+    """The compact order's search holds up to four requests per lane: 64 requests fill one
+    set of lanes, 70 and 256 take two and four, and above 256 the launch falls back to the
+    request-major grid. The answer is the oracle's either way, and inactive requests keep
+    their output."""
     lens = [int(x) for x in np.random.default_rng(44 + batch).integers(0, 700, batch)]
     lens[3] = 0
     lens[batch - 1] = 0

@@ -54,7 +54,7 @@ def parse_args():
                         "shapes), prefill (configs 1 and 4), e2e (config 5), scale (the "
                         "fused decode at batch 32..256 with config 3's length "
                         "distribution, and prefill of 2k..8k-token sequences; not in the "
-                        "default set)")
+                        "default set), pscale (only the prefill part of scale)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 256 MiB device copy (PMC traffic calibration)")
     return p.parse_args()
@@ -483,6 +483,7 @@ def main():
                 del graphs, sb
                 torch.cuda.empty_cache()
         extras["decode_scale"] = scale
+    if "scale" in groups or "pscale" in groups:
         # prefill with longer sequences: the MFMA rate once a launch is compute-heavy
         pscale = {}
         for name, lens, nh, nkv in (("seq2048_12h", [2048], 12, 12), ("seq4096_12h", [4096], 12, 12),

@@ -388,7 +388,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     // Which (split s, kv head g, request b) this workgroup serves, its page ids, the
     // request's length and its append position.
     int s, g, b, len, pos = -1;
-    int gathered = 0;  // lanes < PAGES: this wave's page ids
+    int pid[PAGES] = {};  // this wave's page ids, through the scalar cache
     if constexpr (ORDER == kOrderCompact) {
         // Workgroup i serves the i-th unit (compact_find), so the units take the lowest
         // workgroup ids and a launch whose units fit the CUs gets one CU per unit; the ids
@@ -406,31 +406,47 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
         len = u.len;
         if constexpr (APPEND) pos = u.pos;
         s = k < u.n_active ? k : u.split_append;
-        if (PAGED && lane < PAGES)
-            gathered = a.tables[(int64_t)b * a.table_stride +
-                                min((s << a.split_shift) + wave * PAGES + lane, a.max_pages - 1)];
+        // The page ids are uniform per wave: scalar loads (the table in the constant
+        // address space: nothing writes it during the launch), which do not queue behind
+        // the vector loads of workgroups already streaming pages on this CU.
+        if constexpr (PAGED) {
+            typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+            const const_i32_ptr row = (const_i32_ptr)(a.tables + (int64_t)b * a.table_stride);
+            const int i0 = (s << a.split_shift) + wave * PAGES;
+#pragma unroll
+            for (int i = 0; i < PAGES; ++i) {
+                pid[i] = row[min(i0 + i, a.max_pages - 1)];
+                asm volatile("" : "+s"(pid[i]));  // issued here, not behind a branch
+            }
+        }
     } else {
         // Grid (kv head, request, split), request-major: every request's first splits are
         // dispatched before any later split, and the later ones (often past the request's
         // end) queue last; or (split, kv head, request). No integer division on the way to
-        // the loads. The page ids, the length and the append position come from ONE vector
-        // load (lane i < PAGES: page id i; lane PAGES: length; lane PAGES + 1: append
-        // position) and are broadcast with readlane, so no compiler scheduling can split
-        // them into dependent scalar loads. Table indices are clamped into the table, so
-        // every lane's address is in bounds (ids of pages past the request's end are never
-        // used).
+        // the loads. The page ids, the length and the append position are independent
+        // scalar loads (one round trip through the scalar cache). Table indices are
+        // clamped into the table, so every address is in bounds (ids of pages past the
+        // request's end are never used).
         s = ORDER == kOrderRequest ? blockIdx.z : blockIdx.x;
         g = ORDER == kOrderRequest ? blockIdx.x : blockIdx.y;
         b = ORDER == kOrderRequest ? blockIdx.y : blockIdx.z;
-        const int32_t* src = a.lens + b * a.lens_stride + a.lens_off;
-        if (PAGED && lane < PAGES)
-            src = a.tables + (int64_t)b * a.table_stride +
-                  min((s << a.split_shift) + wave * PAGES + lane, a.max_pages - 1);
-        if (APPEND && lane == PAGES + 1) src = a.positions + b;
-        gathered = *src;
-        const int len_raw = __builtin_amdgcn_readlane(gathered, PAGES);
-        len = len_raw < a.max_seq ? len_raw : a.max_seq;  // never index past the table
-        if constexpr (APPEND) pos = __builtin_amdgcn_readlane(gathered, PAGES + 1);
+        typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+        const int len_raw = ((const_i32_ptr)a.lens)[b * a.lens_stride + a.lens_off];
+        if constexpr (PAGED) {
+            const const_i32_ptr row = (const_i32_ptr)(a.tables + (int64_t)b * a.table_stride);
+            const int i0 = (s << a.split_shift) + wave * PAGES;
+#pragma unroll
+            for (int i = 0; i < PAGES; ++i) pid[i] = row[min(i0 + i, a.max_pages - 1)];
+        }
+        if constexpr (APPEND) pos = ((const_i32_ptr)a.positions)[b];
+        // Pin the loads here, so that none is sunk behind a branch on the length (which
+        // would make it a second, dependent round trip).
+        int lr = len_raw;
+        asm volatile("" : "+s"(lr));
+#pragma unroll
+        for (int i = 0; i < PAGES; ++i) asm volatile("" : "+s"(pid[i]));
+        if constexpr (APPEND) asm volatile("" : "+s"(pos));
+        len = lr < a.max_seq ? lr : a.max_seq;  // never index past the table
     }
     const int bg = b * a.n_kv_head + g;
 
@@ -468,7 +484,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     int64_t page[PAGES];
 #pragma unroll
     for (int i = 0; i < PAGES; ++i)
-        page[i] = PAGED ? (int64_t)__builtin_amdgcn_readlane(gathered, i) : (int64_t)(wp0 + i);
+        page[i] = PAGED ? (int64_t)pid[i] : (int64_t)(wp0 + i);
     int apos = -1;  // position of the row this workgroup appends, or -1
     if (APPEND && pos >= 0 && pos < (a.max_pages << kPageShift) &&
         (pos >> (kPageShift + a.split_shift)) == s)

@@ -680,21 +680,51 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
     const int h = wp.x;
     const int g = h / a.n_rep;
 
-    int row = -1, owner = 0, pos = 0;
-    if (tid < 16) {
-        tile_row(a, wp.req, wp.tile * 16 + tid, row, owner, pos);
-        s_row[tid] = row;
-        s_owner[tid] = owner;
-        s_pos[tid] = pos;
+    // Rows of this tile. Outside the OWNERS mode they follow from one uniform descriptor
+    // (first row, row count, first position, owner) read through the scalar cache, and
+    // the valid rows are one range [lo, hi) of the tile: no LDS round trip, no barrier.
+    // OWNERS tiles take their rows from per-row arrays, staged in LDS.
+    uint64_t mask;
+    int my_row, my_pos, d_owner = 0, d_hist = 0;
+    if (a.mode != kOwners) {
+        typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+        int64_t row0 = 0, len = a.rows, pos0 = a.pos_offset;
+        if (a.mode == kSegments) {
+            const const_i32_ptr seg = (const_i32_ptr)(a.segments + 4 * wp.req);
+            row0 = seg[0];
+            len = seg[1];
+            pos0 = seg[2];
+            d_owner = seg[3];
+        } else if (a.mode == kParams) {
+            pos0 = ((const_i32_ptr)a.params)[kParamPrefillPos];
+        }
+        const int64_t base = wp.tile * 16;
+        // local row base + r is valid iff r < len - base and 0 <= pos0 + base + r < max_seq
+        const int64_t lo64 = max((int64_t)0, -(pos0 + base));
+        const int64_t hi64 = min((int64_t)16, min(len - base, (int64_t)a.max_seq - (pos0 + base)));
+        if (lo64 >= hi64) return;  // uniform: no row of this tile is valid
+        const int lo = (int)lo64, hi = (int)hi64;
+        mask = ((hi == 64 ? 0ull : (1ull << hi)) - 1) & ~((1ull << lo) - 1);
+        const bool valid = col >= lo && col < hi;
+        my_row = valid ? (int)(row0 + base + col) : -1;
+        my_pos = (int)(pos0 + base + (valid ? col : lo));
+        d_hist = (int)(pos0 + base + hi);  // one past the last valid row's position
+    } else {
+        int row = -1, owner = 0, pos = 0;
+        if (tid < 16) {
+            tile_row(a, wp.req, wp.tile * 16 + tid, row, owner, pos);
+            s_row[tid] = row;
+            s_owner[tid] = owner;
+            s_pos[tid] = pos;
+        }
+        const uint64_t vmask = __ballot(tid < 16 && row >= 0);
+        if (wave == 0 && lane == 0) s_mask = vmask;
+        __syncthreads();
+        mask = s_mask;
+        if (mask == 0) return;  // uniform: no row of this tile is valid
+        my_row = s_row[col];
+        my_pos = s_pos[col];
     }
-    const uint64_t vmask = __ballot(tid < 16 && row >= 0);
-    if (wave == 0 && lane == 0) s_mask = vmask;
-    __syncthreads();
-    const uint64_t mask = s_mask;
-    if (mask == 0) return;  // uniform: no row of this tile is valid
-
-    const int my_row = s_row[col];
-    const int my_pos = s_pos[col];
     const int64_t ld_q = (int64_t)a.n_head * kHeadDim;
     half8_t qh0 = {}, qh1 = {}, ql0 = {}, ql1 = {};
     if (my_row >= 0) {
@@ -726,9 +756,9 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
         int r1, owner_r, hist_end, wave_last;
         if (a.mode != kOwners) {
             r1 = last_valid + 1;
-            owner_r = s_owner[r0];
-            hist_end = s_pos[last_valid] + 1;
-            wave_last = s_pos[last_valid];
+            owner_r = d_owner;
+            hist_end = d_hist;
+            wave_last = d_hist - 1;
         } else {
             while (r0 < 16 && s_row[r0] < 0) ++r0;
             if (r0 >= 16) break;

@@ -17,6 +17,11 @@ F32, F16 = 0, 1
 POOL_K, POOL_V = 0, 1
 PARAM_SEQ, PARAM_PREFILL_POS = 3, 5
 PAGE_TOKENS = 16
+# launch-shape override keys (enum crucible_tuning_key) and the decode order values
+TUNE_KEYS = {"decode_pages": 0, "decode_waves": 1, "decode_order": 2, "prefill_direct": 3,
+             "prefill_heavy_first": 4, "prefill_qb": 5, "prefill_bufs": 6, "linear_tile": 7,
+             "decode_split_pages": 8}
+DECODE_ORDERS = {"split": 0, "request": 1, "compact": 2}
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -27,6 +32,9 @@ _SZ = ctypes.c_size_t
 SIGNATURES = {
     "crucible_attn_version": ([], ctypes.c_char_p),
     "crucible_attn_last_error": ([ctypes.c_char_p, _SZ], _I),
+    "crucible_attn_set_tuning": ([_I, _I], _I),
+    "crucible_attn_get_tuning": ([_I], _I),
+    "crucible_attn_tuning_name": ([_I], ctypes.c_char_p),
     "crucible_cache_store": ([_P, _I, _P, _I, _I64, _I64, _I64, _I64, _P], _I),
     "crucible_cache_store_paged": ([_P, _I, _P, _I, _P, _I64, _I64, _I64, _I64, _P, _P], _I),
     "crucible_cache_store_rows_paged": ([_P, _I, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _I64, _P], _I),

@@ -3,7 +3,9 @@
 #include "common.hpp"
 
 #include <atomic>
+#include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 namespace crucible {
 
@@ -39,6 +41,69 @@ int device_cu_count() {
     return n;
 }
 
+// Launch-shape overrides. Each key starts at its environment variable, read once per process
+// (the first time any key is asked for), and after that changes only through
+// crucible_attn_set_tuning. -1 means the launcher's own choice.
+namespace {
+struct TuneKey {
+    const char* env;
+    int lo, hi;  // accepted values
+};
+constexpr TuneKey kTuneKeys[CRUCIBLE_TUNE_COUNT] = {
+    {"CRUCIBLE_DECODE_PAGES", 1, 4},          // pages per wave: 1, 2 or 4
+    {"CRUCIBLE_DECODE_WAVES", 4, 8},          // waves per workgroup: 4 or 8
+    {"CRUCIBLE_DECODE_ORDER", 0, 2},          // 0 split, 1 request, 2 compact
+    {"CRUCIBLE_PREFILL_DIRECT", 0, 1},        // register-direct form off / on
+    {"CRUCIBLE_PREFILL_HEAVY_FIRST", 0, 1},   // longest-first grid off / on
+    {"CRUCIBLE_PREFILL_QB", 1, 2},            // 16-row blocks per wave
+    {"CRUCIBLE_PREFILL_BUFS", 4, 6},          // key tiles in the LDS ring: 4 or 6
+    {"CRUCIBLE_LINEAR_TILE", 4, 16},          // projection tile columns: 4 or 16
+    {"CRUCIBLE_DECODE_SPLIT_PAGES", 1, 16},   // pages per unit in the work plan
+};
+
+bool tune_value_ok(int key, int v) {
+    switch (key) {
+        case CRUCIBLE_TUNE_DECODE_PAGES: return v == 1 || v == 2 || v == 4;
+        case CRUCIBLE_TUNE_DECODE_WAVES: return v == 4 || v == 8;
+        case CRUCIBLE_TUNE_PREFILL_BUFS: return v == 4 || v == 6;
+        case CRUCIBLE_TUNE_LINEAR_TILE: return v == 4 || v == 16;
+        default: return v >= kTuneKeys[key].lo && v <= kTuneKeys[key].hi;
+    }
+}
+
+int parse_env(int key, const char* s) {
+    if (key == CRUCIBLE_TUNE_DECODE_ORDER) {
+        if (!std::strcmp(s, "split")) return 0;
+        if (!std::strcmp(s, "request")) return 1;
+        if (!std::strcmp(s, "compact")) return 2;
+        return -1;
+    }
+    char* end = nullptr;
+    const long v = std::strtol(s, &end, 10);
+    if (end == s || *end != '\0') return -1;
+    if (key == CRUCIBLE_TUNE_PREFILL_DIRECT || key == CRUCIBLE_TUNE_PREFILL_HEAVY_FIRST)
+        return v != 0;
+    return tune_value_ok(key, (int)v) ? (int)v : -1;
+}
+
+std::atomic<int> g_tune[CRUCIBLE_TUNE_COUNT];
+std::once_flag g_tune_once;
+
+void tune_init() {
+    std::call_once(g_tune_once, [] {
+        for (int k = 0; k < CRUCIBLE_TUNE_COUNT; ++k) {
+            const char* env = std::getenv(kTuneKeys[k].env);
+            g_tune[k].store(env ? parse_env(k, env) : -1, std::memory_order_relaxed);
+        }
+    });
+}
+}  // namespace
+
+int tuning(int key) {
+    tune_init();
+    return g_tune[key].load(std::memory_order_relaxed);
+}
+
 int fail_launch(const char* what) {
     const hipError_t e = hipGetLastError();
     if (e == hipSuccess) return CRUCIBLE_OK;
@@ -50,6 +115,31 @@ int fail_launch(const char* what) {
 
 extern "C" const char* crucible_attn_version(void) {
     return "crucible_attn 0.1.0 gfx950";
+}
+
+extern "C" int crucible_attn_set_tuning(int key, int value) {
+    if (key < 0 || key >= CRUCIBLE_TUNE_COUNT) {
+        crucible::set_error(CRUCIBLE_ERR_INVALID, "set_tuning: unknown key %d", key);
+        return CRUCIBLE_ERR_INVALID;
+    }
+    if (value != -1 && !crucible::tune_value_ok(key, value)) {
+        crucible::set_error(CRUCIBLE_ERR_INVALID, "set_tuning: %s does not take %d",
+                            crucible::kTuneKeys[key].env, value);
+        return CRUCIBLE_ERR_INVALID;
+    }
+    crucible::tune_init();
+    crucible::g_tune[key].store(value, std::memory_order_relaxed);
+    return CRUCIBLE_OK;
+}
+
+extern "C" int crucible_attn_get_tuning(int key) {
+    if (key < 0 || key >= CRUCIBLE_TUNE_COUNT) return -1;
+    return crucible::tuning(key);
+}
+
+extern "C" const char* crucible_attn_tuning_name(int key) {
+    if (key < 0 || key >= CRUCIBLE_TUNE_COUNT) return nullptr;
+    return crucible::kTuneKeys[key].env;
 }
 
 extern "C" int crucible_attn_last_error(char* buf, size_t n) {

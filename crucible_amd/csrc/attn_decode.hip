@@ -709,14 +709,8 @@ DecodeShape decode_shape(int64_t batch, int64_t n_kv_head, int64_t max_pages) {
     if (units > 2048) sh = {2, 8};        // 16-page splits (e.g. b16 x 3 kv heads x 2048)
     if (units > 8192) sh = {4, 8};        // 32-page splits, 4 pages a wave (b16 x 12 x 2048)
     if (units > 32768) sh = {4, 4};       // 16-page splits, 4 pages a wave (b64 x 12 x 2048)
-    if (const char* env = std::getenv("CRUCIBLE_DECODE_PAGES")) {
-        const int v = std::atoi(env);
-        if (v == 1 || v == 2 || v == 4) sh.pages = v;
-    }
-    if (const char* env = std::getenv("CRUCIBLE_DECODE_WAVES")) {
-        const int v = std::atoi(env);
-        if (v == 4 || v == 8) sh.waves = v;
-    }
+    if (const int v = tuning(CRUCIBLE_TUNE_DECODE_PAGES); v > 0) sh.pages = v;
+    if (const int v = tuning(CRUCIBLE_TUNE_DECODE_WAVES); v > 0) sh.waves = v;
     return sh;
 }
 
@@ -765,16 +759,13 @@ int launch_decode(DecodeArgs a, DecodeShape sh, bool q_f32, hipStream_t stream,
     // a second round trip before the pages (lengths first, then the page ids), so a grid
     // that fits the CUs keeps the request-major order: every request's first splits are
     // dispatched first (measured faster than split-major with the default shapes).
-    // CRUCIBLE_DECODE_ORDER = split | request | compact overrides the choice; compact needs
-    // batch <= 256 (four requests per lane) and falls back to request-major past it.
+    // CRUCIBLE_TUNE_DECODE_ORDER overrides the choice; compact needs batch <= 256 (four
+    // requests per lane) and falls back to request-major past it.
     const int64_t units = (int64_t)a.n_splits * a.n_kv_head * a.batch;
     int order = (units > device_cu_count() && a.batch <= kCompactMaxBatch) ? kOrderCompact
                                                                             : kOrderRequest;
-    if (const char* env = std::getenv("CRUCIBLE_DECODE_ORDER")) {
-        if (!std::strcmp(env, "split")) order = kOrderSplit;
-        if (!std::strcmp(env, "request")) order = kOrderRequest;
-        if (!std::strcmp(env, "compact") && a.batch <= kCompactMaxBatch) order = kOrderCompact;
-    }
+    if (const int v = tuning(CRUCIBLE_TUNE_DECODE_ORDER); v >= 0)
+        order = (v == kOrderCompact && a.batch > kCompactMaxBatch) ? kOrderRequest : v;
     CRUCIBLE_CHECK(units <= 0x7fffffff, CRUCIBLE_ERR_INVALID, "%s: grid of %lld too large", what,
                    (long long)units);
     const dim3 grid = order == kOrderCompact ? dim3((unsigned)units)

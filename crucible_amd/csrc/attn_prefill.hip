@@ -931,10 +931,7 @@ LdsGrid lds_grid(const PrefillArgs& a, int64_t tile_rows_total, int64_t z) {
     const int rs = 4 / lg.hpw;
     auto tiles = [&](int qb) { return (tile_rows_total + rs * 16 * qb - 1) / (rs * 16 * qb); };
     lg.qb = (lg.gx * tiles(2) * z * 4 >= 2048) ? 2 : 1;
-    if (const char* env = std::getenv("CRUCIBLE_PREFILL_QB")) {
-        const int v = std::atoi(env);
-        if (v == 1 || v == 2) lg.qb = v;
-    }
+    if (const int v = tuning(CRUCIBLE_TUNE_PREFILL_QB); v > 0) lg.qb = v;
     lg.gy = tiles(lg.qb);
     return lg;
 }
@@ -946,8 +943,7 @@ int launch_prefill(const PrefillArgs& a_in, int64_t tile_rows_total, int64_t z, 
     // Longest-first for the LDS form, whose grids exceed the resident workgroups (config 4:
     // 16.5 -> 13.3 us); the direct form's grid fits the chip and keeps the plain order
     // (config 1: 7.9 against 8.2 us longest-first).
-    int heavy = -1;  // by form
-    if (const char* env = std::getenv("CRUCIBLE_PREFILL_HEAVY_FIRST")) heavy = std::atoi(env) != 0;
+    const int heavy = tuning(CRUCIBLE_TUNE_PREFILL_HEAVY_FIRST);  // -1: by form
     // (x, row tiles, requests) as the chosen order lays them out
     auto make_grid = [&](int64_t gx, int64_t gy, bool lds_form) {
         const int64_t n = gx * gy * z;
@@ -962,7 +958,7 @@ int launch_prefill(const PrefillArgs& a_in, int64_t tile_rows_total, int64_t z, 
     // (short prompts: config 1 is 96 workgroups); the LDS form, which reads each K/V tile
     // once per 64 rows instead of once per 16, when its grid fills the chip.
     int direct = lg.gx * lg.gy * z < device_cu_count();
-    if (const char* env = std::getenv("CRUCIBLE_PREFILL_DIRECT")) direct = std::atoi(env) != 0;
+    if (const int v = tuning(CRUCIBLE_TUNE_PREFILL_DIRECT); v >= 0) direct = v;
     if (direct) {
         const int64_t gy = (tile_rows_total + 15) / 16;
         CRUCIBLE_CHECK(a.n_head <= INT32_MAX && gy <= 65535 && z <= 65535, CRUCIBLE_ERR_INVALID,
@@ -982,10 +978,7 @@ int launch_prefill(const PrefillArgs& a_in, int64_t tile_rows_total, int64_t z, 
     // A grid that fits the chip at one workgroup per CU affords the deeper ring (96 KiB
     // of LDS); larger grids keep two workgroups per CU.
     int kb = (gx * gy * z <= 256) ? 6 : 4;
-    if (const char* env = std::getenv("CRUCIBLE_PREFILL_BUFS")) {
-        const int v = std::atoi(env);
-        if (v == 4 || v == 6) kb = v;
-    }
+    if (const int v = tuning(CRUCIBLE_TUNE_PREFILL_BUFS); v > 0) kb = v;
     CRUCIBLE_CHECK(gx <= INT32_MAX && gy <= 65535 && z <= 65535, CRUCIBLE_ERR_INVALID,
                    "%s: grid (%lld, %lld, %lld) too large", what, (long long)gx, (long long)gy,
                    (long long)z);

@@ -140,6 +140,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 void set_error(int status, const char* fmt, ...);
 int fail_launch(const char* what);
+// Current value of a launch-shape override (CRUCIBLE_TUNE_*), -1 for the automatic choice.
+int tuning(int key);
 // CUs of the current device (256 on MI355X), queried once per device: the launch-shape
 // choices compare grids against it.
 int device_cu_count();

@@ -42,17 +42,23 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
 
     int64_t pos;
     int64_t page;
+    // A row whose position lies outside its table (an inactive request's -1, or a position
+    // past table_stride * 16) is skipped, as the fused decode append skips it: the reference
+    // kernels would index the table out of bounds there.
     switch (a.mode) {
         case kRows:
             pos = a.positions[row];
+            if (pos < 0 || (pos >> kPageShift) >= a.table_stride) return;
             page = a.tables[row * a.table_stride + (pos >> kPageShift)];
             break;
         case kParams:
             pos = (int64_t)a.params[kParamPrefillPos] + row;
+            if (pos < 0) return;
             page = a.tables[pos >> kPageShift];
             break;
         case kPacked:
             pos = a.positions[row];
+            if (pos < 0 || (pos >> kPageShift) >= a.table_stride) return;
             page = a.tables[(int64_t)a.owners[row] * a.table_stride + (pos >> kPageShift)];
             break;
         default:

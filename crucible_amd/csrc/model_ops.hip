@@ -710,9 +710,9 @@ void launch_linear4(const LinArgs& a, hipStream_t stream) {
 // fused (the decode step's o and down projections: 5.16 -> 4.84 and 10.2 -> 8.9 us).
 // With a fused norm every workgroup loads and normalises the whole rows, and four times
 // the workgroups made it slower (qkv 6.9 -> 8.8 us, gate/up 7.4 -> 11.6 us), so those keep
-// 16 columns. CRUCIBLE_LINEAR_TILE = 4 | 16 overrides the choice.
+// 16 columns. CRUCIBLE_TUNE_LINEAR_TILE = 4 | 16 overrides the choice.
 bool use_tile4(int64_t n_out, int64_t rows, int cols16, bool norm) {
-    if (const char* env = std::getenv("CRUCIBLE_LINEAR_TILE")) return std::atoi(env) == 4;
+    if (const int v = tuning(CRUCIBLE_TUNE_LINEAR_TILE); v > 0) return v == 4;
     return !norm && ((n_out + cols16 - 1) / cols16) * ((rows + 15) / 16) < device_cu_count();
 }
 

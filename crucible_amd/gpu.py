@@ -16,6 +16,8 @@ Differences from the reference, all from the allowed page-layout change:
 """
 from __future__ import annotations
 
+import contextlib
+
 import torch
 
 from . import _lib
@@ -51,6 +53,49 @@ def _need(t, what, *, dtype=None, numel=None):
     if numel is not None and t.numel() < numel:
         raise CrucibleError(_lib.ERR_INVALID, f"{what}: {t.numel()} elements, need {numel}")
     return t
+
+
+def set_tuning(**overrides) -> None:
+    """Force launch shapes for every later launch in the process (crucible_attn_set_tuning):
+    decode_pages, decode_waves, decode_order ("split" | "request" | "compact"),
+    prefill_direct, prefill_heavy_first, prefill_qb, prefill_bufs, linear_tile,
+    decode_split_pages. None returns a key to the launcher's own choice."""
+    lib = _lib.load()
+    for name, value in overrides.items():
+        if name not in _lib.TUNE_KEYS:
+            raise CrucibleError(_lib.ERR_INVALID, f"unknown tuning key {name!r}")
+        if value is None:
+            v = -1
+        elif name == "decode_order" and isinstance(value, str):
+            v = _lib.DECODE_ORDERS[value]
+        else:
+            v = int(value)
+        _lib.check(lib.crucible_attn_set_tuning(_lib.TUNE_KEYS[name], v))
+
+
+def tuning_state() -> dict:
+    """The overrides in force, by environment-variable name (automatic keys left out)."""
+    lib = _lib.load()
+    out = {}
+    for key in _lib.TUNE_KEYS.values():
+        v = lib.crucible_attn_get_tuning(key)
+        if v != -1:
+            out[lib.crucible_attn_tuning_name(key).decode()] = v
+    return out
+
+
+@contextlib.contextmanager
+def tuning(**overrides):
+    """set_tuning for the duration of a with-block; the previous values come back after."""
+    lib = _lib.load()
+    saved = {name: lib.crucible_attn_get_tuning(key) for name, key in _lib.TUNE_KEYS.items()
+             if name in overrides}
+    try:
+        set_tuning(**overrides)
+        yield
+    finally:
+        for name, v in saved.items():
+            _lib.check(lib.crucible_attn_set_tuning(_lib.TUNE_KEYS[name], v))
 
 
 def pool_elems(n_pages: int, n_layer: int, kv_dim: int) -> int:

@@ -65,6 +65,30 @@ enum crucible_pool_kind { CRUCIBLE_POOL_K = 0, CRUCIBLE_POOL_V = 1 };
 /* Version string of this library (static storage). */
 const char* crucible_attn_version(void);
 
+/* Launch-shape overrides, for tests and tuning sweeps. Every entry point picks its
+ * kernel shape on its own; a key set to a value other than -1 forces that choice for
+ * every later launch in the process. Each key starts at the value of its environment
+ * variable (crucible_attn_tuning_name), read once per process; unset or unparsable
+ * means -1. Values that a key does not accept are rejected with CRUCIBLE_ERR_INVALID.
+ * The setting is process-wide: change it only while no other thread launches. */
+enum crucible_tuning_key {
+    CRUCIBLE_TUNE_DECODE_PAGES = 0,        /* decode pages per wave: 1, 2, 4 */
+    CRUCIBLE_TUNE_DECODE_WAVES = 1,        /* decode waves per workgroup: 4, 8 */
+    CRUCIBLE_TUNE_DECODE_ORDER = 2,        /* decode grid order: 0 split, 1 request, 2 compact */
+    CRUCIBLE_TUNE_PREFILL_DIRECT = 3,      /* prefill register-direct form: 0, 1 */
+    CRUCIBLE_TUNE_PREFILL_HEAVY_FIRST = 4, /* prefill longest-first grid: 0, 1 */
+    CRUCIBLE_TUNE_PREFILL_QB = 5,          /* prefill 16-row blocks per wave: 1, 2 */
+    CRUCIBLE_TUNE_PREFILL_BUFS = 6,        /* prefill LDS ring depth in key tiles: 4, 6 */
+    CRUCIBLE_TUNE_LINEAR_TILE = 7,         /* projection tile columns: 4, 16 */
+    CRUCIBLE_TUNE_DECODE_SPLIT_PAGES = 8,  /* pages per unit of a decode work plan: 1..16 */
+    CRUCIBLE_TUNE_COUNT = 9
+};
+int crucible_attn_set_tuning(int key, int value);
+/* Current value of a key (-1: automatic, or an unknown key). */
+int crucible_attn_get_tuning(int key);
+/* Name of a key's environment variable (static storage), NULL for an unknown key. */
+const char* crucible_attn_tuning_name(int key);
+
 /* Copy the calling thread's last error message into buf (NUL-terminated,
  * truncated to n). Returns the status of that error (CRUCIBLE_OK if none). */
 int crucible_attn_last_error(char* buf, size_t n);

@@ -27,3 +27,16 @@ def gpu(dev):
     from crucible_amd.gpu import Gpu
 
     return Gpu(0)
+
+
+@pytest.fixture
+def tune():
+    """set_tuning for one test: every key the test sets returns to its previous value."""
+    from crucible_amd import _lib
+    from crucible_amd.gpu import set_tuning
+
+    lib = _lib.load()
+    saved = {name: lib.crucible_attn_get_tuning(key) for name, key in _lib.TUNE_KEYS.items()}
+    yield set_tuning
+    for name, key in _lib.TUNE_KEYS.items():
+        _lib.check(lib.crucible_attn_set_tuning(key, saved[name]))

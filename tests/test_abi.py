@@ -148,3 +148,28 @@ def test_qkv_decode_entry_validates_before_launch():
     assert call(cos=None) == _lib.ERR_INVALID             # cos without sin
     assert call(max_pos=1024) == _lib.ERR_INVALID         # tables shorter than max_seq
     assert call(ws_bytes=16) == _lib.ERR_WORKSPACE        # split-K workspace too small
+
+
+def test_tuning_overrides_are_validated_and_restorable():
+    """Launch-shape overrides: every key has its environment name, accepts only its
+    documented values, and reads back what was set (no GPU involved)."""
+    from crucible_amd.gpu import set_tuning, tuning, tuning_state
+
+    lib = _lib.load()
+    names = [lib.crucible_attn_tuning_name(k).decode() for k in _lib.TUNE_KEYS.values()]
+    assert all(n.startswith("CRUCIBLE_") for n in names) and len(set(names)) == len(names)
+    assert lib.crucible_attn_tuning_name(len(_lib.TUNE_KEYS)) is None
+    key = _lib.TUNE_KEYS["decode_waves"]
+    before = lib.crucible_attn_get_tuning(key)
+    assert lib.crucible_attn_set_tuning(key, 5) == _lib.ERR_INVALID
+    assert "does not take 5" in _lib.last_error()[1]
+    assert lib.crucible_attn_get_tuning(key) == before
+    with tuning(decode_waves=4, decode_order="split"):
+        assert lib.crucible_attn_get_tuning(key) == 4
+        state = tuning_state()
+        assert state["CRUCIBLE_DECODE_WAVES"] == 4 and state["CRUCIBLE_DECODE_ORDER"] == 0
+    assert lib.crucible_attn_get_tuning(key) == before
+    with pytest.raises(_lib.CrucibleError):
+        set_tuning(prefill_bufs=5)
+    with pytest.raises(_lib.CrucibleError):
+        set_tuning(no_such_key=1)

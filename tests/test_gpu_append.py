@@ -167,3 +167,39 @@ def test_full_size_decode_append_config3(gpu, dev):
         assert torch.equal(got, srcs[layer].to(torch.float16))
         total += float(got.float().abs().sum())
     assert abs(float(pool.float().abs().sum()) - total) < 1e-3 * max(total, 1.0)
+
+
+@pytest.mark.parametrize("kind", ["k", "v"])
+def test_rows_outside_the_table_are_skipped(gpu, dev, kind):
+    """An inactive row (position -1) and a row past its table's capacity (position
+    table_stride * 16) write nothing, in the rows and packed forms, as in the fused decode
+    append; the other rows land exactly where the oracle puts them."""
+    rng = np.random.default_rng(41 + (kind == "v"))
+    kv, n_pages, stride, rows = 192, 64, 4, 6
+    lens = rng.integers(1, stride * 16, rows)
+    tables = disjoint_tables(rng, n_pages, lens, stride)
+    positions = (lens - 1).astype(np.int32)
+    positions[1] = -1
+    positions[4] = stride * 16
+    valid = [r for r in range(rows) if r not in (1, 4)]
+    src = _src(rng, rows, kv, "f32")
+    k = oracle.POOL_K if kind == "k" else oracle.POOL_V
+    pool = np.full(n_pages * N_LAYER * 16 * kv, 0x7E00, np.uint16)
+    want = pool.copy()
+    oracle.cache_store(oracle.STORE_ROWS, k, want, np.ascontiguousarray(src[valid]),
+                       tables=np.ascontiguousarray(tables[valid]),
+                       positions=np.ascontiguousarray(positions[valid]), rows=len(valid),
+                       kv_dim=kv, table_stride=stride, n_layer=N_LAYER, layer=LAYER)
+    d_pool = _dev(pool, dev)
+    gpu.cache_store_rows_paged(_dev(src, dev), d_pool, _dev(tables, dev), _dev(positions, dev),
+                               rows, kv, stride, N_LAYER, LAYER, kind=kind)
+    torch.cuda.synchronize()
+    assert np.array_equal(_host_bits(d_pool), want)
+    # packed form: owners name the table rows
+    owners = np.arange(rows, dtype=np.int32)
+    d_pool = _dev(pool, dev)
+    gpu.cache_store_packed_paged(_dev(src, dev), d_pool, _dev(tables, dev), _dev(owners, dev),
+                                 _dev(positions, dev), rows, kv, stride, N_LAYER, LAYER,
+                                 kind=kind)
+    torch.cuda.synchronize()
+    assert np.array_equal(_host_bits(d_pool), want)

@@ -12,7 +12,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = 2e-3  # max-abs 2e-3 against the fp32 reference
 SENTINEL = -12345.25
-ORDERS = ["split", "request", "compact"]  # CRUCIBLE_DECODE_ORDER values
+ORDERS = ["split", "request", "compact"]  # decode_order tuning values
 
 
 def _dev(a, dev):
@@ -289,11 +289,11 @@ def test_fused_append_decode_equals_separate_calls(gpu, dev, n_head, n_kv, kv_dt
 
 
 @pytest.mark.parametrize("order", ORDERS)
-def test_fused_append_off_the_last_slot_and_inactive_rows(gpu, dev, monkeypatch, order):
+def test_fused_append_off_the_last_slot_and_inactive_rows(gpu, dev, tune, order):
     """Rows appended inside the attended range, past it (a later page, and a later split:
     a unit of its own in the compact order), and for inactive requests (len 0) give the
     same pools and outputs as the separate calls."""
-    monkeypatch.setenv("CRUCIBLE_DECODE_ORDER", order)
+    tune(decode_order=order)
     lens = [40, 40, 0, 300, 17, 129, 0]
     positions = [20, 100, 5, 299, 16, 128, 700]
     for rep in range(3):  # repeated launches reuse the workspace counters
@@ -306,17 +306,16 @@ def test_fused_append_off_the_last_slot_and_inactive_rows(gpu, dev, monkeypatch,
 
 
 @pytest.mark.parametrize("order", ORDERS)
-def test_decode_shapes_agree(gpu, dev, monkeypatch, order):
+def test_decode_shapes_agree(gpu, dev, tune, order):
     """Every split shape (pages per wave x waves per workgroup) gives the oracle's answer,
     with the fused and plain entries, on lengths that exercise 1..many splits, in every
     grid order (split-major, request-major, and the compact list of units with work)."""
     lens = [3, 64, 65, 500, 1023, 2048, 1500, 16]
     positions = [n - 1 for n in lens]
-    monkeypatch.setenv("CRUCIBLE_DECODE_ORDER", order)
+    tune(decode_order=order)
     for pages in ("1", "2", "4"):
         for waves in ("4", "8"):
-            monkeypatch.setenv("CRUCIBLE_DECODE_PAGES", pages)
-            monkeypatch.setenv("CRUCIBLE_DECODE_WAVES", waves)
+            tune(decode_pages=pages, decode_waves=waves)
             k2, v2, k1, v1, o2, o1, q, tables = _fused_vs_separate(
                 gpu, dev, lens, positions, 12, 3, seed=int(pages) * 10 + int(waves))
             assert np.array_equal(k2, k1) and np.array_equal(v2, v1)
@@ -325,14 +324,14 @@ def test_decode_shapes_agree(gpu, dev, monkeypatch, order):
             assert np.abs(o2 - want).max() <= TOL, (pages, waves)
 
 
-def test_grid_orders_are_bit_identical(gpu, dev, monkeypatch):
+def test_grid_orders_are_bit_identical(gpu, dev, tune):
     """The grid order only places the workgroups: splits merge in split order whatever
     order they finish in, so every order gives the same bits."""
     lens = [1, 17, 256, 257, 700, 2048, 1999, 64, 0, 1024]
     positions = [max(n - 1, 0) for n in lens]
     outs = []
     for order in ORDERS:
-        monkeypatch.setenv("CRUCIBLE_DECODE_ORDER", order)
+        tune(decode_order=order)
         _, _, _, _, o2, o1, _, _ = _fused_vs_separate(gpu, dev, lens, positions, 12, 3, seed=5)
         assert np.array_equal(o2.view(np.uint32), o1.view(np.uint32))
         outs.append(o2.view(np.uint32))

@@ -41,7 +41,7 @@ def _mat(rng, shape, std):
     return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float16)
 
 
-TILES = ["auto", "4", "16"]  # CRUCIBLE_LINEAR_TILE: the launcher's choice, or forced
+TILES = ["auto", "4", "16"]  # linear_tile tuning: the launcher's choice, or forced
 
 
 @pytest.mark.parametrize("rows,n_out,k_in", [(1, 1152, 768), (16, 768, 768), (5, 200, 2048),
@@ -50,11 +50,11 @@ TILES = ["auto", "4", "16"]  # CRUCIBLE_LINEAR_TILE: the launcher's choice, or f
                                              (7, 203, 160)])
 @pytest.mark.parametrize("norm", [False, True])
 @pytest.mark.parametrize("tile", TILES)
-def test_linear_matches_f64_matvec(gpu, dev, monkeypatch, rows, n_out, k_in, norm, tile):
+def test_linear_matches_f64_matvec(gpu, dev, tune, rows, n_out, k_in, norm, tile):
     if tile != "auto":
         if n_out >= 16 * 1024:
             pytest.skip("the vocabulary-sized outputs take the persistent wide kernel")
-        monkeypatch.setenv("CRUCIBLE_LINEAR_TILE", tile)
+        tune(linear_tile=tile)
     rng = np.random.default_rng(rows * 7 + n_out + k_in + norm)
     x = rng.standard_normal((rows, k_in), dtype=np.float32)
     w = _mat(rng, (n_out, k_in), 0.02)
@@ -73,9 +73,9 @@ def test_linear_matches_f64_matvec(gpu, dev, monkeypatch, rows, n_out, k_in, nor
 
 
 @pytest.mark.parametrize("tile", TILES)
-def test_linear_residual_in_place(gpu, dev, monkeypatch, tile):
+def test_linear_residual_in_place(gpu, dev, tune, tile):
     if tile != "auto":
-        monkeypatch.setenv("CRUCIBLE_LINEAR_TILE", tile)
+        tune(linear_tile=tile)
     rng = np.random.default_rng(5)
     rows, n_out, k_in = 16, 768, 2048
     a = rng.standard_normal((rows, k_in), dtype=np.float32)
@@ -93,9 +93,9 @@ def test_linear_residual_in_place(gpu, dev, monkeypatch, tile):
 
 @pytest.mark.parametrize("rows,hidden,k_in", [(16, 2048, 768), (5, 2045, 96), (21, 130, 1056)])
 @pytest.mark.parametrize("tile", TILES)
-def test_swiglu_matches_reference_ops(gpu, dev, monkeypatch, rows, hidden, k_in, tile):
+def test_swiglu_matches_reference_ops(gpu, dev, tune, rows, hidden, k_in, tile):
     if tile != "auto":
-        monkeypatch.setenv("CRUCIBLE_LINEAR_TILE", tile)
+        tune(linear_tile=tile)
     rng = np.random.default_rng(9 + hidden)
     x = rng.standard_normal((rows, k_in), dtype=np.float32)
     wg = _mat(rng, (hidden, k_in), 0.05)

@@ -22,10 +22,10 @@ TOL = 2e-3
 
 
 @pytest.fixture(autouse=True, params=["lds", "direct"])
-def prefill_form(request, monkeypatch):
+def prefill_form(request, tune):
     """Every test runs through both prefill kernels: the LDS-tiled form and the
-    register-direct form (the library picks one by grid size; the variable forces it)."""
-    monkeypatch.setenv("CRUCIBLE_PREFILL_DIRECT", "1" if request.param == "direct" else "0")
+    register-direct form (the library picks one by grid size; the override forces it)."""
+    tune(prefill_direct=1 if request.param == "direct" else 0)
     return request.param
 
 
@@ -121,7 +121,7 @@ def test_repeated_launches_are_bit_identical(gpu, dev):
             assert np.array_equal(d.result().view(np.uint32), first.view(np.uint32)), case.name
 
 
-def test_grid_orders_are_bit_identical(gpu, dev, monkeypatch):
+def test_grid_orders_are_bit_identical(gpu, dev, tune):
     """The longest-first grid (the last row tiles of every request dispatched first, the
     default) and the plain (x, row tile, request) grid only place the workgroups: the
     outputs are the same bits."""
@@ -129,7 +129,7 @@ def test_grid_orders_are_bit_identical(gpu, dev, monkeypatch):
         fx = A.fixture(case)
         outs = []
         for order in ("1", "0"):
-            monkeypatch.setenv("CRUCIBLE_PREFILL_HEAVY_FIRST", order)
+            tune(prefill_heavy_first=order)
             for runner in (run_segments, run_owners):
                 d = Device(fx, dev)
                 runner(gpu, d)

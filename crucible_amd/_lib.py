@@ -42,6 +42,7 @@ SIGNATURES = {
     "crucible_attention_decode_workspace_bytes": ([_I64, _I64, _I64], _SZ),
     "crucible_attention_decode_paged": ([_P, _I, _P, _P, _P, _I, _P, _P] + [_I64] * 9 + [_P, _SZ, _P], _I),
     "crucible_attention_decode_paged_append": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P] + [_I64] * 9 + [_P, _SZ, _P], _I),
+    "crucible_attention_decode_paged_append_noalloc": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P] + [_I64] * 9 + [_P], _I),
     "crucible_attention_decode_qkv_paged_append": ([_P, _I64, _P, _P, _I64, _P, _P, _P, _I, _P, _P, _P] + [_I64] * 9 + [_P, _SZ, _P], _I),
     "crucible_attention_decode": ([_P, _I, _P, _P, _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _SZ, _P], _I),
     "crucible_attention_split": ([_P, _I, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P], _I),

@@ -43,6 +43,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 namespace crucible {
 namespace {
@@ -886,6 +887,64 @@ int decode_with_workspace(DecodeArgs& a, bool q_f32, void* workspace, size_t wor
     return launch_decode(a, sh, q_f32, stream, what);
 }
 
+// ---------------------------------------------------------------- allocation-free form
+// For callers that cannot allocate (code under graph capture, serving loops, harnesses that
+// forbid hipMalloc): the split-K scratch of crucible_attention_decode_paged_append_noalloc
+// lives in this file-scope device array, one copy per GPU, held until the process ends.
+// Its first kScratchCounters u32 are the combine counters (zero at load, cleared again by
+// a fill kernel at set-up, and left zero by every launch); the partials follow. Host code
+// never passes `scratch` itself to a kernel: in host code the name is only a stand-in, so
+// the device address comes from hipGetSymbolAddress, once per device.
+constexpr size_t kScratchBytes = size_t(4) << 20;
+constexpr int64_t kScratchCounters = 8192;
+constexpr size_t kScratchCounterBytes = kScratchCounters * sizeof(uint32_t);
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+__global__ __launch_bounds__(256) void clear_counters_kernel(uint32_t* c, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) c[i] = 0u;
+}
+
+constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+    std::once_flag once;
+    void* ptr = nullptr;
+    hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+// The device address of this GPU's `scratch`, looked up (and its counters cleared on
+// `stream`) the first time a device is used; nullptr with the error message set on failure.
+void* scratch_ptr(hipStream_t stream, const char* what) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        set_error(CRUCIBLE_ERR_LAUNCH, "%s: no current device (or more than %d)", what,
+                  kMaxDevices);
+        return nullptr;
+    }
+    ScratchSlot& slot = g_scratch[dev];
+    std::call_once(slot.once, [&] {
+        void* p = nullptr;
+        slot.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (slot.err != hipSuccess) {
+            (void)hipGetLastError();
+            return;
+        }
+        hipLaunchKernelGGL(clear_counters_kernel, dim3((kScratchCounters + 255) / 256),
+                           dim3(256), 0, stream, static_cast<uint32_t*>(p),
+                           (int)kScratchCounters);
+        slot.err = hipGetLastError();
+        if (slot.err == hipSuccess) slot.ptr = p;
+    });
+    if (!slot.ptr) {
+        set_error(CRUCIBLE_ERR_LAUNCH, "%s: device scratch unavailable on device %d: %s", what,
+                  dev, hipGetErrorString(slot.err));
+        return nullptr;
+    }
+    return slot.ptr;
+}
+
 }  // namespace
 }  // namespace crucible
 
@@ -973,6 +1032,76 @@ extern "C" int crucible_attention_decode_paged_append(
     a.table_stride = (int32_t)table_stride;
     return decode_with_workspace(a, q_dtype == CRUCIBLE_F32, workspace, workspace_bytes, stream,
                                  what);
+}
+
+extern "C" int crucible_attention_decode_paged_append_noalloc(
+    const void* q, int q_dtype, const void* k_new, const void* v_new, int kv_dtype,
+    void* k_pool, void* v_pool, void* out, int out_dtype, const int32_t* page_tables,
+    const int32_t* positions, const int32_t* seq_lens, int64_t batch, int64_t n_head,
+    int64_t n_kv_head, int64_t head_dim, int64_t table_stride, int64_t n_layer, int64_t layer,
+    int64_t kv_dim, int64_t max_seq, crucible_stream_t stream) {
+    const char* what = "attention_decode_paged_append_noalloc";
+    CRUCIBLE_CHECK(dtype_ok(q_dtype) && dtype_ok(out_dtype) && dtype_ok(kv_dtype),
+                   CRUCIBLE_ERR_INVALID, "%s: bad dtype", what);
+    if (int rc = check_geometry(what, n_head, n_kv_head, head_dim, kv_dim)) return rc;
+    CRUCIBLE_CHECK(batch >= 0 && batch <= INT32_MAX, CRUCIBLE_ERR_INVALID, "%s: batch %lld",
+                   what, (long long)batch);
+    if (batch == 0) return CRUCIBLE_OK;
+    CRUCIBLE_CHECK(q && k_new && v_new && k_pool && v_pool && out && page_tables && positions &&
+                       seq_lens,
+                   CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
+    CRUCIBLE_CHECK(n_layer > 0 && layer >= 0 && layer < n_layer, CRUCIBLE_ERR_INVALID,
+                   "%s: layer %lld outside n_layer %lld", what, (long long)layer,
+                   (long long)n_layer);
+    CRUCIBLE_CHECK(table_stride > 0 && table_stride <= INT32_MAX && max_seq > 0 &&
+                       max_seq <= table_stride * kPageTokens && max_seq <= INT32_MAX,
+                   CRUCIBLE_ERR_INVALID, "%s: max_seq %lld must be in 1..table_stride*16", what,
+                   (long long)max_seq);
+    DecodeArgs a = common_args(q, k_pool, v_pool, out, out_dtype, batch, n_head, n_kv_head,
+                               max_seq);
+    a.tables = page_tables;
+    a.lens = seq_lens;
+    a.lens_stride = 1;
+    a.positions = positions;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.kv_new_f16 = kv_dtype == CRUCIBLE_F16;
+    a.kv_new_stride = (int32_t)kv_dim;
+    a.addr.kv_dim = (int32_t)kv_dim;
+    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
+    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    a.table_stride = (int32_t)table_stride;
+    CRUCIBLE_CHECK(aligned16(a.q) && aligned16(a.k_pool) && aligned16(a.v_pool) &&
+                       aligned16(a.out) && aligned16(a.k_new) && aligned16(a.v_new),
+                   CRUCIBLE_ERR_INVALID, "%s: q, pools, out and new rows must be 16-byte aligned",
+                   what);
+    const DecodeShape sh = decode_shape(a.batch, a.n_kv_head, a.max_pages);
+    const int split_pages = sh.pages * sh.waves;
+    a.split_shift = __builtin_ctz((unsigned)split_pages);
+    a.n_splits = (a.max_pages + split_pages - 1) / split_pages;
+    if (a.n_splits > 1) {
+        // the limits of the static scratch: counters and partials
+        const size_t partial_bytes = partial_floats(a.batch, a.n_head, a.n_splits) * sizeof(float);
+        CRUCIBLE_CHECK((int64_t)a.batch * a.n_kv_head <= kScratchCounters &&
+                           partial_bytes <= kScratchBytes - kScratchCounterBytes,
+                       CRUCIBLE_ERR_WORKSPACE,
+                       "%s: batch %lld x %lld kv heads at max_seq %lld needs %zu bytes of split "
+                       "partials and %lld counters; the static scratch holds %zu bytes and %lld "
+                       "counters (use crucible_attention_decode_paged_append with a workspace)",
+                       what, (long long)batch, (long long)n_kv_head, (long long)max_seq,
+                       partial_bytes, (long long)a.batch * a.n_kv_head,
+                       kScratchBytes - kScratchCounterBytes, (long long)kScratchCounters);
+        void* ptr = scratch_ptr(stream, what);
+        if (!ptr) return CRUCIBLE_ERR_LAUNCH;
+        a.counters = static_cast<uint32_t*>(ptr);
+        float* f = reinterpret_cast<float*>(static_cast<char*>(ptr) + kScratchCounterBytes);
+        const size_t n = (size_t)a.batch * a.n_head * a.n_splits;
+        a.po = f;
+        a.pm = f + n * kHeadDim;
+        a.pl = a.pm + n;
+        a.po_bytes = (uint32_t)(n * kHeadDim * sizeof(float));
+    }
+    return launch_decode(a, sh, q_dtype == CRUCIBLE_F32, stream, what);
 }
 
 extern "C" int crucible_attention_decode_qkv_paged_append(

@@ -171,6 +171,26 @@ int crucible_attention_decode_paged_append(
     int64_t kv_dim, int64_t max_seq, void* workspace, size_t workspace_bytes,
     crucible_stream_t stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory
+ * (code under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * crucible_attention_decode_paged_append with the split-K scratch taken from a
+ * file-scope device array of this library (4 MiB per GPU, held until the process ends)
+ * instead of a workspace argument. Same kernels, same results bit for bit. Limits:
+ * batch * n_kv_head <= 8192, and batch * n_head * n_splits * 66 * 4 bytes of partials
+ * <= 4 MiB - 32 KiB, where n_splits = ceil(ceil(max_seq / 16) / split pages) and a split
+ * is 8, 16 or 32 pages (b16 x 12 heads fits up to max_seq 65536 tokens); larger calls
+ * return CRUCIBLE_ERR_WORKSPACE before any launch. It calls no hipMalloc or hipFree;
+ * the first call on a device looks up the array's address and clears its counters with
+ * a small kernel on `stream`. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (several streams, or threads) race and must be ordered by the
+ * caller. */
+int crucible_attention_decode_paged_append_noalloc(
+    const void* q, int q_dtype, const void* k_new, const void* v_new, int kv_dtype,
+    void* k_pool, void* v_pool, void* out, int out_dtype, const int32_t* page_tables,
+    const int32_t* positions, const int32_t* seq_lens, int64_t batch, int64_t n_head,
+    int64_t n_kv_head, int64_t head_dim, int64_t table_stride, int64_t n_layer, int64_t layer,
+    int64_t kv_dim, int64_t max_seq, crucible_stream_t stream);
+
 /* The same fused step fed straight from the fused q/k/v projection, with the RoPE of
  * the reference's decode step (rope_rows before the K append and on q, gpu_model.rs:1424-1444;
  * RopeTable::apply, ops.rs:124-135) applied in the same launch (§8f rank 2). Row b of qkv

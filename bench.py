@@ -56,7 +56,8 @@ def parse_args():
                         "distribution, and prefill of 2k..8k-token sequences; not in the "
                         "default set), pscale (only the prefill part of scale)")
     p.add_argument("--copy-probe", action="store_true",
-                   help="also run a plain 256 MiB device copy (PMC traffic calibration)")
+                   help="also run 5 more plain 256 MiB device copies (PMC traffic calibration)")
+
     return p.parse_args()
 
 
@@ -206,7 +207,8 @@ class DecodeBench:
 def pmc_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
     (profiles/decode_b16_gqa3_pmc_traffic.txt: FETCH_SIZE and WRITE_SIZE runs scaled by a
-    copy kernel of known size), or None when the summary is for another kernel."""
+    copy kernel of known size), or None unless the summary is for this very kernel built
+    from these very sources (its kernel and source_sha lines)."""
     path = os.path.join(ROOT, "profiles", "decode_b16_gqa3_pmc_traffic.txt")
     try:
         fields = dict(line.split(": ", 1) for line in open(path).read().splitlines()
@@ -214,6 +216,8 @@ def pmc_traffic(kernel: str):
     except OSError:
         return None
     if fields.get("kernel", "").strip() != kernel:
+        return None
+    if fields.get("source_sha", "").strip() != source_sha():
         return None
     return int(fields["traffic_bytes_per_launch"])
 
@@ -229,7 +233,17 @@ def flush_llc(dev):
 
 # ---------------------------------------------------------------- prefill workloads
 
-def bench_prefill(gpu, dev, cfg, launches: int = 50, q_dtype=None):
+def gather_rows(pool, table_row, n, n_layer, layer, kv_dim, v_kind):
+    """Rows [0, n) of one sequence from a device pool, reference element order [n][kv_dim]
+    (V blocks are stored transposed)."""
+    n_pages = -(-n // 16)
+    blocks = pool.view(-1, n_layer, 16 * kv_dim)[table_row[:n_pages].long(), layer]
+    if v_kind:
+        blocks = blocks.view(n_pages, kv_dim, 16).transpose(1, 2)
+    return blocks.reshape(n_pages * 16, kv_dim)[:n]
+
+
+def bench_prefill(gpu, dev, cfg, launches: int = 50, q_dtype=None, cpu_inputs=None):
     """Time the segment-form prefill kernel (gpu.rs:1606-1751 path) on config 1 or 4:
     `launches` back-to-back launches replayed from one HIP graph (us_per_launch, the
     figure TFLOP/s uses, timed like the decode step), and eager launches each bracketed by
@@ -294,6 +308,13 @@ def bench_prefill(gpu, dev, cfg, launches: int = 50, q_dtype=None):
     avg = e0.elapsed_time(e1) / (4 * launches)
     del g
     tflops = cfg.flops() / (avg * 1e-3) / 1e12
+    if cpu_inputs is not None:  # the rows this run used, for the CPU baseline beside it
+        ks, vs = [], []
+        for i, n in enumerate(cfg.seq_lens):
+            ks.append(gather_rows(k_pool, d_tab[i], int(n), 1, 0, kv_dim, False))
+            vs.append(gather_rows(v_pool, d_tab[i], int(n), 1, 0, kv_dim, True))
+        cpu_inputs.update(q=q.float().cpu().numpy(), k=torch.cat(ks).float().cpu().numpy(),
+                          v=torch.cat(vs).float().cpu().numpy())
     return {"workload": cfg.name, "n_head": cfg.n_head, "n_kv_head": cfg.n_kv_head,
             "q_dtype": str(q.dtype).replace("torch.", ""),
             "seq_lens": [int(x) for x in cfg.seq_lens], "flops": cfg.flops(),
@@ -332,45 +353,119 @@ def bench_e2e(gpu, reps: int = 2):
 
 # ---------------------------------------------------------------- CPU baseline
 
-def cpu_prefill(cfg, seconds: float):
+def cpu_prefill(cfg, inputs, seconds: float):
     """The reference CPU attention for a prefill config (one SDPA(is_causal) per sequence,
-    fp32), bounded to about `seconds`: GFLOP/s on the config's visible-pair FLOPs."""
+    fp32) on the same rows the GPU run used: GFLOP/s on the config's visible-pair FLOPs."""
     from oracle import cpu_path
 
     cores = cpu_path.threads()
-    cpu = cpu_path.PrefillCPU(cfg.seq_lens, cfg.n_head, cfg.n_kv_head, seed=3)
-    reps, s_per = cpu_path.time_bounded(cpu.step, seconds)
+    cpu = cpu_path.PrefillCPU(cfg.seq_lens, cfg.n_head, cfg.n_kv_head, inputs["q"],
+                              inputs["k"], inputs["v"])
+    reps, s_per = cpu_path.time_median(cpu.step, seconds)
     return {"ms": round(s_per * 1e3, 3), "gflops": round(cfg.flops() / s_per / 1e9, 2),
-            "cores": cores, "kind": "port", "sample": f"{reps} full launches of the config, torch "
-            "SDPA fp32 per sequence"}
+            "cores": cores, "kind": "port", "cpu_model": cpu_path.cpu_model(),
+            "sample": f"median of {reps} full launches after 5 warmups, torch SDPA fp32 per "
+                      "sequence on the GPU run's rows"}
 
 
-def cpu_decode_b1(seconds: float):
-    """Config 2 on the CPU: one 12-layer step of batch 1 at 1024 keys (gather + SDPA + the
-    row append), per-layer microseconds."""
+def decode_cpu_inputs(bench, r: int = 0):
+    """Host copies of what rotation r of a decode bench reads: its pages (compacted, K and V
+    in reference element order), remapped tables, queries and appended rows."""
+    import numpy as np
+    import torch
+
+    lens = bench.lens[r]
+    tab = bench.tables[r]
+    pages = [-(-int(n) // 16) for n in lens]
+    used = np.concatenate([tab[b, :n] for b, n in enumerate(pages)])
+    blk = bench.n_layer * 16 * bench.kv_dim
+    idx = torch.from_numpy(used.astype(np.int64)).to(bench.dev)
+    k = bench.k_pool.view(-1, blk)[idx].view(-1, bench.n_layer, 16, bench.kv_dim)
+    v = bench.v_pool.view(-1, blk)[idx].view(-1, bench.n_layer, bench.kv_dim, 16).transpose(2, 3)
+    compact = []
+    cur = 0
+    for n in pages:
+        compact.append(np.arange(cur, cur + n))
+        cur += n
+    return dict(k_pages=k.contiguous().cpu().numpy(), v_pages=v.contiguous().cpu().numpy(),
+                tables=compact, q=bench.q.cpu().numpy(), src_k=bench.src_k.cpu().numpy(),
+                src_v=bench.src_v.cpu().numpy())
+
+
+def cpu_decode(bench, seconds: float, r: int = 0):
+    """A decode bench's step on the CPU (per layer and sequence: the row append, the page
+    gather and torch SDPA, fp32), on the same bytes as the GPU run's rotation r."""
     from oracle import cpu_path
 
     cores = cpu_path.threads()
-    cpu = cpu_path.DecodeBatchCPU([1024], 12, 12, 3, seed=2)
-    reps, s_per = cpu_path.time_bounded(cpu.step, seconds)
-    return {"us_per_layer": round(s_per * 1e6 / 12, 2), "cores": cores, "kind": "port",
-            "sample": f"{reps} 12-layer steps"}
+    lens = bench.lens[r]
+    cpu = cpu_path.DecodeBatchCPU(lens, bench.n_layer, bench.n_head, bench.n_kv,
+                                  **decode_cpu_inputs(bench, r))
+    reps, s_per_step = cpu_path.time_median(cpu.step, seconds)
+    return reps, s_per_step, cores, cpu_path.cpu_model()
 
 
-def cpu_baseline(bench: DecodeBench, seconds: float):
-    from oracle import cpu_path
+def cpu_baseline(bench, seconds: float):
+    import torch
 
-    cores = cpu_path.threads()
+    reps, s_per_step, cores, model = cpu_decode(bench, seconds)
     lens = bench.lens[0]
-    cpu = cpu_path.DecodeBatchCPU(lens, bench.n_layer, bench.n_head, bench.n_kv, seed=1)
-    reps, s_per_step = cpu_path.time_bounded(cpu.step, seconds)
     gbs = bench.step_bytes(0) / s_per_step / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "ms_per_step": round(s_per_step * 1e3, 3),
-            "sample": (f"{reps} full {bench.n_layer}-layer decode steps of batch 0 "
-                       f"(16 sequences, lens {int(lens.min())}..{int(lens.max())}): per layer "
-                       f"and sequence a row append, a page gather and torch SDPA, fp32, "
-                       f"torch {__import__('torch').__version__}")}
+            "cpu_model": model, "ms_per_step": round(s_per_step * 1e3, 3),
+            "sample": (f"median of {reps} full {bench.n_layer}-layer decode steps of batch 0 "
+                       f"after 5 warmups (16 sequences, lens {int(lens.min())}..{int(lens.max())}, "
+                       f"the GPU run's own pages, queries and rows): per layer and sequence a row "
+                       f"append, a page gather and torch SDPA, fp32, torch {torch.__version__}")}
+
+
+def copy_bandwidth(dev, mib: int = 256, reps: int = 10):
+    """Device-to-device copy of `mib` MiB (HIP's copy kernel), GB/s counting the bytes read
+    and written: the measured ceiling beside the 8 TB/s spec."""
+    import torch
+
+    src = torch.ones(mib << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    stream = torch.cuda.current_stream(dev)
+    e0.record(stream)
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    ms = e0.elapsed_time(e1) / reps
+    del src, dst
+    return 2 * (mib << 20) / (ms * 1e-3) / 1e9
+
+
+def source_sha() -> str:
+    """Hash of the library sources (csrc and the C header): a profile summary applies to the
+    kernels built from exactly these."""
+    import hashlib
+
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "crucible_amd", "csrc")
+    for name in sorted(os.listdir(csrc)):
+        with open(os.path.join(csrc, name), "rb") as f:
+            h.update(name.encode() + b"\0" + f.read())
+    with open(os.path.join(ROOT, "include", "crucible_attn.h"), "rb") as f:
+        h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def decode_kernel_name(gpu, batch, n_head, n_kv, max_seq, entry) -> str:
+    """The kernel the library launches for this decode call (its own launch choices)."""
+    import ctypes
+
+    from crucible_amd import _lib
+
+    buf = ctypes.create_string_buffer(128)
+    _lib.check(gpu.lib.crucible_attention_decode_kernel_name(batch, n_head, n_kv, max_seq,
+                                                             _lib.F16, entry, buf, 128))
+    return buf.value.decode()
 
 
 # ---------------------------------------------------------------- main
@@ -386,7 +481,7 @@ def main():
     import torch
 
     from crucible_amd import workloads as W
-    from crucible_amd.gpu import Gpu
+    from crucible_amd.gpu import Gpu, tuning_state
 
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
@@ -402,11 +497,11 @@ def main():
     b16 = DecodeBench(gpu, dev, batch=16, n_head=12, n_kv_head=args.kv_heads, n_layer=12,
                       n_pages=8192, max_seq=2048, rotations=7, seed=W.BASE_SEED + 2)
     log(f"config 3: {b16.rotations} rotations, lens of rotation 0: {b16.lens[0].tolist()}")
-    fused_graphs = b16.capture("fused")
+    step_graphs = b16.capture("fused")
     log("graphs captured")
 
     # headline: the whole step (12 fused append + decode launches), timed steps
-    ms_per_step, ev_ms_per_step, step_bytes = b16.time_steps(fused_graphs, args.steps,
+    ms_per_step, ev_ms_per_step, step_bytes = b16.time_steps(step_graphs, args.steps,
                                                              args.warmup)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"timed {args.steps} steps: {ms_per_step:.4f} ms/step (events {ev_ms_per_step:.4f}), "
@@ -419,15 +514,20 @@ def main():
     bytes_per_launch = step_bytes / b16.n_layer
     achieved = bytes_per_launch / (launch_us * 1e-6) / 1e9
     log(f"fused decode launch: {launch_us:.2f} us avg, {achieved:.1f} GB/s")
-    kernel = "decode_kernel<2, 8, false, true, true, 2, false, 8>"
+    kernel = decode_kernel_name(gpu, 16, 12, args.kv_heads, 2048, 1)
+    copy_gbs = copy_bandwidth(dev)
+    log(f"device copy: {copy_gbs:.1f} GB/s (read + write)")
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": pmc_traffic(kernel),
-                "kernel": kernel + " (append + split-K attention + combine, one launch "
-                                   "per layer)",
+                "kernel": kernel,
+                "kernel_role": "append + split-K attention + combine, one launch per layer",
                 "us_per_launch": round(launch_us, 3),
-                "algorithmic_bytes_per_launch": int(bytes_per_launch)}
-    del fused_graphs
+                "algorithmic_bytes_per_launch": int(bytes_per_launch),
+                "copy_gbs": round(copy_gbs, 1),
+                "frac_of_copy": round(achieved / copy_gbs, 4),
+                "source_sha": source_sha()}
+    del step_graphs
 
     extras = {}
     groups = set() if args.no_extras else {g.strip() for g in args.extras.split(",")}
@@ -451,6 +551,12 @@ def main():
         extras["decode_b1_ctx1024"] = {"us_per_launch": round(ev * 1e3 / 12, 3),
                                        "gbs": round(by1 / (ev * 1e-3 / 12) / 1e9, 2),
                                        "bytes_per_launch": int(by1)}
+        if not args.no_cpu_baseline:
+            reps, s_step, cores, model = cpu_decode(b1, 2.0)
+            extras["decode_b1_ctx1024"]["cpu"] = {
+                "us_per_layer": round(s_step * 1e6 / 12, 2), "cores": cores, "kind": "port",
+                "cpu_model": model,
+                "sample": f"median of {reps} 12-layer steps after 5 warmups, the GPU run's bytes"}
         del graphs, b1
         if args.kv_heads != 12:
             mha = DecodeBench(gpu, dev, batch=16, n_head=12, n_kv_head=12, n_layer=12,
@@ -494,9 +600,13 @@ def main():
             torch.cuda.empty_cache()
         extras["prefill_scale"] = pscale
     if "prefill" in groups:
-        extras["prefill_config1"] = bench_prefill(gpu, dev, W.config1_prefill(n_kv_head=12))
-        extras["prefill_config1_gqa3"] = bench_prefill(gpu, dev, W.config1_prefill(n_kv_head=3))
-        extras["packed_config4"] = bench_prefill(gpu, dev, W.config4_packed())
+        for key, cfg in (("prefill_config1", W.config1_prefill(n_kv_head=12)),
+                         ("prefill_config1_gqa3", W.config1_prefill(n_kv_head=3)),
+                         ("packed_config4", W.config4_packed())):
+            inputs = {} if not args.no_cpu_baseline else None
+            extras[key] = bench_prefill(gpu, dev, cfg, cpu_inputs=inputs)
+            if inputs:
+                extras[key]["cpu"] = cpu_prefill(cfg, inputs, 2.0)
         torch.cuda.empty_cache()
     if "e2e" in groups:
         extras["e2e_config5"] = bench_e2e(gpu)
@@ -515,13 +625,6 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(b16, args.cpu_seconds)
         log(f"cpu baseline: {cpu}")
-        # the reference CPU path beside the other configs
-        if "decode_b1_ctx1024" in extras:
-            extras["decode_b1_ctx1024"]["cpu"] = cpu_decode_b1(2.0)
-        if "prefill_config1" in extras:
-            extras["prefill_config1"]["cpu"] = cpu_prefill(W.config1_prefill(n_kv_head=12), 2.0)
-            extras["prefill_config1_gqa3"]["cpu"] = cpu_prefill(W.config1_prefill(n_kv_head=3), 2.0)
-            extras["packed_config4"]["cpu"] = cpu_prefill(W.config4_packed(), 2.0)
         if extras:
             log("cpu beside the extras: " + str({k: v.get("cpu") for k, v in extras.items()
                                                  if isinstance(v, dict) and "cpu" in v}))
@@ -539,6 +642,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic",
+        "tuning": tuning_state(),
         "config": {"workload": "config3 paged decode b16, ctx U[64,2048], 12 layers, "
                                "append + attention per layer",
                    "batch": 16, "n_head": 12, "n_kv_head": args.kv_heads, "head_dim": 64,

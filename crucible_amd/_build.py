@@ -1,9 +1,7 @@
-"""Build the gfx950 shared library and the host-only paging test binary.
+"""Build the gfx950 shared library.
 
 ``build_library()`` compiles every source under ``csrc/`` with hipcc for gfx950 into
 ``crucible_amd/libcrucible_attn.so`` (objects under ``crucible_amd/_build/``).
-``build_paging_kat()`` builds ``_build/paging_kat`` with g++ (no HIP), the C++ port of
-the reference's paging unit tests.
 """
 from __future__ import annotations
 
@@ -16,7 +14,6 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB_PATH = os.path.join(HERE, "libcrucible_attn.so")
-KAT_PATH = os.path.join(BUILD, "paging_kat")
 
 ARCH = "gfx950"
 DEVICE_SOURCES = ["kv_append.hip", "attn_decode.hip", "attn_prefill.hip", "argmax.hip",
@@ -25,6 +22,10 @@ DEVICE_SOURCES = ["kv_append.hip", "attn_decode.hip", "attn_prefill.hip", "argma
 HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                "-Wall", "-Wno-unused-function"]
+# Per-source additions. The decode kernel's leading scalar arguments (the prologue's table,
+# length and position pointers, batch and length indexing: 6 arguments, 9 SGPRs) are
+# preloaded into SGPRs at wave launch, so its first loads do not wait for the argument block.
+EXTRA_FLAGS = {"attn_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=6"]}
 
 
 def _hipcc() -> str:
@@ -51,7 +52,8 @@ def build_library(jobs: int = 8) -> str:
         obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
         lang = ["-x", "hip"] if src.endswith(".cpp") else []
-        cmds.append([hipcc, *HIPCC_FLAGS, *lang, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), *lang, "-c",
+                     os.path.join(CSRC, src), "-o", obj])
     with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         list(ex.map(_run, cmds))
     tmp = LIB_PATH + ".tmp"
@@ -60,18 +62,8 @@ def build_library(jobs: int = 8) -> str:
     return LIB_PATH
 
 
-def build_paging_kat() -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    cxx = os.environ.get("CXX", "g++")
-    _run([cxx, "-O2", "-std=c++17", "-Wall", "-Wextra",
-          os.path.join(CSRC, "paging_kat.cpp"), os.path.join(CSRC, "paging.cpp"),
-          "-o", KAT_PATH])
-    return KAT_PATH
-
-
 def build_all() -> None:
     build_library()
-    build_paging_kat()
 
 
 if __name__ == "__main__":

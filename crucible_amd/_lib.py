@@ -20,7 +20,7 @@ PAGE_TOKENS = 16
 # launch-shape override keys (enum crucible_tuning_key) and the decode order values
 TUNE_KEYS = {"decode_pages": 0, "decode_waves": 1, "decode_order": 2, "prefill_direct": 3,
              "prefill_heavy_first": 4, "prefill_qb": 5, "prefill_bufs": 6, "linear_tile": 7,
-             "decode_split_pages": 8}
+             "decode_combine_width": 8}
 DECODE_ORDERS = {"split": 0, "request": 1, "compact": 2}
 
 _P = ctypes.c_void_p
@@ -43,6 +43,7 @@ SIGNATURES = {
     "crucible_attention_decode_paged": ([_P, _I, _P, _P, _P, _I, _P, _P] + [_I64] * 9 + [_P, _SZ, _P], _I),
     "crucible_attention_decode_paged_append": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P] + [_I64] * 9 + [_P, _SZ, _P], _I),
     "crucible_attention_decode_paged_append_noalloc": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P] + [_I64] * 9 + [_P], _I),
+    "crucible_attention_decode_kernel_name": ([_I64, _I64, _I64, _I64, _I, _I, ctypes.c_char_p, _SZ], _I),
     "crucible_attention_decode_qkv_paged_append": ([_P, _I64, _P, _P, _I64, _P, _P, _P, _I, _P, _P, _P] + [_I64] * 9 + [_P, _SZ, _P], _I),
     "crucible_attention_decode": ([_P, _I, _P, _P, _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _SZ, _P], _I),
     "crucible_attention_split": ([_P, _I, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P], _I),

@@ -89,6 +89,7 @@ struct DecodeArgs {
     int out_row_stride;          // elements between output rows (n_head * 64)
 };
 
+
 __device__ __forceinline__ int request_len(const DecodeArgs& a, int b) {
     const int len = a.lens[b * a.lens_stride + a.lens_off];
     return len < a.max_seq ? len : a.max_seq;  // never index past the table
@@ -205,41 +206,54 @@ struct NewRow {
     half_t v[4];
 };
 
-// One uniform branch on the source dtype, then every load of the row is issued back to
-// back (vector loads for K, four scalar loads for V) before any conversion waits on them.
+// The appended row as loaded. Every lane loads its K channels 8*grp..+7 and 32+8*grp..+7
+// and its V channels 16*db + col (db < 4) of kv head g, whatever its column, and the f32 and
+// fp16 forms use the same instructions at dtype-dependent byte offsets: four 16-byte loads
+// (fp16 rows load their two 16-byte pieces twice) and four 4-byte loads (for fp16, the
+// aligned word that holds the value). No branch, no lane mask, no zero-filled register, so
+// the loads issue ahead of the page loads without a wait; with a branch on the dtype the
+// compiler converted the values inside it and waited for them before the page loads.
+struct RawRow {
+    u32x4_t k[4];
+    uint32_t v[4];
+};
+
+__device__ __forceinline__ RawRow load_row_raw(const DecodeArgs& a, int b, int g, int col,
+                                               int grp) {
+    RawRow r;
+    const int elt = a.kv_new_f16 ? 2 : 4;
+    const char* k = static_cast<const char*>(a.k_new) + ((int64_t)b * a.kv_new_stride + g * kHeadDim) * elt;
+    const char* v = static_cast<const char*>(a.v_new) + ((int64_t)b * a.kv_new_stride + g * kHeadDim) * elt;
+    // f32: channels 8grp..+3, 8grp+4..+7, 32+8grp..+3, 32+8grp+4..+7; fp16: 8grp..+7, 32+8grp..+7
+    const int k0 = 8 * grp * elt;
+    const int k2 = (32 + 8 * grp) * elt;
+    const int k1 = a.kv_new_f16 ? k0 : k0 + 16;
+    const int k3 = a.kv_new_f16 ? k2 : k2 + 16;
+    r.k[0] = *reinterpret_cast<const u32x4_t*>(k + k0);
+    r.k[1] = *reinterpret_cast<const u32x4_t*>(k + k1);
+    r.k[2] = *reinterpret_cast<const u32x4_t*>(k + k2);
+    r.k[3] = *reinterpret_cast<const u32x4_t*>(k + k3);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+        r.v[db] = *reinterpret_cast<const uint32_t*>(v + (((16 * db + col) * elt) & ~3));
+    return r;
+}
+
+// Rotate (ROPE, f32 rows) and round the loaded row to fp16.
 template <bool ROPE>
-__device__ __forceinline__ NewRow load_new_row(const DecodeArgs& a, int b, int g, int col,
-                                               int grp, int slot, const RopeCS& rc) {
-    NewRow r{};
-    const int64_t row = (int64_t)b * a.kv_new_stride + g * kHeadDim;
-    const bool k_lane = col == slot;
-    const bool v_lane = grp == (slot >> 2);
+__device__ __forceinline__ NewRow finish_row(const DecodeArgs& a, const RawRow& raw, int col,
+                                             const RopeCS& rc) {
+    NewRow r;
     if (a.kv_new_f16) {
-        const half_t* k = static_cast<const half_t*>(a.k_new) + row;
-        const half_t* v = static_cast<const half_t*>(a.v_new) + row;
-        if (k_lane) {
-            r.k0 = *reinterpret_cast<const half8_t*>(k + 8 * grp);
-            r.k1 = *reinterpret_cast<const half8_t*>(k + 32 + 8 * grp);
-        }
-        if (v_lane) {
+        r.k0 = __builtin_bit_cast(half8_t, raw.k[0]);
+        r.k1 = __builtin_bit_cast(half8_t, raw.k[2]);
 #pragma unroll
-            for (int db = 0; db < 4; ++db) r.v[db] = v[16 * db + col];
-        }
+        for (int db = 0; db < 4; ++db)
+            r.v[db] = __builtin_bit_cast(half_t, (uint16_t)(raw.v[db] >> ((col & 1) * 16)));
     } else {
-        const float* k = static_cast<const float*>(a.k_new) + row;
-        const float* v = static_cast<const float*>(a.v_new) + row;
-        float4_t k4[4] = {};
-        float vf[4] = {};
-        if (k_lane) {
-            k4[0] = *reinterpret_cast<const float4_t*>(k + 8 * grp);
-            k4[1] = *reinterpret_cast<const float4_t*>(k + 8 * grp + 4);
-            k4[2] = *reinterpret_cast<const float4_t*>(k + 32 + 8 * grp);
-            k4[3] = *reinterpret_cast<const float4_t*>(k + 32 + 8 * grp + 4);
-        }
-        if (v_lane) {
+        float4_t k4[4];
 #pragma unroll
-            for (int db = 0; db < 4; ++db) vf[db] = v[16 * db + col];
-        }
+        for (int i = 0; i < 4; ++i) k4[i] = __builtin_bit_cast(float4_t, raw.k[i]);
         if constexpr (ROPE) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -258,7 +272,7 @@ __device__ __forceinline__ NewRow load_new_row(const DecodeArgs& a, int b, int g
             r.k0[4 + j] = (half_t)k4[1][j];
             r.k1[j] = (half_t)k4[2][j];
             r.k1[4 + j] = (half_t)k4[3][j];
-            r.v[j] = (half_t)vf[j];
+            r.v[j] = (half_t)__builtin_bit_cast(float, raw.v[j]);
         }
     }
     return r;
@@ -278,6 +292,20 @@ __device__ __forceinline__ void store_new_row(const DecodeArgs& a, const NewRow&
 #pragma unroll
         for (int db = 0; db < 4; ++db) vp[db * 16 * kPageTokens] = r.v[db];
     }
+}
+
+// Max of a lane's 8 scores (v_max3 chains; fmaxf would add a canonicalising v_max per
+// operand). The inputs are VALU results, which the hardware interlocks.
+__device__ __forceinline__ float max8(const float (&v)[8]) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3\n\t"
+        "v_max3_f32 %0, %0, %4, %5\n\t"
+        "v_max3_f32 %0, %0, %6, %7\n\t"
+        "v_max_f32 %0, %0, %8"
+        : "=&v"(r)
+        : "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]),
+          "v"(v[7]));
+    return r;
 }
 
 constexpr int kOrderSplit = 0;
@@ -374,7 +402,19 @@ __device__ __forceinline__ bool compact_find(const DecodeArgs& a, int lane, Comp
 // CW: splits merged per round trip by the combining workgroup (combine_partials).
 template <int PAGES, int WAVES, bool QF32, bool APPEND, bool PAGED, int ORDER, bool ROPE,
           int CW = 8>
-__global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(WAVES * 64) void decode_kernel(
+    const int32_t* __restrict__ tables, const int32_t* __restrict__ lens,
+    const int32_t* __restrict__ positions, int batch, int lens_stride, int lens_off,
+    DecodeArgs a) {
+    // The leading arguments repeat what the prologue's first loads need (they are also in
+    // `a`): the library is built with kernarg preloading, so they arrive in SGPRs and the
+    // length / page-id loads issue without waiting for the argument block to be fetched.
+    a.tables = tables;
+    a.lens = lens;
+    a.positions = positions;
+    a.batch = batch;
+    a.lens_stride = lens_stride;
+    a.lens_off = lens_off;
     static_assert(!ROPE || (QF32 && APPEND), "RoPE is fused for f32 rows with the append");
     __shared__ float4_t s_acc[WAVES][16][17];  // [wave][col][dim/4], padded
     __shared__ float s_m[WAVES][16];
@@ -390,6 +430,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     // request's length and its append position.
     int s, g, b, len, pos = -1;
     int pid[PAGES] = {};  // this wave's page ids, through the scalar cache
+    int u_begin, u_end;   // the unit's logical pages
     if constexpr (ORDER == kOrderCompact) {
         // Workgroup i serves the i-th unit (compact_find), so the units take the lowest
         // workgroup ids and a launch whose units fit the CUs gets one CU per unit; the ids
@@ -449,6 +490,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
         if constexpr (APPEND) asm volatile("" : "+s"(pos));
         len = lr < a.max_seq ? lr : a.max_seq;  // never index past the table
     }
+    u_begin = s << a.split_shift;
+    u_end = u_begin + (1 << a.split_shift);
     const int bg = b * a.n_kv_head + g;
 
     // Query operand: B[k = channel][col = head], 8 channels per lane per MFMA.
@@ -481,18 +524,17 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
         }
     }
 
-    const int wp0 = (s << a.split_shift) + wave * PAGES;
+    const int wp0 = u_begin + wave * PAGES;
     int64_t page[PAGES];
 #pragma unroll
     for (int i = 0; i < PAGES; ++i)
         page[i] = PAGED ? (int64_t)pid[i] : (int64_t)(wp0 + i);
     int apos = -1;  // position of the row this workgroup appends, or -1
     if (APPEND && pos >= 0 && pos < (a.max_pages << kPageShift) &&
-        (pos >> (kPageShift + a.split_shift)) == s)
+        (pos >> kPageShift) >= u_begin && (pos >> kPageShift) < u_end)
         apos = pos;
     const int n_pages = len > 0 ? (len + kPageMask) >> kPageShift : 0;
-    const int p_begin = s << a.split_shift;
-    const bool attend = p_begin < n_pages;
+    const bool attend = u_begin < n_pages;
     if (!attend && apos < 0) return;
     // index of the appended row's page among this wave's pages (wave-uniform), or -1
     const int aidx = (apos >= 0 && (apos >> kPageShift) >= wp0 && (apos >> kPageShift) < wp0 + PAGES)
@@ -505,7 +547,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     if (!attend) {
         // append only: the row lies past the attended length
         if (aidx >= 0) {
-            const NewRow nr = load_new_row<ROPE>(a, b, g, col, grp, aslot, rc);
+            const NewRow nr = finish_row<ROPE>(a, load_row_raw(a, b, g, col, grp), col, rc);
 #pragma unroll
             for (int i = 0; i < PAGES; ++i)
                 if (i == aidx) store_new_row(a, nr, block_base(a.addr, page[i]), g, col, grp, aslot);
@@ -513,16 +555,24 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
         return;
     }
     const int n_active = (n_pages + (1 << a.split_shift) - 1) >> a.split_shift;
-    const int wp_end = min(wp0 + PAGES, n_pages);
+    const int wp_end = min(min(wp0 + PAGES, u_end), n_pages);
 
-    // Issue every load of this wave's pages before any arithmetic.
+    // The appended row's loads go out first (wave-uniform branch), then every load of this
+    // wave's pages, before any arithmetic: the row is needed only when the pages are in.
+    RawRow raw;
+    if (APPEND && aidx >= 0) raw = load_row_raw(a, b, g, col, grp);
+    // Every slot loads (no branch per page): a slot past the wave's pages reads its first
+    // page again, which is in bounds, and is never used. Conditional loads made the compiler
+    // merge registers between the two paths, which waited for the first page's K before the
+    // second page's loads went out: two round trips instead of one. A wave without pages
+    // loads nothing (uniform branch).
     half8_t ka[PAGES][2];
     half4_t va[PAGES][4];
     const int kv_dim = a.addr.kv_dim;
+    if (wp0 < wp_end) {
 #pragma unroll
-    for (int i = 0; i < PAGES; ++i) {
-        if (wp0 + i < wp_end) {
-            const int64_t base = block_base(a.addr, page[i]);
+        for (int i = 0; i < PAGES; ++i) {
+            const int64_t base = block_base(a.addr, wp0 + i < wp_end ? page[i] : page[0]);
             const half_t* kp = a.k_pool + base + (int64_t)col * kv_dim + g * kHeadDim + 8 * grp;
             ka[i][0] = *reinterpret_cast<const half8_t*>(kp);
             ka[i][1] = *reinterpret_cast<const half8_t*>(kp + 32);
@@ -546,7 +596,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     if (APPEND && aidx >= 0) {
         // The appended row replaces what the page held in this wave's operands and is
         // written to the page for later steps.
-        const NewRow nr = load_new_row<ROPE>(a, b, g, col, grp, aslot, rc);
+        const NewRow nr = finish_row<ROPE>(a, raw, col, rc);
 #pragma unroll
         for (int i = 0; i < PAGES; ++i) {
             if (i == aidx) {
@@ -565,59 +615,98 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
         }
     }
 
-    float m = -INFINITY;
-    float l = 0.0f;
-    float4_t acc[4] = {};
+    // V operands that must not reach the PV products as they are: slots past the wave's
+    // pages (a re-read of its first page) and the keys at or past the end of the last page
+    // (unwritten slots may hold NaN, and 0 * NaN would poison the product) are zeroed here,
+    // once, by uniform branches.
 #pragma unroll
     for (int i = 0; i < PAGES; ++i) {
         const int p = wp0 + i;
-        if (p < wp_end) {
-            float4_t st = {};
-            st = mfma_16x16x32(ka[i][0], qh0, st);
-            st = mfma_16x16x32(ka[i][1], qh1, st);
-            if constexpr (QF32) {
-                st = mfma_16x16x32(ka[i][0], ql0, st);
-                st = mfma_16x16x32(ka[i][1], ql1, st);
-            }
-            // st[r] = S^T[token 4*grp + r][col]
+        if (p >= wp_end) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) va[i][db] = half4_t{0, 0, 0, 0};
+        } else if (p == n_pages - 1 && (len & kPageMask)) {
             const int tok0 = p * kPageTokens + 4 * grp;
-            float sv[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) sv[r] = (tok0 + r < len) ? st[r] * a.scale_log2 : -INFINITY;
-            float tm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-            tm = group_max4(tm);
-            const float mn = fmaxf(m, tm);
-            const float alpha = fast_exp2(m - mn);
-            float pv[4];
-            float ps = 0.0f;
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    va[i][db][r] = (tok0 + r < len) ? va[i][db][r] : (half_t)0.0f;
+        }
+    }
+
+    // Pages go through the softmax and the PV product in pairs. S^T of the two pages leaves
+    // lane group grp with keys 4grp..+3 of the first page and of the second; those 8 values
+    // are the k range 8grp..+7 of one 32-key PV step (mfma 16x16x32), whose V^T operand is
+    // the lane's two 8-byte page quarters side by side. So a pair costs one max, one rescale
+    // and 4 dim blocks x (hi, lo) PV products, half the products of a page at a time. Scores
+    // stay unscaled (the scale is positive), folded into the exponent's FMA.
+    const float scale = a.scale_log2;
+    float m = -INFINITY;  // running max of the raw scores
+    float l = 0.0f;
+    float4_t acc[4] = {};
+#pragma unroll
+    for (int i = 0; i < PAGES; i += 2) {
+        const int p = wp0 + i;
+        if (p < wp_end) {
+            const bool two = PAGES > 1 && p + 1 < wp_end;
+            float4_t s0 = {}, s1 = {};
+            s0 = mfma_16x16x32(ka[i][0], qh0, s0);
+            s0 = mfma_16x16x32(ka[i][1], qh1, s0);
+            if constexpr (QF32) {
+                s0 = mfma_16x16x32(ka[i][0], ql0, s0);
+                s0 = mfma_16x16x32(ka[i][1], ql1, s0);
+            }
+            if constexpr (PAGES > 1) {
+                s1 = mfma_16x16x32(ka[i + 1][0], qh0, s1);
+                s1 = mfma_16x16x32(ka[i + 1][1], qh1, s1);
+                if constexpr (QF32) {
+                    s1 = mfma_16x16x32(ka[i + 1][0], ql0, s1);
+                    s1 = mfma_16x16x32(ka[i + 1][1], ql1, s1);
+                }
+            }
+            // visible keys of the pair for this lane group: s0[r] is key 4grp + r of page p,
+            // s1[r] key 4grp + r of page p + 1
+            const int lim = min(len, (p + (two ? 2 : 1)) * kPageTokens) - p * kPageTokens - 4 * grp;
+            float sv[8];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                pv[r] = fast_exp2(sv[r] - mn);
-                ps += pv[r];
+                sv[r] = (r < lim) ? s0[r] : -INFINITY;
+                sv[4 + r] = (kPageTokens + r < lim) ? s1[r] : -INFINITY;
             }
-            l = l * alpha + ps;
+            const float tm = group_max4(max8(sv));
+            const float mn = fmaxf(m, tm);  // finite: the pair's first page has a visible key
+            const float mu = mn * scale;
+            float pv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pv[j] = fast_exp2(__builtin_fmaf(sv[j], scale, -mu));
+            const float alpha = fast_exp2(__builtin_fmaf(m, scale, -mu));  // m = -inf: 0
+            l = l * alpha + (((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7])));
             m = mn;
-            half4_t ph, plo;
+            u32x4_t hw, lw;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                ph[r] = (half_t)pv[r];
-                plo[r] = (half_t)(pv[r] - (float)ph[r]);
+            for (int h = 0; h < 2; ++h) {
+                const float q4[4] = {pv[4 * h], pv[4 * h + 1], pv[4 * h + 2], pv[4 * h + 3]};
+                hw[2 * h] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(q4[0], q4[1]));
+                hw[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(q4[2], q4[3]));
+                uint32_t lo01, lo23;
+                split_lo4(q4, hw[2 * h], hw[2 * h + 1], lo01, lo23);
+                lw[2 * h] = lo01;
+                lw[2 * h + 1] = lo23;
             }
-            const bool tail = (p == n_pages - 1) && (len & kPageMask);
+            const half8_t ph = __builtin_bit_cast(half8_t, hw);
+            const half8_t pl = __builtin_bit_cast(half8_t, lw);
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                half4_t v = va[i][db];
-                if (tail) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        if (tok0 + r >= len) v[r] = (half_t)0.0f;  // unwritten slots may hold NaN
-                }
-                acc[db] = acc[db] * alpha;
-                acc[db] = mfma_16x16x16(v, ph, acc[db]);
-                acc[db] = mfma_16x16x16(v, plo, acc[db]);
+                const half4_t vb = PAGES > 1 ? va[i + (PAGES > 1)][db] : half4_t{0, 0, 0, 0};
+                const half8_t v = __builtin_shufflevector(va[i][db], vb, 0, 1, 2, 3, 4, 5, 6, 7);
+                if (i > 0) acc[db] = acc[db] * alpha;  // the first pair starts from zero
+                acc[db] = mfma_16x16x32(v, ph, acc[db]);
+                acc[db] = mfma_16x16x32(v, pl, acc[db]);
             }
         }
     }
+    m *= scale;  // the wave merge and the partials work in log2-scaled units
     l = group_sum4(l);
 
     // Merge the waves' states: acc[db][r] = O^T[16*db + 4*grp + r][col].
@@ -715,17 +804,27 @@ DecodeShape decode_shape(int64_t batch, int64_t n_kv_head, int64_t max_pages) {
     return sh;
 }
 
+// The combine width: 16 splits per round trip where a launch can have more than 8, unless
+// CRUCIBLE_TUNE_DECODE_COMBINE_WIDTH says otherwise (the merge loops over any count).
+bool wide_combine(const DecodeArgs& a) {
+    const int v = tuning(CRUCIBLE_TUNE_DECODE_COMBINE_WIDTH);
+    return v > 0 ? v == 16 : a.n_splits > 8;
+}
+
+// The decode kernel's arguments: the preloaded prologue values, then the block.
+#define DECODE_ARGS(a) (a).tables, (a).lens, (a).positions, (a).batch, (a).lens_stride, (a).lens_off, (a)
+
 template <bool QF32, bool APPEND, bool PAGED, bool ROPE = false>
 bool launch_shape(const DecodeArgs& a, DecodeShape sh, int order, dim3 grid,
                   hipStream_t stream) {
     // The 16-wide combine only where a launch can have more than 8 splits.
 #define CRUCIBLE_DECODE_ORDER(P, W, O)                                                         \
-    if (a.n_splits > 8)                                                                         \
+    if (wide_combine(a))                                                                        \
         hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, O, ROPE, 16>), grid,       \
-                           dim3(W * 64), 0, stream, a);                                         \
+                           dim3(W * 64), 0, stream, DECODE_ARGS(a));                                         \
     else                                                                                        \
         hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, O, ROPE>), grid,           \
-                           dim3(W * 64), 0, stream, a);
+                           dim3(W * 64), 0, stream, DECODE_ARGS(a));
 #define CRUCIBLE_DECODE_CASE(P, W)                                                             \
     if (sh.pages == P && sh.waves == W) {                                                       \
         if (order == kOrderCompact) {                                                           \
@@ -734,7 +833,7 @@ bool launch_shape(const DecodeArgs& a, DecodeShape sh, int order, dim3 grid,
             CRUCIBLE_DECODE_ORDER(P, W, kOrderRequest)                                          \
         } else {                                                                                \
             hipLaunchKernelGGL((decode_kernel<P, W, QF32, APPEND, PAGED, kOrderSplit, ROPE>),   \
-                               grid, dim3(W * 64), 0, stream, a);                               \
+                               grid, dim3(W * 64), 0, stream, DECODE_ARGS(a));                               \
         }                                                                                       \
         return true;                                                                            \
     }
@@ -1156,6 +1255,39 @@ extern "C" int crucible_attention_decode_qkv_paged_append(
     a.addr.layer_off = layer * kPageTokens * kv_dim;
     a.table_stride = (int32_t)table_stride;
     return decode_with_workspace(a, true, workspace, workspace_bytes, stream, what);
+}
+
+// The decode kernel an entry point would launch for this shape, as rocprof names it
+// (template arguments PAGES, WAVES, QF32, APPEND, PAGED, ORDER, ROPE, CW), following the
+// same choices as the launch path (shape, grid order, combine width, overrides).
+extern "C" int crucible_attention_decode_kernel_name(int64_t batch, int64_t n_head,
+                                                     int64_t n_kv_head, int64_t max_seq,
+                                                     int q_dtype, int entry, char* buf,
+                                                     size_t n) {
+    if (!buf || n == 0 || batch <= 0 || n_head <= 0 || n_kv_head <= 0 || max_seq <= 0 ||
+        entry < 0 || entry > 2) {
+        set_error(CRUCIBLE_ERR_INVALID, "decode_kernel_name: bad arguments");
+        return CRUCIBLE_ERR_INVALID;
+    }
+    const int64_t max_pages = (max_seq + kPageMask) >> kPageShift;
+    const bool append = entry != 0;
+    const bool rope = entry == 2;
+    const bool qf32 = rope || q_dtype == CRUCIBLE_F32;
+    const DecodeShape sh = decode_shape(batch, n_kv_head, max_pages);
+    const int pages = sh.pages;
+    const int waves = sh.waves;
+    const int n_splits = (int)((max_pages + pages * waves - 1) / (pages * waves));
+    const int64_t units = (int64_t)n_splits * n_kv_head * batch;
+    int order = (units > device_cu_count() && batch <= kCompactMaxBatch) ? kOrderCompact
+                                                                        : kOrderRequest;
+    if (const int v = tuning(CRUCIBLE_TUNE_DECODE_ORDER); v >= 0)
+        order = (v == kOrderCompact && batch > kCompactMaxBatch) ? kOrderRequest : v;
+    const int wv = tuning(CRUCIBLE_TUNE_DECODE_COMBINE_WIDTH);
+    const int cw = order == kOrderSplit ? 8 : (wv > 0 ? wv : (n_splits > 8 ? 16 : 8));
+    std::snprintf(buf, n, "decode_kernel<%d, %d, %s, %s, true, %d, %s, %d>", pages, waves,
+                  qf32 ? "true" : "false", append ? "true" : "false", order,
+                  rope ? "true" : "false", cw);
+    return CRUCIBLE_OK;
 }
 
 extern "C" int crucible_attention_decode(const void* q, int q_dtype, const void* k_cache,

@@ -144,25 +144,6 @@ __device__ __forceinline__ void mask_tile_blocks(float4_t (&st)[4], int lim) {
 // in the LDS form, see tile_key; keys 4 grp .. +3 of each 16-key block in the direct
 // form). Returns the lane's sum of P.
 //
-// The split per pair of values: hi = v_cvt_pkrtz (round toward zero), and lo = RNE(p -
-// hi) from v_fma_mix{lo,hi}_f16, which take hi as an fp16 operand, form p - hi exactly in
-// f32 and round once to fp16 into one half of the packed result (one instruction per value
-// where the C form needs a convert, a subtract and half a pack).
-//
-// It reads v_exp_f32 results (1 wait state) and an MFMA reads what it writes (2 wait
-// states): the block opens with s_nop 0 and ends with s_nop 1.
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void split_lo4(const float (&p)[4], uint32_t h01, uint32_t h23,
-                                          uint32_t& lo01, uint32_t& lo23) {
-    asm("s_nop 0\n\t"
-        "v_fma_mixlo_f16 %0, %2, -1.0, %4 op_sel_hi:[1,0,0]\n\t"
-        "v_fma_mixhi_f16 %0, %2, -1.0, %5 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
-        "v_fma_mixlo_f16 %1, %3, -1.0, %6 op_sel_hi:[1,0,0]\n\t"
-        "v_fma_mixhi_f16 %1, %3, -1.0, %7 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
-        "s_nop 1"
-        : "=&v"(lo01), "=&v"(lo23)
-        : "v"(h01), "v"(h23), "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]));
-}
 __device__ __forceinline__ float tile_p(const float4_t (&st)[4], float scale, float mu,
                                         half8_t (&pb)[2], half8_t (&pl)[2]) {
     u32x4_t hw[2], lw[2];

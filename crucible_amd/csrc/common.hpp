@@ -31,6 +31,7 @@ typedef _Float16 half_t;
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------- addressing
 
@@ -94,6 +95,26 @@ __device__ __forceinline__ float group_sum4(float x) {
     return x;
 }
 
+// P as fp16 hi + lo (the operand pairs of the PV products): hi = v_cvt_pkrtz (round toward
+// zero) of a pair of values, and lo = RNE(p - hi) from v_fma_mix{lo,hi}_f16, which take hi
+// as an fp16 operand, form p - hi exactly in f32 and round once to fp16 into one half of the
+// packed result (one instruction per value where the C form needs a convert, a subtract
+// and half a pack). hi + lo carries p to about 2^-22 relative.
+//
+// It reads v_exp_f32 results (1 wait state) and an MFMA reads what it writes (2 wait
+// states): the block opens with s_nop 0 and ends with s_nop 1.
+__device__ __forceinline__ void split_lo4(const float (&p)[4], uint32_t h01, uint32_t h23,
+                                          uint32_t& lo01, uint32_t& lo23) {
+    asm("s_nop 0\n\t"
+        "v_fma_mixlo_f16 %0, %2, -1.0, %4 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, %2, -1.0, %5 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixlo_f16 %1, %3, -1.0, %6 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %1, %3, -1.0, %7 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "s_nop 1"
+        : "=&v"(lo01), "=&v"(lo23)
+        : "v"(h01), "v"(h23), "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]));
+}
+
 __device__ __forceinline__ float4_t mfma_16x16x32(half8_t a, half8_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -105,8 +126,6 @@ __device__ __forceinline__ float4_t mfma_16x16x16(half4_t a, half4_t b, float4_t
 // Raw buffer resource over [base, base + bytes) for 16-byte loads and stores that carry a
 // cache policy (word 3 is the gfx9 raw-buffer format). Accesses past `bytes` are dropped
 // (stores) or read zero (loads).
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }

@@ -80,7 +80,7 @@ enum crucible_tuning_key {
     CRUCIBLE_TUNE_PREFILL_QB = 5,          /* prefill 16-row blocks per wave: 1, 2 */
     CRUCIBLE_TUNE_PREFILL_BUFS = 6,        /* prefill LDS ring depth in key tiles: 4, 6 */
     CRUCIBLE_TUNE_LINEAR_TILE = 7,         /* projection tile columns: 4, 16 */
-    CRUCIBLE_TUNE_DECODE_SPLIT_PAGES = 8,  /* pages per unit of a decode work plan: 1..16 */
+    CRUCIBLE_TUNE_DECODE_COMBINE_WIDTH = 8, /* decode splits merged per round trip: 8, 16 */
     CRUCIBLE_TUNE_COUNT = 9
 };
 int crucible_attn_set_tuning(int key, int value);
@@ -170,6 +170,14 @@ int crucible_attention_decode_paged_append(
     int64_t n_kv_head, int64_t head_dim, int64_t table_stride, int64_t n_layer, int64_t layer,
     int64_t kv_dim, int64_t max_seq, void* workspace, size_t workspace_bytes,
     crucible_stream_t stream);
+
+/* The decode kernel a call would launch for this shape, as profilers name it:
+ * "decode_kernel<PAGES, WAVES, QF32, APPEND, PAGED, ORDER, ROPE, CW>" (NUL-terminated,
+ * truncated to n). entry: 0 attention_decode_paged, 1 attention_decode_paged_append,
+ * 2 attention_decode_qkv_paged_append. Launches nothing. */
+int crucible_attention_decode_kernel_name(int64_t batch, int64_t n_head, int64_t n_kv_head,
+                                          int64_t max_seq, int q_dtype, int entry, char* buf,
+                                          size_t n);
 
 /* No counterpart in the reference. For callers that cannot allocate device memory
  * (code under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc):

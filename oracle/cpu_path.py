@@ -9,7 +9,10 @@ engine does implicitly, engine/kernels/kernels.cu:1741-1839 reads ``table[pos >>
 and the per-step KV append is the row scatter of engine/kernels/kernels.cu:1713-1731.
 
 The pool here is the reference's f32 layout [page][layer][16][kv_dim] holding the
-fp16-representable values the GPU pools hold, widened to f32.
+fp16-representable values the GPU pools hold, widened to f32. bench.py hands in the very
+values its GPU run used (host copies of the device pools' pages, queries and appended rows),
+so both sides time the same bytes. Timing follows the plan the baseline states: 5 untimed
+warmup repetitions, then the median of at least 20 timed repetitions.
 """
 from __future__ import annotations
 
@@ -39,30 +42,28 @@ def threads() -> int:
 class DecodeBatchCPU:
     """One continuous-batching decode step over all layers, on the CPU.
 
-    ``lens[b]`` includes the token appended this step at position ``lens[b] - 1``.
+    ``lens[b]`` includes the token appended this step at position ``lens[b] - 1``. The
+    inputs are the GPU run's: ``k_pages``/``v_pages`` [n_pages][n_layer][16][kv_dim] (fp16
+    values, reference element order), ``tables`` [batch][>= pages] into them, ``q``
+    [n_layer][batch][n_head * head_dim] and the appended rows ``src_k``/``src_v``
+    [n_layer][batch][kv_dim] (f32, rounded to fp16 when stored, as the GPU append does).
     """
 
-    def __init__(self, lens, n_layer: int, n_head: int, n_kv_head: int, head_dim: int = 64,
-                 seed: int = 0):
+    def __init__(self, lens, n_layer: int, n_head: int, n_kv_head: int, k_pages, v_pages,
+                 tables, q, src_k, src_v, head_dim: int = 64):
         self.lens = np.asarray(lens, np.int64)
         self.n_layer, self.n_head, self.n_kv, self.hd = n_layer, n_head, n_kv_head, head_dim
         self.kv_dim = n_kv_head * head_dim
-        g = torch.Generator().manual_seed(seed)
         pages = [-(-int(n) // PAGE_TOKENS) for n in self.lens]
-        n_pages = sum(pages)
-        perm = torch.randperm(n_pages, generator=g)
-        self.tables = []
-        cur = 0
-        for n in pages:
-            self.tables.append(perm[cur:cur + n].clone())
-            cur += n
-        shape = (n_pages, n_layer, PAGE_TOKENS, self.kv_dim)
-        self.k_pool = torch.randn(shape, generator=g).half().float()
-        self.v_pool = torch.randn(shape, generator=g).half().float()
+        self.tables = [torch.from_numpy(np.asarray(tables[b][:n], np.int64))
+                       for b, n in enumerate(pages)]
+        self.k_pool = torch.from_numpy(np.asarray(k_pages, np.float16)).float()
+        self.v_pool = torch.from_numpy(np.asarray(v_pages, np.float16)).float()
         b = len(self.lens)
-        self.q = torch.randn((n_layer, b, n_head, 1, head_dim), generator=g).half().float()
-        self.src_k = torch.randn((n_layer, b, self.kv_dim), generator=g)
-        self.src_v = torch.randn((n_layer, b, self.kv_dim), generator=g)
+        self.q = torch.from_numpy(np.asarray(q, np.float16)).float().reshape(
+            n_layer, b, n_head, 1, head_dim)
+        self.src_k = torch.from_numpy(np.asarray(src_k, np.float32))
+        self.src_v = torch.from_numpy(np.asarray(src_v, np.float32))
 
     def step(self) -> list[torch.Tensor]:
         outs = []
@@ -86,18 +87,24 @@ class DecodeBatchCPU:
 
 
 class PrefillCPU:
-    """Causal prefill of packed sequences: one SDPA(is_causal) call per sequence."""
+    """Causal prefill of packed sequences: one SDPA(is_causal) call per sequence, on the GPU
+    run's packed rows q [rows][n_head * head_dim] and k, v [rows][n_kv_head * head_dim]."""
 
-    def __init__(self, seq_lens, n_head: int, n_kv_head: int, head_dim: int = 64, seed: int = 0):
-        g = torch.Generator().manual_seed(seed)
+    def __init__(self, seq_lens, n_head: int, n_kv_head: int, q, k, v, head_dim: int = 64):
         self.n_head, self.n_kv = n_head, n_kv_head
         self.seqs = []
+        q = torch.from_numpy(np.asarray(q, np.float32))
+        k = torch.from_numpy(np.asarray(k, np.float32))
+        v = torch.from_numpy(np.asarray(v, np.float32))
+        start = 0
         for n in seq_lens:
             n = int(n)
-            q = torch.randn((1, n_head, n, head_dim), generator=g)
-            k = torch.randn((1, n_kv_head, n, head_dim), generator=g)
-            v = torch.randn((1, n_kv_head, n, head_dim), generator=g)
-            self.seqs.append((q, k, v))
+            sl = slice(start, start + n)
+            self.seqs.append((
+                q[sl].reshape(n, n_head, head_dim).transpose(0, 1).unsqueeze(0).contiguous(),
+                k[sl].reshape(n, n_kv_head, head_dim).transpose(0, 1).unsqueeze(0).contiguous(),
+                v[sl].reshape(n, n_kv_head, head_dim).transpose(0, 1).unsqueeze(0).contiguous()))
+            start += n
 
     def step(self) -> list[torch.Tensor]:
         return [F.scaled_dot_product_attention(q, k, v, is_causal=True,
@@ -105,15 +112,27 @@ class PrefillCPU:
                 for q, k, v in self.seqs]
 
 
-def time_bounded(fn, seconds: float, min_reps: int = 3, warmup: int = 1):
-    """Run fn at least min_reps times and until `seconds` have passed; return (reps, s/rep)."""
+def time_median(fn, seconds: float, min_reps: int = 20, warmup: int = 5):
+    """5 untimed warmup calls, then timed calls until at least min_reps have run and
+    `seconds` have passed; returns (reps, median seconds per call)."""
     for _ in range(warmup):
         fn()
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_reps or time.perf_counter() - t_start < seconds:
+        t0 = time.perf_counter()
         fn()
-        reps += 1
-        dt = time.perf_counter() - t0
-        if reps >= min_reps and dt >= seconds:
-            return reps, dt / reps
+        times.append(time.perf_counter() - t0)
+    return len(times), float(np.median(times))
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name", read from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:  # pragma: no cover
+        pass
+    return "unknown"

@@ -13,7 +13,10 @@ reference's helpers from engine/src/ops.rs:
   * silu (:84-86) and the tied vocabulary projection (model.rs:288-297);
   * greedy selection: sampling.rs:141-150 (oracle.c orc_argmax).
 The one change is the storage contract of the paged fp16 KV cache: K (after RoPE) and V
-are rounded to fp16 (RNE) when they are written, as the GPU pools hold them.
+are rounded to fp16 (RNE) when they are written, as the GPU pools hold them. With
+kv_fp16=False the cache keeps f32 values, which is the reference's own f32 cache
+(engine/src/cache.rs:16-105); comparing the two measures what the storage change alone does
+to greedy tokens (oracle/kv_storage_report.py).
 
 Prompts are processed layer by layer over all their positions at once, which performs
 exactly the per-position arithmetic of the reference's token-major loop (a position at
@@ -27,8 +30,9 @@ from . import attention_dense, f16_bits_to_f32, f32_to_f16_bits, argmax
 
 
 class OracleModel:
-    def __init__(self, cfg, weights: dict[str, np.ndarray]):
+    def __init__(self, cfg, weights: dict[str, np.ndarray], kv_fp16: bool = True):
         self.cfg = cfg
+        self.kv_fp16 = kv_fp16
         f64 = lambda n: weights[n].astype(np.float64)  # noqa: E731
         f32 = lambda n: weights[n].astype(np.float32)  # noqa: E731
         self.tok_emb32 = f32("tok_emb.weight")
@@ -86,8 +90,9 @@ class OracleModel:
             q = self.rope(self.matvec(L["wq"], h), positions, cfg.n_head)
             k = self.rope(self.matvec(L["wk"], h), positions, cfg.n_kv_head)
             v = self.matvec(L["wv"], h)
-            k = f16_bits_to_f32(f32_to_f16_bits(k))  # paged fp16 storage contract
-            v = f16_bits_to_f32(f32_to_f16_bits(v))
+            if self.kv_fp16:  # paged fp16 storage contract
+                k = f16_bits_to_f32(f32_to_f16_bits(k))
+                v = f16_bits_to_f32(f32_to_f16_bits(v))
             attn = np.zeros_like(q)
             for b in np.unique(owners):
                 sel = np.nonzero(owners == b)[0]

@@ -76,6 +76,41 @@ def cases(seed=SEED):
     return out
 
 
+def fuzz_cases(n=64, seed=SEED):
+    """The reference's fuzz corpus (gpu_attention_validation.rs:564-586; 64 rounds at seed
+    20260908 by default, main.rs:216-219): 1..16 requests per case, each with a length drawn
+    from the remaining context budget (at most 257) and a random start, ids round * 16 + i,
+    the case seed and Q profile round % 4, all from the xorshift stream (:40-45)."""
+    stream = _Xorshift(max(seed, 1))
+    out = []
+    for rnd in range(n):
+        count = 1 + stream.next() % 16
+        remaining = CONTEXT
+        slices = []
+        for i in range(count):
+            length = 1 + stream.next() % min(remaining - (count - i - 1), 257)
+            start = stream.next() % (CONTEXT - length + 1)
+            slices.append(Slice(rnd * 16 + i, start, length))
+            remaining -= length
+        out.append(Case(f"fuzz-{rnd}", slices, stream.next(), rnd % 4))
+    return out
+
+
+class _Xorshift:
+    """xorshift64 13/7/17 (gpu_attention_validation.rs:40-45) through the oracle's
+    orc_xorshift, one value at a time."""
+
+    def __init__(self, state):
+        import ctypes
+
+        self._st = ctypes.c_uint64(state)
+
+    def next(self) -> int:
+        import ctypes
+
+        return int(oracle.lib().orc_xorshift(ctypes.byref(self._st)))
+
+
 def _values(case, id_, n_pos):
     """[n_pos, KV_HEADS, HD] K (salt 31; profile 3 ramps d=0) and V (salt 47), float32."""
     k = oracle.value_grid(id_, 0, n_pos, KV_HEADS, HD, 31)

@@ -1,0 +1,177 @@
+"""BASELINE configs 1-4 fed with seeded fp32 Q, K and V, checked against the f64 oracle on
+the UNROUNDED fp32 values: the north-star bar (max-abs 2e-3 against the fp32 reference on the
+same seeded inputs) with the fp16 KV storage inside the measured error.
+
+K and V enter the pools through this library's f32 -> fp16 appends (the reference's
+cache_store_* scatters); queries stay f32 (carried as fp16 hi + lo halves). The oracle is
+orc_attention_dense in f64 over the original fp32 rows. Inputs come from the shared
+splitmix64 -> Box-Muller generator (oracle.normal_f32), seeds 20260908 + config index.
+
+The fp16 rounding of V bounds what is reachable: a causal row that sees one key returns that
+key's V, so its error is V's rounding, at most 2^-9 for |v| < 8 (half an ulp in [4, 8)). The
+bar of 2e-3 leaves 2.5% above that.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gates import north_star
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20260908
+
+
+def _normal(seed, *shape):
+    n = int(np.prod(shape))
+    return oracle.normal_f32(seed, n).reshape(shape)
+
+
+def _dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _want(q, k, v, lens, n_head, n_kv):
+    return oracle.attention_dense(q, k, v, np.asarray(lens, np.int32), n_head, n_kv, 64)
+
+
+@pytest.mark.parametrize("n_kv", [12, 3])
+def test_config1_fp32_prefill(gpu, dev, n_kv):
+    """Config 1: one causal sequence of 512 rows, 12 heads (12 or 3 KV heads), params form."""
+    L, H, kv = 512, 12, n_kv * 64
+    q = _normal(SEED, L, H * 64)
+    k = _normal(SEED + 100, L, kv)
+    v = _normal(SEED + 200, L, kv)
+    n_pages = 40
+    table = np.random.default_rng(SEED).permutation(n_pages)[:L // 16].astype(np.int32)
+    k_pool = torch.zeros(n_pages * 16 * kv, dtype=torch.float16, device=dev)
+    v_pool = torch.zeros_like(k_pool)
+    params = _dev(np.array([0, 0, 0, 0, 0, 0], np.int32), dev)
+    d_tab = _dev(table, dev)
+    gpu.cache_store_paged(_dev(k, dev), k_pool, d_tab, L, kv, 1, 0, params, kind="k")
+    gpu.cache_store_paged(_dev(v, dev), v_pool, d_tab, L, kv, 1, 0, params, kind="v")
+    out = torch.zeros(L, H * 64, device=dev)
+    gpu.attention_prefill_paged(_dev(q, dev), k_pool, v_pool, out, d_tab, L, H, n_kv, 64, 1, 0,
+                                kv, L, params)
+    torch.cuda.synchronize()
+    want = _want(q, k, v, np.arange(1, L + 1), H, n_kv)
+    err = north_star(out.cpu().numpy(), want, f"config 1 fp32, {n_kv} kv heads")
+    print(f"config 1 fp32 ({n_kv} kv heads): max-abs {err:.3e} against unrounded inputs")
+
+
+@pytest.mark.parametrize("n_kv", [3, 12])
+def test_config2_fp32_decode(gpu, dev, n_kv):
+    """Config 2: batch 1, 1024 keys from a 4096-page pool through a seeded 64-page table."""
+    from crucible_amd.workloads import config2_decode_b1
+    cfg = config2_decode_b1(n_kv_head=n_kv)
+    ctx, H, kv = 1024, 12, cfg.kv_dim
+    q = _normal(SEED + 1, 1, H * 64)
+    k = _normal(SEED + 101, ctx, kv)
+    v = _normal(SEED + 201, ctx, kv)
+    n_elem = cfg.n_pages * cfg.n_layer * 16 * kv
+    k_pool = torch.zeros(n_elem, dtype=torch.float16, device=dev)
+    v_pool = torch.zeros_like(k_pool)
+    layer = 5
+    d_tab = _dev(cfg.tables, dev)
+    params = _dev(np.zeros(6, np.int32), dev)
+    gpu.cache_store_paged(_dev(k, dev), k_pool, d_tab, ctx, kv, cfg.n_layer, layer, params,
+                          kind="k")
+    gpu.cache_store_paged(_dev(v, dev), v_pool, d_tab, ctx, kv, cfg.n_layer, layer, params,
+                          kind="v")
+    out = torch.zeros(1, H * 64, device=dev)
+    gpu.attention_decode_paged(_dev(q, dev), k_pool, v_pool, out, d_tab,
+                               _dev(np.array([ctx], np.int32), dev), 1, H, n_kv, 64,
+                               cfg.table_stride, cfg.n_layer, layer, kv, cfg.max_seq)
+    torch.cuda.synchronize()
+    want = _want(q, k, v, [ctx], H, n_kv)
+    err = north_star(out.cpu().numpy(), want, f"config 2 fp32, {n_kv} kv heads")
+    print(f"config 2 fp32 ({n_kv} kv heads): max-abs {err:.3e}")
+
+
+def test_config3_fp32_decode_all_layers(gpu, dev):
+    """Config 3: batch 16, lengths U[64, 2048], 8192-page pool, 12 layers. Each layer's history
+    (len - 1 rows a request) enters through the packed f32 append, the new token through the
+    fused append + decode; every layer is checked on the unrounded rows."""
+    from crucible_amd.workloads import config3_decode_b16
+    cfg = config3_decode_b16()
+    rng = np.random.default_rng(cfg.seed)
+    lens = np.asarray(cfg.lens, np.int32)
+    stride, H, n_kv, kv = cfg.table_stride, 12, 3, cfg.kv_dim
+    perm = rng.permutation(cfg.n_pages).astype(np.int32)
+    tables = np.zeros((16, stride), np.int32)
+    cur = 0
+    for b, n in enumerate(lens):
+        need = -(-int(n) // 16)
+        tables[b, :need] = perm[cur:cur + need]
+        cur += need
+    n_elem = cfg.n_pages * cfg.n_layer * 16 * kv
+    k_pool = torch.zeros(n_elem, dtype=torch.float16, device=dev)
+    v_pool = torch.zeros_like(k_pool)
+    d_tab, d_len = _dev(tables, dev), _dev(lens, dev)
+    d_pos = _dev(lens - 1, dev)
+    hist = int((lens - 1).sum())
+    owners = np.repeat(np.arange(16, dtype=np.int32), lens - 1)
+    positions = np.concatenate([np.arange(n - 1, dtype=np.int32) for n in lens])
+    d_own, d_hpos = _dev(owners, dev), _dev(positions, dev)
+    worst = 0.0
+    starts = np.concatenate([[0], np.cumsum(lens - 1)])
+    for layer in range(cfg.n_layer):
+        s = SEED + 2 + 1000 * layer
+        kh, vh = _normal(s + 1, hist, kv), _normal(s + 2, hist, kv)
+        kn, vn = _normal(s + 3, 16, kv), _normal(s + 4, 16, kv)
+        q = _normal(s + 5, 16, H * 64)
+        gpu.cache_store_packed_paged(_dev(kh, dev), k_pool, d_tab, d_own, d_hpos, hist, kv,
+                                     stride, cfg.n_layer, layer, kind="k")
+        gpu.cache_store_packed_paged(_dev(vh, dev), v_pool, d_tab, d_own, d_hpos, hist, kv,
+                                     stride, cfg.n_layer, layer, kind="v")
+        out = torch.zeros(16, H * 64, device=dev)
+        gpu.attention_decode_paged_append(_dev(q, dev), _dev(kn, dev), _dev(vn, dev), k_pool,
+                                          v_pool, out, d_tab, d_pos, d_len, 16, H, n_kv, 64,
+                                          stride, cfg.n_layer, layer, kv, cfg.max_seq)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        for b in range(16):
+            kb = np.concatenate([kh[starts[b]:starts[b + 1]], kn[b:b + 1]])
+            vb = np.concatenate([vh[starts[b]:starts[b + 1]], vn[b:b + 1]])
+            want = _want(q[b:b + 1], kb, vb, [int(lens[b])], H, n_kv)
+            worst = max(worst, north_star(got[b:b + 1], want, f"config 3 layer {layer} req {b}"))
+    print(f"config 3 fp32 (12 layers): max-abs {worst:.3e}")
+
+
+def test_config4_fp32_packed_prefill(gpu, dev):
+    """Config 4: 8 packed sequences U[32, 512], 16/4 heads, K/V through the packed append
+    (slot mapping), segment-form prefill with f32 queries."""
+    from crucible_amd.paged import segments_from_cu_seqlens
+    from crucible_amd.workloads import config4_packed
+    cfg = config4_packed()
+    H, n_kv, kv = cfg.n_head, cfg.n_kv_head, cfg.kv_dim
+    rows = cfg.rows
+    q = _normal(SEED + 3, rows, H * 64)
+    k = _normal(SEED + 103, rows, kv)
+    v = _normal(SEED + 203, rows, kv)
+    owners = np.concatenate([np.full(n, i, np.int32) for i, n in enumerate(cfg.seq_lens)])
+    positions = np.concatenate([np.arange(n, dtype=np.int32) for n in cfg.seq_lens])
+    stride = cfg.tables.shape[1]
+    n_elem = cfg.n_pages * cfg.n_layer * 16 * kv
+    k_pool = torch.zeros(n_elem, dtype=torch.float16, device=dev)
+    v_pool = torch.zeros_like(k_pool)
+    d_tab, d_own, d_pos = _dev(cfg.tables, dev), _dev(owners, dev), _dev(positions, dev)
+    gpu.cache_store_packed_paged(_dev(k, dev), k_pool, d_tab, d_own, d_pos, rows, kv, stride,
+                                 cfg.n_layer, 0, kind="k")
+    gpu.cache_store_packed_paged(_dev(v, dev), v_pool, d_tab, d_own, d_pos, rows, kv, stride,
+                                 cfg.n_layer, 0, kind="v")
+    seg, max_chunk = segments_from_cu_seqlens(cfg.cu_seqlens)
+    out = torch.zeros(rows, H * 64, device=dev)
+    gpu.attention_prefill_tiled(_dev(q, dev), k_pool, v_pool, None, None, out, d_tab,
+                                _dev(seg, dev), len(cfg.seq_lens), max_chunk, stride, H, n_kv,
+                                64, cfg.n_layer, 0, kv)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    worst = 0.0
+    cu = cfg.cu_seqlens
+    for i, n in enumerate(cfg.seq_lens):
+        sl = slice(cu[i], cu[i + 1])
+        want = _want(q[sl], k[sl], v[sl], np.arange(1, n + 1), H, n_kv)
+        worst = max(worst, north_star(got[sl], want, f"config 4 sequence {i}"))
+    print(f"config 4 fp32: max-abs {worst:.3e}")

@@ -3,7 +3,8 @@
 The reference's attention corpus (gpu_attention_validation.rs:431-509: page boundaries,
 offsets, singles up to 1024, packed 16x16..2x512, ragged rows at four Q-scale profiles) runs
 through every prefill entry point (segments, owners/positions, params, contiguous) and is
-compared with the f64 oracle on every element (bar: max-abs 2e-3). Structural contracts are
+compared with the f64 oracle on every element under the reference's element gate
+(|d| <= 2e-5 + 2e-5 |ref|, :20-22) and the north-star max-abs 2e-3. Structural contracts are
 exact: future-page poison leaves outputs bit-identical (:597-632), descriptor composition,
 order and page reuse leave each request's bits unchanged (:639-682), and output rows outside
 the written range keep their sentinel (:23, :271-287). Both prefill kernels (LDS-tiled and
@@ -15,10 +16,9 @@ import torch
 
 import attn_cases as A
 import oracle
+from gates import element_gate
 
 pytestmark = pytest.mark.gpu
-
-TOL = 2e-3
 
 
 @pytest.fixture(autouse=True, params=["lds", "direct"])
@@ -85,10 +85,45 @@ def test_corpus_segments_and_owners_match_oracle(gpu, dev, case):
     for runner in (run_segments, run_owners):
         d.reset()
         runner(gpu, d)
-        got = d.result()
-        errs.append(float(np.abs(got - want).max()))
+        errs.append(element_gate(d.result(), want, f"{case.name} {runner.__name__}"))
     print(f"{case.name}: segments {errs[0]:.3e} owners {errs[1]:.3e}")
-    assert max(errs) <= TOL
+
+
+FUZZ = A.fuzz_cases()
+_FUZZ_ORACLE = {}
+
+
+def _fuzz_oracle():
+    """f64 oracle outputs of the 64 fuzz cases, computed once per session on up to 16 host
+    threads (the C oracle releases the interpreter lock)."""
+    if not _FUZZ_ORACLE:
+        import concurrent.futures
+        import os
+
+        workers = max(1, min(16, len(os.sched_getaffinity(0))))
+        with concurrent.futures.ThreadPoolExecutor(workers) as ex:
+            outs = list(ex.map(lambda c: A.oracle_out(A.fixture(c)), FUZZ))
+        _FUZZ_ORACLE.update({c.name: o for c, o in zip(FUZZ, outs)})
+    return _FUZZ_ORACLE
+
+
+@pytest.mark.timeout(300)
+def test_fuzz_corpus_matches_oracle(gpu, dev):
+    """The reference's 64 fuzz cases (seed 20260908: 1..16 requests of up to 257 rows at
+    random starts, the four Q profiles) through the segment and owners forms; every element
+    against the f64 oracle. The reference checks its fuzz cases only against its own
+    reference kernel; here the oracle covers every element."""
+    want_all = _fuzz_oracle()
+    worst = 0.0
+    for case in FUZZ:
+        fx = A.fixture(case)
+        d = Device(fx, dev)
+        for runner in (run_segments, run_owners):
+            d.reset()
+            runner(gpu, d)
+            worst = max(worst, element_gate(d.result(), want_all[case.name],
+                                            f"{case.name} {runner.__name__}"))
+    print(f"fuzz corpus ({len(FUZZ)} cases): max-abs {worst:.3e}")
 
 
 @pytest.mark.parametrize("case", [c for c in CASES if c.name.startswith("boundary-")],
@@ -151,7 +186,7 @@ def test_single_sequence_params_and_contiguous_forms(gpu, dev):
                                     A.HEADS, A.KV_HEADS, A.HD, A.LAYERS, A.LAYER, A.KD,
                                     A.CONTEXT, params)
         got = d.result()[:rows]
-        assert np.abs(got - want[:rows]).max() <= TOL
+        element_gate(got, want[:rows], f"{case.name} params form")
         # contiguous cache holding the same history for that request at layer 1
         cap = A.CONTEXT
         k_c = np.zeros(A.LAYERS * cap * A.KD, np.uint16)
@@ -213,7 +248,7 @@ def test_fp16_query_and_fp16_output(gpu, dev):
                                 len(case.slices), fx.max_chunk, A.STRIDE, A.HEADS, A.KV_HEADS,
                                 A.HD, A.LAYERS, A.LAYER, A.KD)
     torch.cuda.synchronize()
-    assert np.abs(out16.float().cpu().numpy() - want).max() <= TOL + 2e-3
+    element_gate(out16.float().cpu().numpy(), want, "fp16 query and output", out_f16=True)
 
 
 def _packed_config_check(gpu, dev, cfg, seed):
@@ -248,9 +283,8 @@ def _packed_config_check(gpu, dev, cfg, seed):
                                        positions + 1, table_index=owners, n_head=cfg.n_head,
                                        n_kv_head=cfg.n_kv_head, head_dim=64, table_stride=stride,
                                        n_layer=cfg.n_layer, layer=0)
-    err = float(np.abs(out.cpu().numpy() - want).max())
+    err = element_gate(out.cpu().numpy(), want, cfg.name)
     print(f"{cfg.name}: max-abs {err:.3e}")
-    assert err <= TOL
 
 
 def test_config1_causal_prefill_512(gpu, dev):

@@ -148,3 +148,58 @@ def test_normal_generator_matches_numpy_restatement():
     assert abs(float(got.mean())) < 0.02 and abs(float(got.std()) - 1.0) < 0.02
     h = oracle.normal_f16(20260908, 1000)
     assert np.array_equal(h, oracle.f32_to_f16_bits(oracle.normal_f32(20260908, 1000)))
+
+
+def test_cpu_baseline_paths_compute_attention():
+    """The CPU baseline (oracle/cpu_path.py) on explicit inputs: its decode step appends the
+    rows and attends exactly what the f64 oracle computes on the same values, and its
+    prefill is causal attention per sequence."""
+    import torch
+
+    from oracle import cpu_path
+
+    rng = np.random.default_rng(3)
+    n_layer, n_head, n_kv, hd = 2, 4, 2, 64
+    kv = n_kv * hd
+    lens = np.array([5, 33, 16])
+    pages = [-(-int(n) // 16) for n in lens]
+    n_pages = sum(pages)
+    k_pages = rng.standard_normal((n_pages, n_layer, 16, kv)).astype(np.float16)
+    v_pages = rng.standard_normal((n_pages, n_layer, 16, kv)).astype(np.float16)
+    tables = []
+    cur = 0
+    for n in pages:
+        tables.append(np.arange(cur, cur + n))
+        cur += n
+    q = rng.standard_normal((n_layer, 3, n_head * hd)).astype(np.float16)
+    src_k = rng.standard_normal((n_layer, 3, kv)).astype(np.float32)
+    src_v = rng.standard_normal((n_layer, 3, kv)).astype(np.float32)
+    cpu = cpu_path.DecodeBatchCPU(lens, n_layer, n_head, n_kv, k_pages, v_pages, tables, q,
+                                  src_k, src_v)
+    outs = cpu.step()
+    for layer in range(n_layer):
+        for b, n in enumerate(lens):
+            k = k_pages[tables[b], layer].reshape(-1, kv)[:n].astype(np.float32)
+            v = v_pages[tables[b], layer].reshape(-1, kv)[:n].astype(np.float32)
+            k[n - 1] = src_k[layer, b].astype(np.float16)
+            v[n - 1] = src_v[layer, b].astype(np.float16)
+            want = oracle.attention_dense(q[layer, b:b + 1].astype(np.float32), k, v, [int(n)],
+                                          n_head, n_kv, hd)
+            got = outs[layer * 3 + b].reshape(n_head * hd).numpy()
+            assert np.abs(got - want[0]).max() < 1e-5
+    seq = [7, 20]
+    qp = rng.standard_normal((27, n_head * hd)).astype(np.float32)
+    kp = rng.standard_normal((27, kv)).astype(np.float32)
+    vp = rng.standard_normal((27, kv)).astype(np.float32)
+    pre = cpu_path.PrefillCPU(seq, n_head, n_kv, qp, kp, vp).step()
+    start = 0
+    for i, n in enumerate(seq):
+        sl = slice(start, start + n)
+        want = oracle.attention_dense(qp[sl], kp[sl], vp[sl], np.arange(1, n + 1), n_head, n_kv,
+                                      hd)
+        got = pre[i][0].transpose(0, 1).reshape(n, n_head * hd).numpy()
+        assert np.abs(got - want).max() < 1e-5
+        start += n
+    reps, t = cpu_path.time_median(lambda: None, 0.0)
+    assert reps == 20 and t >= 0.0
+    assert isinstance(cpu_path.cpu_model(), str)

@@ -11,9 +11,14 @@ from crucible_amd.paged import PagePool, SequencePages, request_page_reservation
     segments_from_cu_seqlens
 
 
-def test_reference_paging_kats_pass():
-    """engine/src/paged.rs:244-496 and prefill.rs:394-453, ported to C++ (paging_kat.cpp)."""
-    path = _build.KAT_PATH if os.path.exists(_build.KAT_PATH) else _build.build_paging_kat()
+def test_reference_paging_kats_pass(tmp_path):
+    """engine/src/paged.rs:244-496 and prefill.rs:394-453, ported to C++ (tests/paging_kat.cpp),
+    built here with g++ against the library's host allocator source (no HIP)."""
+    here = os.path.dirname(os.path.abspath(__file__))
+    path = str(tmp_path / "paging_kat")
+    subprocess.run([os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-Wall", "-Wextra",
+                    "-I", _build.CSRC, os.path.join(here, "paging_kat.cpp"), os.path.join(_build.CSRC, "paging.cpp"),
+                    "-o", path], check=True, capture_output=True, text=True)
     proc = subprocess.run([path], capture_output=True, text=True, timeout=60)
     assert proc.returncode == 0, proc.stdout + proc.stderr
     assert "19 tests, 0 failed" in proc.stdout

@@ -57,7 +57,7 @@ constexpr TuneKey kTuneKeys[CRUCIBLE_TUNE_COUNT] = {
     {"CRUCIBLE_PREFILL_HEAVY_FIRST", 0, 1},   // longest-first grid off / on
     {"CRUCIBLE_PREFILL_QB", 1, 2},            // 16-row blocks per wave
     {"CRUCIBLE_PREFILL_BUFS", 4, 6},          // key tiles in the LDS ring: 4 or 6
-    {"CRUCIBLE_LINEAR_TILE", 4, 16},          // projection tile columns: 4 or 16
+    {"CRUCIBLE_LINEAR_TILE", 4, 32},          // projection tiles: 4, 16 or 32 (see below)
     {"CRUCIBLE_DECODE_COMBINE_WIDTH", 8, 16}, // splits merged per round trip: 8 or 16
 };
 
@@ -66,7 +66,7 @@ bool tune_value_ok(int key, int v) {
         case CRUCIBLE_TUNE_DECODE_PAGES: return v == 1 || v == 2 || v == 4;
         case CRUCIBLE_TUNE_DECODE_WAVES: return v == 4 || v == 8;
         case CRUCIBLE_TUNE_PREFILL_BUFS: return v == 4 || v == 6;
-        case CRUCIBLE_TUNE_LINEAR_TILE: return v == 4 || v == 16;
+        case CRUCIBLE_TUNE_LINEAR_TILE: return v == 4 || v == 16 || v == 32;
         case CRUCIBLE_TUNE_DECODE_COMBINE_WIDTH: return v == 8 || v == 16;
         default: return v >= kTuneKeys[key].lo && v <= kTuneKeys[key].hi;
     }

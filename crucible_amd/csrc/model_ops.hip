@@ -625,6 +625,209 @@ __global__ __launch_bounds__(kLinThreads) void linear_wide_kernel(LinArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- prompt-sized products
+
+// Products over a whole prompt batch (thousands of rows; the reference's prefill runs them
+// as WMMA GEMMs, kernels.cu:2402-2526) are bound by the f64 MFMA itself: a 16x16x4 step
+// occupies a SIMD for 64 cycles, so 16 bytes of operands per lane every 64 cycles keep it
+// busy, and no LDS staging is needed. The decode tilings (16-row tiles, the K range split
+// over 8 waves, every weight read once per 16 rows) give way to output tiles: each wave
+// owns RB x CB MFMA blocks (RB*16 rows x CB*16 columns) over the whole K range, so no sum
+// crosses waves and each output is one wave's fixed-order f64 sum. Operands come from L2
+// straight into registers, two 32-wide K chunks ahead of the MFMAs.
+//
+// The waves of a workgroup share their rows (and the fused norm's row scales) and take
+// adjacent column ranges. Workgroup L runs on XCD L % 8; XCD x takes tiles
+// [x * per_xcd, (x + 1) * per_xcd) in row-major order, so each XCD's L2 holds one slice of
+// the rows plus the weights, instead of every XCD fetching every row.
+constexpr int kGemmWaves = 4;
+constexpr int kGemmThreads = 64 * kGemmWaves;
+constexpr int kGemmMinRows = 128;  // below this the decode tilings are used
+
+template <int RB, int CB, bool NORM>
+struct GemmChunk {
+    float4_t x[RB][2];
+    half8_t w[CB];
+    float4_t nw[NORM ? 2 : 1];  // the norm weights of the chunk's K range (NORM only)
+};
+
+template <bool NORM, int MODE, int RB, int CB>
+__global__ __launch_bounds__(kGemmThreads, 2) void linear_gemm_kernel(LinArgs a, int col_tiles,
+                                                                      int n_tiles, int per_xcd) {
+    static_assert(MODE != kSwiGLU || CB % 2 == 0, "SwiGLU pairs each gate block with its up block");
+    constexpr int ROWS = RB * 16;
+    // a wave's output columns: CB blocks, or CB / 2 gate blocks beside their up blocks
+    constexpr int NBLK = MODE == kSwiGLU ? CB / 2 : CB;
+    __shared__ double s_scale[ROWS];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int col = lane & 15, g = lane >> 4;
+    const int L = blockIdx.x;
+    const int t = (L & 7) * per_xcd + (L >> 3);
+    if (t >= n_tiles) return;  // uniform over the workgroup
+    const int rt = t / col_tiles;
+    const int m0 = rt * ROWS;
+    const int n0 = ((t - rt * col_tiles) * kGemmWaves + wave) * NBLK * 16;
+
+    if constexpr (NORM) {
+        // f64 sums of squares of the workgroup's rows: TPR threads a row over interleaved
+        // float4s, 8 loads in flight; rows past the end get sum 0 (their outputs are not
+        // stored)
+        constexpr int TPR = kGemmThreads / ROWS;
+        const int r = tid / TPR, q = tid % TPR;
+        const int row = m0 + r;
+        double ss = 0.0;
+        if (row < a.rows) {
+            const float4_t* xr = reinterpret_cast<const float4_t*>(a.x + (int64_t)row * a.ldx);
+            const int n4 = a.k_in / 4;
+            for (int i0 = q; i0 < n4; i0 += TPR * 8) {
+                float4_t v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    v[i] = (i0 + TPR * i < n4) ? xr[i0 + TPR * i] : float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const double d = (double)v[i][e];
+                        ss += d * d;
+                    }
+            }
+        }
+#pragma unroll
+        for (int off = TPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, TPR);
+        if (q == 0) s_scale[r] = 1.0 / sqrt(ss / (double)a.k_in + a.eps);
+        __syncthreads();
+    }
+    if (n0 >= a.n_out) return;
+
+    // Lane (col, g) feeds row m0 + 16 rb + col of A and column 16 cb + col of B with
+    // k = k0 + 8 g + i at MFMA step i of a 32-wide chunk. Rows and columns past the end
+    // read the last valid one: an MFMA output depends only on its own row and column, and
+    // those outputs are not stored.
+    const float* xp[RB];
+    double scale[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int row = m0 + 16 * rb + col;
+        xp[rb] = a.x + (int64_t)(row < a.rows ? row : a.rows - 1) * a.ldx + 8 * g;
+        scale[rb] = NORM ? s_scale[16 * rb + col] : 1.0;
+    }
+    const half_t* wp[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+        const half_t* base = (MODE == kSwiGLU && cb >= NBLK) ? a.w2 : a.w;
+        const int n = n0 + 16 * (cb % NBLK) + col;
+        wp[cb] = base + (int64_t)(n < a.n_out ? n : a.n_out - 1) * a.k_in + 8 * g;
+    }
+    const float* nwp = NORM ? a.norm_w + 8 * g : nullptr;
+
+    // the residual is requested first, so its round trip is long over by the epilogue
+    // (out may alias resid: each element is read and written by the same lane)
+    float rv[RB][NBLK][4];
+    if constexpr (MODE == kResidual) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < NBLK; ++cb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = min(m0 + 16 * rb + g + 4 * r, a.rows - 1);
+                    const int n = min(n0 + 16 * cb + col, a.n_out - 1);
+                    rv[rb][cb][r] = a.resid[(int64_t)row * a.ldo + n];
+                }
+    }
+
+    using Chunk = GemmChunk<RB, CB, NORM>;
+    auto load = [&](int k0, Chunk& c) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            c.x[rb][0] = *reinterpret_cast<const float4_t*>(xp[rb] + k0);
+            c.x[rb][1] = *reinterpret_cast<const float4_t*>(xp[rb] + k0 + 4);
+        }
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) c.w[cb] = *reinterpret_cast<const half8_t*>(wp[cb] + k0);
+        if constexpr (NORM) {
+            c.nw[0] = *reinterpret_cast<const float4_t*>(nwp + k0);
+            c.nw[1] = *reinterpret_cast<const float4_t*>(nwp + k0 + 4);
+        }
+    };
+
+    double4_t acc[RB][CB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = double4_t{0.0, 0.0, 0.0, 0.0};
+
+    auto feed = [&](const Chunk& c) {
+        double av[RB][8];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            float xs[8] = {c.x[rb][0][0], c.x[rb][0][1], c.x[rb][0][2], c.x[rb][0][3],
+                           c.x[rb][1][0], c.x[rb][1][1], c.x[rb][1][2], c.x[rb][1][3]};
+            if constexpr (NORM) {
+                const float nw[8] = {c.nw[0][0], c.nw[0][1], c.nw[0][2], c.nw[0][3],
+                                     c.nw[1][0], c.nw[1][1], c.nw[1][2], c.nw[1][3]};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xs[i] = (float)((double)xs[i] * scale[rb]) * nw[i];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) av[rb][i] = (double)xs[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            double bv[CB];
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) bv[cb] = (double)(float)c.w[cb][i];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = mfma_f64(av[rb][i], bv[cb], acc[rb][cb]);
+        }
+    };
+
+    // Two chunks in flight, reloaded in place: the loads are unconditional (the last
+    // iteration re-reads the final pair, unused), so each buffer keeps its registers
+    // across the loop and the wait before a feed counts only the other buffer's loads.
+    // k_in is a multiple of 64.
+    Chunk c0, c1;
+    load(0, c0);
+    __builtin_amdgcn_sched_barrier(0);  // c0's loads before c1's, as in the loop
+    load(32, c1);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int k0 = 0; k0 < a.k_in; k0 += 64) {
+        feed(c0);
+        __builtin_amdgcn_sched_barrier(0);
+        load(min(k0 + 64, a.k_in - 64), c0);
+        __builtin_amdgcn_sched_barrier(0);
+        feed(c1);
+        __builtin_amdgcn_sched_barrier(0);
+        load(min(k0 + 96, a.k_in - 32), c1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // lane (col, g) holds rows 16 rb + g + 4 r, column 16 cb + col of the wave's blocks
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < NBLK; ++cb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + 16 * rb + g + 4 * r;
+                const int n = n0 + 16 * cb + col;
+                if (row >= a.rows || n >= a.n_out) continue;
+                float* dst = a.out + (int64_t)row * a.ldo + n;
+                if constexpr (MODE == kSwiGLU) {
+                    const float gf = (float)acc[rb][cb][r];
+                    *dst = gf / (1.0f + expf(-gf)) * (float)acc[rb][cb + NBLK][r];
+                } else if constexpr (MODE == kResidual) {
+                    *dst = rv[rb][cb][r] + (float)acc[rb][cb][r];
+                } else {
+                    *dst = (float)acc[rb][cb][r];
+                }
+            }
+}
+
 // ---------------------------------------------------------------- RMSNorm rows
 
 constexpr int kNormThreads = 256;
@@ -706,6 +909,30 @@ void launch_linear4(const LinArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((linear4_kernel<NORM, MODE>), grid, dim3(kLinThreads), 0, stream, a);
 }
 
+template <bool NORM, int MODE, int RB, int CB>
+void launch_gemm(const LinArgs& a, hipStream_t stream) {
+    constexpr int wg_cols = (MODE == kSwiGLU ? CB / 2 : CB) * 16 * kGemmWaves;
+    const int col_tiles = (a.n_out + wg_cols - 1) / wg_cols;
+    const int n_tiles = col_tiles * ((a.rows + RB * 16 - 1) / (RB * 16));
+    const int per_xcd = (n_tiles + 7) / 8;
+    hipLaunchKernelGGL((linear_gemm_kernel<NORM, MODE, RB, CB>), dim3((unsigned)(8 * per_xcd)),
+                       dim3(kGemmThreads), 0, stream, a, col_tiles, n_tiles, per_xcd);
+}
+
+// Output-tiled products for prompt-sized row counts (k_in a multiple of 64);
+// CRUCIBLE_TUNE_LINEAR_TILE = 32 forces them, 4 or 16 the decode tilings.
+bool use_gemm(int64_t rows, int64_t k_in) {
+    if (k_in % 64 != 0) return false;
+    if (const int v = tuning(CRUCIBLE_TUNE_LINEAR_TILE); v > 0) return v == 32;
+    return rows >= kGemmMinRows;
+}
+
+template <int MODE>
+void launch_gemm_mode(const LinArgs& a, hipStream_t stream) {
+    if (a.norm_w) launch_gemm<true, MODE, 2, 2>(a, stream);
+    else launch_gemm<false, MODE, 2, 2>(a, stream);
+}
+
 // 4-column tiles where 16-column tiles would leave CUs without a workgroup and no norm is
 // fused (the decode step's o and down projections: 5.16 -> 4.84 and 10.2 -> 8.9 us).
 // With a fused norm every workgroup loads and normalises the whole rows, and four times
@@ -750,6 +977,11 @@ extern "C" int crucible_linear_f64acc(const float* x, int64_t ldx, const float* 
     LinArgs a{x, ldx, norm_w, (double)eps, static_cast<const half_t*>(w), nullptr, resid, out,
               ldo, (int)rows, (int)n_out, (int)k_in};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (use_gemm(rows, k_in)) {
+        if (resid) launch_gemm_mode<kResidual>(a, s);
+        else launch_gemm_mode<kPlain>(a, s);
+        return fail_launch(what);
+    }
     // Wide outputs (the vocabulary projection): the persistent tile walk when the K range
     // fits its registers, else 4 column blocks per workgroup so each activation fragment
     // feeds 4 MFMAs; narrow ones keep a workgroup per 16 columns.
@@ -821,6 +1053,10 @@ extern "C" int crucible_linear_swiglu_f64acc(const float* x, int64_t ldx, const 
               static_cast<const half_t*>(w_up), nullptr, out, ldo, (int)rows, (int)hidden,
               (int)k_in};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (use_gemm(rows, k_in)) {
+        launch_gemm_mode<kSwiGLU>(a, s);
+        return fail_launch(what);
+    }
     if (use_tile4(hidden, rows, 8, norm_w != nullptr)) {
         if (norm_w) launch_linear4<true, kSwiGLU>(a, s);
         else launch_linear4<false, kSwiGLU>(a, s);

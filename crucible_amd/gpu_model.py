@@ -248,9 +248,13 @@ class GpuModel:
         d_own = torch.from_numpy(owners).to(dev)
         d_pos = torch.from_numpy(positions).to(dev)
         tok = torch.from_numpy(np.concatenate([np.asarray(p, np.int64) for p in prompts])).to(dev)
+        x = self.tok_emb.index_select(0, tok)
+        if self.precision == "reference":
+            # this library's projections (f64-accumulated, norms, RoPE, SwiGLU and the
+            # residual adds fused as in the decode step) over every prompt row
+            return self._prefill_native(prompts, x, cu, d_tables, d_seg, d_own, d_pos, max_chunk)
         cos = self.rope_cos.index_select(0, d_pos)
         sin = self.rope_sin.index_select(0, d_pos)
-        x = self.tok_emb.index_select(0, tok)
         attn = torch.empty((rows, cfg.n_embd), dtype=torch.float32, device=dev)
         for layer_i, layer in enumerate(self.layers):
             q, k, v = self._qkv(x, layer, cos, sin)
@@ -265,6 +269,46 @@ class GpuModel:
             x = self._mlp(x, layer)
         last = torch.from_numpy(cu[1:] - 1).long().to(dev)
         logits = self._logits(x.index_select(0, last)).contiguous()
+        first = torch.empty(len(prompts), dtype=torch.int32, device=dev)
+        gpu.argmax_rows(logits, first, len(prompts), cfg.vocab_size)
+        return first, logits
+
+    def _prefill_native(self, prompts, x, cu, d_tables, d_seg, d_own, d_pos, max_chunk):
+        """The packed prefill as this library's kernels (the reference CPU arithmetic of
+        model.rs:145-299 over all prompt rows at once): per layer the q/k/v projection with
+        the attention RMSNorm fused, RoPE and the q/k/v split, both packed appends, the tiled
+        prefill attention, the o projection with the residual add, the gate/up projection
+        with the MLP norm and SwiGLU, and the down projection with the residual add; then the
+        vocabulary projection of each prompt's last row with the final norm fused."""
+        cfg, gpu, dev = self.cfg, self.gpu, self.dev
+        rows = x.shape[0]
+        eps = float(np.float32(cfg.norm_eps))
+        d, kv = cfg.n_embd, cfg.kv_dim
+        qkv = torch.empty((rows, d + 2 * kv), dtype=torch.float32, device=dev)
+        q = torch.empty((rows, d), dtype=torch.float32, device=dev)
+        k = torch.empty((rows, kv), dtype=torch.float32, device=dev)
+        v = torch.empty((rows, kv), dtype=torch.float32, device=dev)
+        attn = torch.empty((rows, d), dtype=torch.float32, device=dev)
+        act = torch.empty((rows, cfg.hidden), dtype=torch.float32, device=dev)
+        x = x.contiguous()
+        for layer_i, layer in enumerate(self.layers):
+            gpu.linear_f64acc(x, layer["wqkv"], qkv, norm_w=layer["attn_norm"], eps=eps)
+            gpu.rope_split_qkv(qkv, q, k, v, self.rope_cos, self.rope_sin, d_pos, cfg.n_head,
+                               cfg.n_kv_head)
+            for src, pool, kind in ((k, self.k_pool, "k"), (v, self.v_pool, "v")):
+                gpu.cache_store_packed_paged(src, pool, d_tables, d_own, d_pos, rows, kv,
+                                             self.table_stride, cfg.n_layer, layer_i, kind=kind)
+            gpu.attention_prefill_tiled(q, self.k_pool, self.v_pool, None, None, attn, d_tables,
+                                        d_seg, len(prompts), max_chunk, self.table_stride,
+                                        cfg.n_head, cfg.n_kv_head, 64, cfg.n_layer, layer_i, kv)
+            gpu.linear_f64acc(attn, layer["wo"], x, resid=x)
+            gpu.linear_swiglu_f64acc(x, layer["wg"], layer["wu"], act, norm_w=layer["mlp_norm"],
+                                     eps=eps)
+            gpu.linear_f64acc(act, layer["wd"], x, resid=x)
+        last = torch.from_numpy(cu[1:] - 1).long().to(dev)
+        xl = x.index_select(0, last).contiguous()
+        logits = torch.empty((len(prompts), cfg.vocab_size), dtype=torch.float32, device=dev)
+        gpu.linear_f64acc(xl, self.lm_head, logits, norm_w=self.final_norm, eps=eps)
         first = torch.empty(len(prompts), dtype=torch.int32, device=dev)
         gpu.argmax_rows(logits, first, len(prompts), cfg.vocab_size)
         return first, logits

@@ -13,6 +13,12 @@
  *   - Per-step values (positions, lengths, page tables, params) are read from
  *     device memory, never passed by value, so hipGraph capture of a step stays
  *     valid across replays (kernels.cu:17-35 in the reference).
+ *   - Read-only metadata: page tables, seq_lens, positions, owners, segments and
+ *     params are read through the scalar (constant) cache, which does not see
+ *     writes made during the same launch. They must stay unchanged while a launch
+ *     runs and must not overlap `out`, the pools, the workspace or any other buffer
+ *     the launch writes. The library checks none of this; an overlap gives stale
+ *     reads, not a fault.
  *   - Return value: CRUCIBLE_OK (0) or an error code. Argument validation
  *     happens before any launch; on error nothing is enqueued. The message of
  *     the last error on the calling thread is available from
@@ -79,7 +85,7 @@ enum crucible_tuning_key {
     CRUCIBLE_TUNE_PREFILL_HEAVY_FIRST = 4, /* prefill longest-first grid: 0, 1 */
     CRUCIBLE_TUNE_PREFILL_QB = 5,          /* prefill 16-row blocks per wave: 1, 2 */
     CRUCIBLE_TUNE_PREFILL_BUFS = 6,        /* prefill LDS ring depth in key tiles: 4, 6 */
-    CRUCIBLE_TUNE_LINEAR_TILE = 7,         /* projection tile columns: 4, 16 */
+    CRUCIBLE_TUNE_LINEAR_TILE = 7,         /* projection tiles: 4 or 16 columns (decode), 32 (prompt rows) */
     CRUCIBLE_TUNE_DECODE_COMBINE_WIDTH = 8, /* decode splits merged per round trip: 8, 16 */
     CRUCIBLE_TUNE_COUNT = 9
 };
@@ -137,7 +143,20 @@ int crucible_cache_store_packed_paged(const void* src, int src_dtype, void* pool
  * combine of the splits: zero the workspace once when it is allocated; every
  * launch leaves the counters zeroed again. Calls of any batch size may share one
  * workspace, one launch at a time (launches that share it must be ordered, e.g.
- * on one stream).
+ * on one stream). Two launches that run at once on one workspace (two streams
+ * without an event between them) race on the counters and partials: a split can
+ * count toward the other launch's combine, which then merges partials that are
+ * not yet written or belong to the other call. The result is wrong output, and a
+ * counter left nonzero that corrupts later launches too; nothing detects it. Give
+ * each stream its own workspace.
+ *
+ * Ordering of the in-kernel combine: each split writes its partial with
+ * agent-coherent (sc1) stores, which bypass the non-coherent per-XCD L2 state, and
+ * waits for their acknowledgement (s_waitcnt vmcnt(0)) before one lane increments
+ * the counter; the workgroup that completes the count reads the partials with sc1
+ * loads, which miss any stale line. The wait is a hardware ordering point, not a
+ * C++ fence; the cross-order and repeated-launch bit-identity tests guard it.
+ * Verified with the ROCm 7.2 hipcc (AMD clang 22) of this build.
  */
 
 size_t crucible_attention_decode_workspace_bytes(int64_t batch, int64_t n_head,

@@ -41,7 +41,9 @@ def _mat(rng, shape, std):
     return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float16)
 
 
-TILES = ["auto", "4", "16"]  # linear_tile tuning: the launcher's choice, or forced
+# linear_tile tuning: the launcher's choice, or forced: 4 or 16 columns (the decode
+# tilings), 32 (the output-tiled products of prompt-sized batches; k_in % 64 == 0 only)
+TILES = ["auto", "4", "16", "32"]
 
 
 @pytest.mark.parametrize("rows,n_out,k_in", [(1, 1152, 768), (16, 768, 768), (5, 200, 2048),
@@ -52,7 +54,7 @@ TILES = ["auto", "4", "16"]  # linear_tile tuning: the launcher's choice, or for
 @pytest.mark.parametrize("tile", TILES)
 def test_linear_matches_f64_matvec(gpu, dev, tune, rows, n_out, k_in, norm, tile):
     if tile != "auto":
-        if n_out >= 16 * 1024:
+        if n_out >= 16 * 1024 and tile != "32":
             pytest.skip("the vocabulary-sized outputs take the persistent wide kernel")
         tune(linear_tile=tile)
     rng = np.random.default_rng(rows * 7 + n_out + k_in + norm)
@@ -91,7 +93,8 @@ def test_linear_residual_in_place(gpu, dev, tune, tile):
     assert np.abs(got - want).max() <= 4 * np.abs(want).max() * 2.0 ** -24
 
 
-@pytest.mark.parametrize("rows,hidden,k_in", [(16, 2048, 768), (5, 2045, 96), (21, 130, 1056)])
+@pytest.mark.parametrize("rows,hidden,k_in", [(16, 2048, 768), (5, 2045, 96), (21, 130, 1056),
+                                             (37, 1000, 704)])
 @pytest.mark.parametrize("tile", TILES)
 def test_swiglu_matches_reference_ops(gpu, dev, tune, rows, hidden, k_in, tile):
     if tile != "auto":
@@ -150,3 +153,49 @@ def test_rope_split_is_exact(gpu, dev):
     assert np.array_equal(q.cpu().numpy(), rot(qkv[:, :d], nh))
     assert np.array_equal(k.cpu().numpy(), rot(qkv[:, d:d + nkv * 64], nkv))
     assert np.array_equal(v.cpu().numpy(), qkv[:, d + nkv * 64:])
+
+
+@pytest.mark.parametrize("rows", [1003, 2304, 4713])
+def test_prefill_sized_projections_keep_the_f64_contract(gpu, dev, rows):
+    """The packed prefill runs the same projections over every prompt row at once (config 5:
+    about 4,600 rows): q/k/v with the attention norm fused, o and down with the residual add,
+    gate/up with SwiGLU, at the 120m preset's shapes, each against numpy float64."""
+    rng = np.random.default_rng(rows)
+    d, kv, hidden = 768, 192, 2048
+    x = rng.standard_normal((rows, d), dtype=np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    wqkv = _mat(rng, (d + 2 * kv, d), 0.02)
+    h = _rms_ref(x, nw).astype(np.float64)
+    want = (h @ wqkv.astype(np.float64).T).astype(np.float32)
+    out = torch.empty((rows, d + 2 * kv), dtype=torch.float32, device=dev)
+    dx = torch.from_numpy(x).to(dev)
+    gpu.linear_f64acc(dx, torch.from_numpy(wqkv).to(dev), out, norm_w=torch.from_numpy(nw).to(dev),
+                      eps=float(EPS))
+    _assert_f64_contract(out.cpu().numpy(), want, f"qkv {rows} rows")
+    again = torch.empty_like(out)
+    gpu.linear_f64acc(dx, torch.from_numpy(wqkv).to(dev), again,
+                      norm_w=torch.from_numpy(nw).to(dev), eps=float(EPS))
+    assert torch.equal(out, again), "not deterministic"
+    # o projection with the residual add in place
+    wo = _mat(rng, (d, d), 0.02)
+    a = rng.standard_normal((rows, d), dtype=np.float32)
+    y = (a.astype(np.float64) @ wo.astype(np.float64).T).astype(np.float32)
+    res = dx.clone()
+    gpu.linear_f64acc(torch.from_numpy(a).to(dev), torch.from_numpy(wo).to(dev), res, resid=res)
+    _assert_f64_contract(res.cpu().numpy() - x, (x + y) - x, f"o + residual {rows} rows")
+    # gate/up with SwiGLU, then down
+    wg = _mat(rng, (hidden, d), 0.05)
+    wu = _mat(rng, (hidden, d), 0.05)
+    g = (h @ wg.astype(np.float64).T).astype(np.float32)
+    u = (h @ wu.astype(np.float64).T).astype(np.float32)
+    want_act = (g / (np.float32(1.0) + np.exp(-g))) * u
+    act = torch.empty((rows, hidden), dtype=torch.float32, device=dev)
+    gpu.linear_swiglu_f64acc(dx, torch.from_numpy(wg).to(dev), torch.from_numpy(wu).to(dev), act,
+                             norm_w=torch.from_numpy(nw).to(dev), eps=float(EPS))
+    got_act = act.cpu().numpy()
+    assert np.all(np.abs(got_act - want_act) <= 8 * 2.0 ** -24 * np.abs(want_act) + 1e-30)
+    wd = _mat(rng, (d, hidden), 0.02)
+    want_d = (got_act.astype(np.float64) @ wd.astype(np.float64).T).astype(np.float32)
+    down = torch.empty((rows, d), dtype=torch.float32, device=dev)
+    gpu.linear_f64acc(act, torch.from_numpy(wd).to(dev), down)
+    _assert_f64_contract(down.cpu().numpy(), want_d, f"down {rows} rows")

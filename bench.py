@@ -441,18 +441,21 @@ def copy_bandwidth(dev, mib: int = 256, reps: int = 10):
     return 2 * (mib << 20) / (ms * 1e-3) / 1e9
 
 
+# What the decode kernel is built from: its translation unit, the headers it includes and
+# the build script that holds its compiler flags.
+DECODE_SOURCES = ("crucible_amd/csrc/attn_decode.hip", "crucible_amd/csrc/common.hpp",
+                  "include/crucible_attn.h", "crucible_amd/_build.py")
+
+
 def source_sha() -> str:
-    """Hash of the library sources (csrc and the C header): a profile summary applies to the
-    kernels built from exactly these."""
+    """Hash of the decode kernel's sources and build flags: a profile summary applies to the
+    kernel built from exactly these."""
     import hashlib
 
     h = hashlib.sha256()
-    csrc = os.path.join(ROOT, "crucible_amd", "csrc")
-    for name in sorted(os.listdir(csrc)):
-        with open(os.path.join(csrc, name), "rb") as f:
+    for name in DECODE_SOURCES:
+        with open(os.path.join(ROOT, name), "rb") as f:
             h.update(name.encode() + b"\0" + f.read())
-    with open(os.path.join(ROOT, "include", "crucible_attn.h"), "rb") as f:
-        h.update(f.read())
     return h.hexdigest()[:16]
 
 

@@ -313,7 +313,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
     const uint64_t mask1 = R > 64 ? s_mask[1] : 0;
     if (mask0 == 0 && mask1 == 0) return;  // uniform: no row of this tile is valid
 
-    // ---- per-lane query state for each 16-row block
+    // ---- per-lane query state for each 16-row block (the query rows load after the first
+    // run's leading tiles are issued, below, so the two round trips overlap)
     const int64_t ld_q = (int64_t)a.n_head * kHeadDim;
     half8_t qh[QB][2], ql[QB][2];
     float m[QB], l[QB];
@@ -329,7 +330,11 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
 #pragma unroll
         for (int db = 0; db < 4; ++db) acc[qb][db] = float4_t{0.f, 0.f, 0.f, 0.f};
         qh[qb][0] = qh[qb][1] = ql[qb][0] = ql[qb][1] = half8_t{};
-        if (my_row[qb] >= 0) {
+    }
+    auto load_queries = [&]() {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            if (my_row[qb] < 0) continue;
             const int64_t off = (int64_t)my_row[qb] * ld_q + (int64_t)h * kHeadDim + 8 * grp;
             if constexpr (QF32) {
                 const float* qp = static_cast<const float*>(a.q) + off;
@@ -347,12 +352,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                 qh[qb][1] = *reinterpret_cast<const half8_t*>(qp + 32);
             }
         }
-    }
+    };
 
     const int kv_dim = a.addr.kv_dim;
-    // The query operands are complete before the first tile load is issued, so no wait
-    // for them can land inside the tile loop (where it would also wait for the tiles).
-    __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+    typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
 
     // ---- runs of one owner (the values come from LDS: readfirstlane makes the compiler
     // treat them as the wave-uniform values they are, so page ids load as scalars)
@@ -361,10 +364,14 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
     // runs (one per request) and are scanned row by row.
     const int first_valid = mask0 ? __builtin_ctzll(mask0) : 64 + __builtin_ctzll(mask1);
     const int last_valid = mask1 ? 127 - __builtin_clzll(mask1) : 63 - __builtin_clzll(mask0);
+    const int wlo = rs * WROWS, whi = rs * WROWS + WROWS;
+    // Wave w stages page w >> 1 of every tile: K rows 8 (w & 1) .. +7 and V^T dims
+    // 32 (w & 1) .. +31 of that page (below), so each wave needs one page id per tile.
+    const int my_page = wave >> 1;
+    bool first_run = true;
     int r0 = a.mode == kOwners ? 0 : first_valid;
     while (r0 < R) {
         int r1, owner, hist_end, wave_last;
-        const int wlo = rs * WROWS, whi = rs * WROWS + WROWS;
         if (a.mode != kOwners) {
             r1 = last_valid + 1;
             owner = s_owner[r0];
@@ -392,46 +399,46 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
 
         // Page ids go through the scalar cache (constant address space): the tables are
         // never written during a launch, and scalar loads (lgkmcnt) never wait on the
-        // in-flight tile loads the way vector loads (vmcnt) would.
-        typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
-        const_i32_ptr table = tables ? (const_i32_ptr)(tables + (int64_t)owner * a.table_stride)
-                                     : nullptr;
+        // in-flight tile loads the way vector loads (vmcnt) would. Without a table
+        // (contiguous cache) the page index is the id; the load then reads a harmless word
+        // of the pool, so it needs no branch.
+        const bool paged = tables != nullptr;
+        const const_i32_ptr table = paged ? (const_i32_ptr)(tables + (int64_t)owner * a.table_stride)
+                                          : (const_i32_ptr)a.k_pool;
         const int n_tiles = (hist_end + kKeyTile - 1) / kKeyTile;
         const int last_page = (hist_end - 1) >> kPageShift;
+        // This wave's page of tile t; pages past the run's last one are clamped to it (in
+        // bounds; their keys are zeroed or masked later).
+        auto page_of = [&](int t) -> int64_t {
+            const int idx = min(4 * t + my_page, last_page);
+            const int id = table[paged ? idx : 0];
+            return paged ? (int64_t)id : (int64_t)idx;
+        };
 
         // Issue tile t into ring buffer t % KB: 2 direct-to-LDS loads per thread.
-        // Page ids past the run's last page are clamped to it (in bounds; masked later).
-        auto issue = [&](int t) {
+        auto issue = [&](int t, int64_t page) {
             const int buf = t % KB;
-            int64_t pg[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int idx = min(t * 4 + j, last_page);
-                pg[j] = table ? (int64_t)table[idx] : (int64_t)idx;
-            }
-            // K: wave w covers keys 8w .. 8w+7 (page w >> 1 of the tile); lane L puts
-            // chunk (L & 7) ^ (row & 7) of its row at chunk position L & 7.
+            const int64_t base = block_base(a.addr, page);
+            // K: wave w covers keys 8w .. 8w+7 of the tile; lane L puts chunk
+            // (L & 7) ^ (row & 7) of its row at chunk position L & 7.
             {
-                const int r0k = 8 * wave;
-                const int row = r0k + (lane >> 3);
+                const int row = 8 * wave + (lane >> 3);
                 const int c = (lane & 7) ^ (row & 7);
-                const int pj = wave >> 1;
-                const int64_t page = pj == 0 ? pg[0] : pj == 1 ? pg[1] : pj == 2 ? pg[2] : pg[3];
-                const half_t* src = a.k_pool + block_base(a.addr, page) +
-                                    (int64_t)(row & kPageMask) * kv_dim + g * kHeadDim + 8 * c;
-                lds_dma16(src, lds_offset(&s_k[buf][r0k][0]));
+                const half_t* src = a.k_pool + base + (int64_t)(row & kPageMask) * kv_dim +
+                                    g * kHeadDim + 8 * c;
+                lds_dma16(src, lds_offset(&s_k[buf][8 * wave][0]));
             }
-            // V^T: wave w covers dims 8w .. 8w+7; lane L's chunk c (keys 8c .. 8c+7 of the
-            // tile) comes from page c >> 1, slots 8 * (c & 1) ...
+            // V^T, page-major: buffer `buf` holds the tile's 4 pages, each [64 dims][16 keys]
+            // (32-byte rows, the two 8-key halves of a row swapped when bit 3 of the dim is
+            // set, which keeps the operand reads free of bank conflicts). Lane L of wave w
+            // moves dim 32 (w & 1) + (L >> 1), row position L & 1, of page w >> 1: the
+            // wave's 64 lanes fill 1 KiB of that page in order.
             {
-                const int d0 = 8 * wave;
-                const int d = d0 + (lane >> 3);
-                const int c = (lane & 7) ^ (d & 7);
-                const int j = c >> 1;
-                const int64_t page = j == 0 ? pg[0] : j == 1 ? pg[1] : j == 2 ? pg[2] : pg[3];
-                const half_t* src = a.v_pool + block_base(a.addr, page) +
-                                    (int64_t)(g * kHeadDim + d) * kPageTokens + 8 * (c & 1);
-                lds_dma16(src, lds_offset(&s_v[buf][d0][0]));
+                const int d = 32 * (wave & 1) + (lane >> 1);
+                const int half = (lane & 1) ^ ((d >> 3) & 1);
+                const half_t* src = a.v_pool + base +
+                                    (int64_t)(g * kHeadDim + d) * kPageTokens + 8 * half;
+                lds_dma16(src, lds_offset(&s_v[buf][0][0] + my_page * 1024 + (wave & 1) * 512));
             }
         };
 
@@ -451,9 +458,17 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
 #pragma unroll
         for (int p = 0; p < PS - 1; ++p)
             if (p < n_pairs) {
-                issue(2 * p);
-                issue(2 * p + 1);  // past n_tiles: a clamped, in-bounds load nobody reads
+                const int64_t pa = page_of(2 * p), pb = page_of(2 * p + 1);
+                issue(2 * p, pa);
+                issue(2 * p + 1, pb);  // past n_tiles: a clamped, in-bounds load nobody reads
             }
+        if (first_run) {
+            // The query operands are complete before the loop, so no wait for them can land
+            // inside it (where it would also wait for the tiles in flight).
+            load_queries();
+            __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+            first_run = false;
+        }
         for (int ip = 0; ip < n_pairs; ++ip) {
             // Wait for this thread's loads of pair ip (later pairs may stay in flight, 4
             // loads each) and its LDS reads of pair ip - 1; the barrier then makes every
@@ -467,11 +482,12 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
             // the V^T chunk it loaded (its own load has landed), before the barrier.
             if (ip == tail_pair) {
                 const int t = n_tiles - 1;
-                const int d = 8 * wave + (lane >> 3);
-                const int c = (lane & 7) ^ (d & 7);  // keys 8c .. 8c + 7 of the tile
-                const int nv = hist_end - (t * kKeyTile + 8 * c);
+                const int d = 32 * (wave & 1) + (lane >> 1);
+                const int half = (lane & 1) ^ ((d >> 3) & 1);  // keys 16 j + 8 half .. +7
+                const int nv = hist_end - (t * kKeyTile + 16 * my_page + 8 * half);
                 if (nv < 8) {
-                    half8_t* chunk = reinterpret_cast<half8_t*>(&s_v[t % KB][8 * wave][0]) + lane;
+                    half8_t* chunk = reinterpret_cast<half8_t*>(
+                        &s_v[t % KB][0][0] + my_page * 1024 + (wave & 1) * 512) + lane;
                     half8_t v = *chunk;
 #pragma unroll
                     for (int r = 0; r < 8; ++r)
@@ -482,8 +498,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
             }
             __builtin_amdgcn_s_barrier();
             if (ip + PS - 1 < n_pairs) {
-                issue(2 * (ip + PS - 1));
-                issue(2 * (ip + PS - 1) + 1);
+                const int tn = 2 * (ip + PS - 1);
+                const int64_t pa = page_of(tn), pb = page_of(tn + 1);
+                issue(tn, pa);
+                issue(tn + 1, pb);
             }
             const int t = 2 * ip + kh;
             const int kbase = t * kKeyTile;
@@ -544,15 +562,17 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                     l[qb] += tile_p(st[qb], a.scale_log2, mu, pb[qb], pl[qb]);
                 }
                 // O^T[dim][q] += V^T[dim][32 keys] . P^T[32 keys][q], key halves ks = 0, 1
-                // (keys past the run's end were zeroed in LDS above).
+                // (keys past the run's end were zeroed in LDS above). Keys 32 ks + 8 grp .. +7
+                // of dim d are half grp & 1 of page 2 ks + (grp >> 1), at row position
+                // (grp & 1) ^ (bit 3 of d), one 16-byte read.
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
                     const int d = 16 * db + col;
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) {
-                        // keys 32 ks + 8 grp .. +7: 16-byte chunk 4 ks + grp of the row
                         const half8_t va = *reinterpret_cast<const half8_t*>(
-                            &s_v[buf][d][8 * ((4 * ks + grp) ^ (d & 7))]);
+                            &s_v[buf][0][0] + (2 * ks + (grp >> 1)) * 1024 + d * 16 +
+                            8 * ((grp & 1) ^ ((d >> 3) & 1)));
 #pragma unroll
                         for (int qb = 0; qb < QB; ++qb) {
                             acc[qb][db] = mfma_16x16x32(va, pb[qb][ks], acc[qb][db]);

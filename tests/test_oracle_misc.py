@@ -120,6 +120,25 @@ def test_counter_hash_value():
         assert -1.0 <= got < 1.0
 
 
+def test_counter_hash_mixes_with_the_splitmix64_output_function():
+    """The counter hash (gpu_attention_validation.rs:47-61) finishes with splitmix64's output
+    function, which Vigna's published vector pins through orc_splitmix64 (one step from state
+    x - gamma returns mix(x)): value = 2 * (mix(pre) >> 40) / 2^24 - 1. Only the pre-mix
+    combination of the four counters is restated here."""
+    gamma = 0x9E3779B97F4A7C15
+    assert oracle.splitmix64_stream(1234567, 1)[0] == 6457827717110365317  # Vigna's vector
+    rng = np.random.default_rng(1)
+    for _ in range(200):
+        id_, pos, head, dim = (int(x) for x in rng.integers(0, 5000, 4))
+        salt = int(rng.integers(0, 1 << 62))
+        pre = salt ^ ((id_ + 1) * 0x9E3779B97F4A7C15 & M64) ^ ((pos + 1) * 0xBF58476D1CE4E5B9 & M64) \
+            ^ ((head + 1) * 0x94D049BB133111EB & M64) ^ ((dim + 1) * 0xD6E8FEB86659FD93 & M64)
+        mix = oracle.splitmix64_stream((pre - gamma) & M64, 1)[0]
+        want = float(np.float32(np.float32(mix >> 40) / np.float32(16777216.0)) * np.float32(2.0)
+                     - np.float32(1.0))
+        assert oracle.value(id_, pos, head, dim, salt) == want
+
+
 def test_splitmix64_published_vector():
     # Vigna's splitmix64 reference, seed 1234567
     assert oracle.splitmix64_stream(1234567, 3) == [

@@ -40,6 +40,7 @@
 
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 
 namespace crucible {
 namespace {
@@ -208,6 +209,11 @@ struct PrefillArgs {
     int grid_x;       // heavy_first: x extent (heads or head groups)
     int grid_tiles;   // heavy_first: row tiles
     int grid_reqs;    // heavy_first: requests
+    // Hybrid (SEGMENTS, register-direct form only): keys at or past a segment's
+    // absolute_start come from the chunk's own rows, cur_k / cur_v [packed row][kv_dim] f32.
+    int hybrid;
+    const float* cur_k;
+    const float* cur_v;
 };
 
 // (x, row tile, request) of this workgroup. In the longest-first order, row level v
@@ -661,7 +667,9 @@ constexpr int kDirectWaves = 8;
 
 // At most 128 VGPRs (4 waves per SIMD): two 8-wave workgroups per CU, so a config-1 grid
 // (384 workgroups) is resident at once instead of in two rounds.
-template <bool QF32>
+// HYB: the hybrid instantiation (keys of the segment's own chunk from cur_k / cur_v); the
+// pool-only one carries none of that code (its registers stay within the cap).
+template <bool QF32, bool HYB>
 __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
     PrefillArgs a, const int32_t* __restrict__ tables) {
     __shared__ int s_owner[16];
@@ -687,6 +695,7 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
     // OWNERS tiles take their rows from per-row arrays, staged in LDS.
     uint64_t mask;
     int my_row, my_pos, d_owner = 0, d_hist = 0;
+    int d_pstart = 0, d_astart = 0;  // the segment's packed_start and absolute_start (hybrid)
     if (a.mode != kOwners) {
         typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
         int64_t row0 = 0, len = a.rows, pos0 = a.pos_offset;
@@ -696,6 +705,8 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
             len = seg[1];
             pos0 = seg[2];
             d_owner = seg[3];
+            d_pstart = (int)row0;
+            d_astart = (int)pos0;
         } else if (a.mode == kParams) {
             pos0 = ((const_i32_ptr)a.params)[kParamPrefillPos];
         }
@@ -814,6 +825,40 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
                                            4 * grp;
                         va[db][ks][hf] = *reinterpret_cast<const half4_t*>(vp);
                     }
+            // Hybrid (gpu.rs:1691-1697, kernels.cu:2012-2016): keys at or past the segment's
+            // absolute start come from the chunk's own K/V rows (packed row packed_start +
+            // pos - absolute_start), rounded to fp16 as the append would store them, in
+            // place of the pool's. Only keys before the row tile's last visible one are
+            // read, so the rows stay inside the chunk.
+            if (HYB && kbase + kKeyTile > d_astart) {
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+                    const int pos = kbase + 16 * kb + col;
+                    if (pos >= d_astart && pos < hist_end) {
+                        const float* kr = a.cur_k + (int64_t)(d_pstart + pos - d_astart) * kv_dim +
+                                          g * kHeadDim + 8 * grp;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            ka[kb][0][j] = (half_t)kr[j];
+                            ka[kb][1][j] = (half_t)kr[32 + j];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int db = 0; db < 4; ++db)
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const int pos = kbase + 32 * ks + 16 * hf + 4 * grp + r;
+                                if (pos >= d_astart && pos < hist_end)
+                                    va[db][ks][hf][r] = (half_t)a.cur_v[
+                                        (int64_t)(d_pstart + pos - d_astart) * kv_dim +
+                                        g * kHeadDim + 16 * db + col];
+                            }
+            }
 
             float4_t st[4];
 #pragma unroll
@@ -960,18 +1005,24 @@ int launch_prefill(const PrefillArgs& a_in, int64_t tile_rows_total, int64_t z, 
     // once per 64 rows instead of once per 16, when its grid fills the chip.
     int direct = lg.gx * lg.gy * z < device_cu_count();
     if (const int v = tuning(CRUCIBLE_TUNE_PREFILL_DIRECT); v >= 0) direct = v;
+    if (a.hybrid) direct = 1;  // the chunk's own K/V rows: register-direct form only
     if (direct) {
         const int64_t gy = (tile_rows_total + 15) / 16;
         CRUCIBLE_CHECK(a.n_head <= INT32_MAX && gy <= 65535 && z <= 65535, CRUCIBLE_ERR_INVALID,
                        "%s: grid (%d, %lld, %lld) too large", what, a.n_head, (long long)gy,
                        (long long)z);
         const dim3 grid = make_grid(a.n_head, gy, false);
-        if (q_f32)
-            hipLaunchKernelGGL((prefill_direct_kernel<true>), grid, dim3(kDirectWaves * 64), 0,
-                               stream, a, a.tables);
-        else
-            hipLaunchKernelGGL((prefill_direct_kernel<false>), grid, dim3(kDirectWaves * 64), 0,
-                               stream, a, a.tables);
+        auto go = [&](auto qf, auto hyb) {
+            hipLaunchKernelGGL((prefill_direct_kernel<decltype(qf)::value, decltype(hyb)::value>),
+                               grid, dim3(kDirectWaves * 64), 0, stream, a, a.tables);
+        };
+        if (q_f32) {
+            if (a.hybrid) go(std::true_type{}, std::true_type{});
+            else go(std::true_type{}, std::false_type{});
+        } else {
+            if (a.hybrid) go(std::false_type{}, std::true_type{});
+            else go(std::false_type{}, std::false_type{});
+        }
         return fail_launch(what);
     }
     const int hpw = lg.hpw, qb = lg.qb;
@@ -1102,15 +1153,11 @@ extern "C" int crucible_attention_prefill_tiled(
     const int32_t* segments, int64_t requests, int64_t max_chunk, int64_t table_stride,
     int64_t n_head, int64_t n_kv_head, int64_t head_dim, int64_t n_layer, int64_t layer,
     int64_t kv_dim, int hybrid, int64_t score_capacity, crucible_stream_t stream) {
-    (void)current_k;
-    (void)current_v;
     const char* what = "attention_prefill_tiled";
     if (int rc = check_prefill(what, q_dtype, out_dtype, n_head, n_kv_head, head_dim, kv_dim))
         return rc;
-    CRUCIBLE_CHECK(!hybrid, CRUCIBLE_ERR_UNSUPPORTED,
-                   "%s: hybrid (current-chunk K/V from scratch) is not implemented; append "
-                   "the chunk to the pool first",
-                   what);
+    CRUCIBLE_CHECK(!hybrid || (current_k && current_v), CRUCIBLE_ERR_INVALID,
+                   "%s: hybrid needs the chunk's current K/V rows", what);
     // Launch checks of gpu.rs:1680-1719.
     CRUCIBLE_CHECK(requests > 0 && max_chunk > 0 && table_stride > 0 && n_layer > 0 &&
                        layer >= 0 && layer < n_layer && requests <= 65535,
@@ -1128,6 +1175,9 @@ extern "C" int crucible_attention_prefill_tiled(
     a.table_stride = table_stride;
     a.addr.page_stride = n_layer * kPageTokens * kv_dim;
     a.addr.layer_off = layer * kPageTokens * kv_dim;
+    a.hybrid = hybrid != 0;
+    a.cur_k = static_cast<const float*>(current_k);
+    a.cur_v = static_cast<const float*>(current_v);
     return launch_prefill(a, max_chunk, requests, q_dtype == CRUCIBLE_F32, stream, what);
 }
 

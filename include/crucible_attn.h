@@ -283,9 +283,15 @@ int crucible_attention_prefill_packed(const void* q, int q_dtype, const void* k_
 
 /* Replaces Gpu::attention_prefill_tiled (gpu.rs:1606-1751; kernels.cu:1950-2276):
  * segments[4*i .. 4*i+3] = {packed_start, chunk_len, absolute_start, table_index}.
- * Query row packed_start + j is at position absolute_start + j. `hybrid` must be
- * 0 (current_k/current_v are accepted for signature parity and not read);
- * score_capacity is validated as in the reference but not needed here. */
+ * Query row packed_start + j is at position absolute_start + j. With hybrid = 0 every key
+ * comes from the pools (append the chunk first; current_k/current_v are not read). With
+ * hybrid = 1 (gpu.rs:1691-1697, kernels.cu:2012-2016) keys at or past a segment's
+ * absolute_start come from the chunk's own rows instead: current_k / current_v are f32
+ * [packed row][kv_dim], key position p of segment i at packed row packed_start + p -
+ * absolute_start, rounded to fp16 as the append stores them (so the result equals the
+ * hybrid = 0 result over a pool holding the appended chunk); hybrid launches take the
+ * register-direct kernel. score_capacity is validated as in the reference but not needed
+ * here. */
 int crucible_attention_prefill_tiled(const void* q, int q_dtype, const void* k_pool,
                                      const void* v_pool, const void* current_k,
                                      const void* current_v, void* out, int out_dtype,

@@ -66,10 +66,10 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert rc == _lib.ERR_INVALID
     rc = lib.crucible_cache_store_rows_paged(fake, 0, fake, 9, fake, fake, 1, 192, 8, 12, 0, None)
     assert rc == _lib.ERR_INVALID
-    # hybrid prefill is not implemented
+    # hybrid prefill needs the chunk's current K/V rows
     rc = lib.crucible_attention_prefill_tiled(fake, 1, fake, fake, None, None, fake, 0, fake, fake,
                                               1, 16, 4, 12, 3, 64, 12, 0, 192, 1, 256, None)
-    assert rc == _lib.ERR_UNSUPPORTED
+    assert rc == _lib.ERR_INVALID
     # empty batches are a no-op, not an error
     assert lib.crucible_attention_decode_paged(None, 1, None, None, None, 0, None, None, 0, 12, 3,
                                                64, 64, 12, 0, 192, 1024, None, 0, None) == 0

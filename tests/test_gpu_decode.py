@@ -353,8 +353,10 @@ def test_batch_at_and_past_the_compact_limit(gpu, dev, batch):
 
 
 def test_workspace_shared_across_batch_sizes(gpu, dev):
-    """One workspace (sized for the largest batch) serves decode calls whose batch size
-    changes from call to call, as the engine's active count does step to step."""
+    """One workspace (sized for the largest call) serves decode calls whose batch size and
+    context bound change from call to call, as the engine's active count does step to step:
+    the split count, and with it the place of every partial, moves between calls. Each launch
+    leaves its combine counters back at zero."""
     rng = np.random.default_rng(90)
     n_head, n_kv, n_layer, max_batch, stride = 12, 3, 2, 16, 128
     nbytes = gpu.lib.crucible_attention_decode_workspace_bytes(max_batch, n_head, stride * 16)
@@ -362,20 +364,20 @@ def test_workspace_shared_across_batch_sizes(gpu, dev):
     n_pages = max_batch * stride + 2
     kp, vp = random_pools(rng, n_pages, n_layer, n_kv * 64)
     d_k, d_v = _dev(kp, dev), _dev(vp, dev)
-    for batch in (16, 5, 11, 16, 1, 16):
-        lens = rng.integers(1, stride * 16 + 1, batch)
+    for batch, max_seq in ((16, 2048), (5, 512), (11, 2048), (16, 1024), (1, 2048), (16, 2048),
+                           (3, 256)):
+        lens = rng.integers(1, max_seq + 1, batch)
         tables = disjoint_tables(rng, n_pages, lens, stride)
         q = rng.standard_normal((batch, n_head * 64)).astype(np.float16).astype(np.float32)
         out = torch.full((batch, n_head * 64), SENTINEL, device=dev)
         gpu.attention_decode_paged(_dev(q.astype(np.float16), dev), d_k, d_v, out,
                                    _dev(tables, dev), _dev(lens.astype(np.int32), dev), batch,
-                                   n_head, n_kv, 64, stride, n_layer, 1, n_kv * 64, stride * 16,
+                                   n_head, n_kv, 64, stride, n_layer, 1, n_kv * 64, max_seq,
                                    workspace=ws)
         torch.cuda.synchronize()
         want = _oracle(q, kp, vp, tables, lens, n_head, n_kv, n_layer, 1)
-        element_gate(out.cpu().numpy(), want, f"shared workspace, batch {batch}")
-    # every counter is back to zero
-    assert int(ws[:65536 * 4].view(torch.int32).abs().sum()) == 0
+        element_gate(out.cpu().numpy(), want, f"shared workspace, batch {batch}, max_seq {max_seq}")
+        assert int(torch.count_nonzero(ws[:65536 * 4])) == 0, f"counters not reset, batch {batch}"
 
 
 @pytest.mark.parametrize("n_head,n_kv,pad", [(12, 3, 0), (12, 12, 4), (16, 4, 0), (12, 1, 8)])

@@ -39,6 +39,7 @@
 // serves one launch at a time (calls of any batch size may share it: the counters sit
 // at a fixed place at its start).
 #include "common.hpp"
+#include "generic_attend.hpp"
 
 #include <cmath>
 #include <cstdlib>
@@ -785,6 +786,84 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
     combine_partials<8>(a, b, g * a.n_rep + ccol, threadIdx.x & 15, n_active);
 }
 
+// ---------------------------------------------------------------- head_dim other than 64
+// One workgroup per (request, query head) through attend_generic (generic_attend.hpp).
+// ROPE (the qkv entry, f32 rows): q's pairs (i, i + hd/2) are rotated at positions[b], as
+// crucible_rope_split_qkv rotates them.
+template <bool QF32>
+__global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeArgs a, int hd) {
+    __shared__ GenericLds lds;
+    const int b = blockIdx.x;
+    const int h = blockIdx.y;
+    const int len = request_len(a, b);
+    if (len <= 0) return;  // inactive request: output untouched
+    const int half = hd >> 1;
+    const int64_t qoff = (int64_t)b * a.q_row_stride + (int64_t)h * hd;
+    if (a.rope_cos) {
+        const float* qp = static_cast<const float*>(a.q) + qoff;
+        const int pos = min(max(a.positions[b], 0), a.rope_max_pos - 1);
+        for (int i = threadIdx.x; i < half; i += kGenericThreads) {
+            float lo = qp[i], hi = qp[i + half];
+            rope_pair(lo, hi, a.rope_cos[(int64_t)pos * half + i], a.rope_sin[(int64_t)pos * half + i]);
+            lds.q[i] = lo;
+            lds.q[i + half] = hi;
+        }
+    } else {
+        for (int d = threadIdx.x; d < hd; d += kGenericThreads)
+            lds.q[d] = QF32 ? static_cast<const float*>(a.q)[qoff + d]
+                            : (float)static_cast<const half_t*>(a.q)[qoff + d];
+    }
+    __syncthreads();
+    GenericKeys ks{};
+    ks.k_pool = a.k_pool;
+    ks.v_pool = a.v_pool;
+    ks.addr = a.addr;
+    ks.table = a.tables ? a.tables + (int64_t)b * a.table_stride : nullptr;
+    ks.g = h / a.n_rep;
+    ks.hd = hd;
+    ks.astart = INT32_MAX;
+    const int64_t ooff = (int64_t)b * a.out_row_stride + (int64_t)h * hd;
+    attend_generic(lds, ks, len, a.scale_log2, [&](int d, float v) {
+        if (a.out_f16)
+            static_cast<half_t*>(a.out)[ooff + d] = (half_t)v;
+        else
+            static_cast<float*>(a.out)[ooff + d] = v;
+    });
+}
+
+// The qkv entry's two appends for head_dim other than 64: row b's K (rotated at
+// positions[b] when RoPE tables are given) and its V, f32 rows of stride kv_new_stride,
+// rounded to fp16 and stored at positions[b] as crucible_rope_split_qkv followed by
+// crucible_cache_store_rows_paged stores them (a row whose position lies outside its table
+// is skipped). One thread per (row, kv head, pair).
+__global__ __launch_bounds__(256) void append_rope_generic_kernel(DecodeArgs a, int hd) {
+    const int half = hd >> 1;
+    const int64_t per_row = (int64_t)a.n_kv_head * half;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)a.batch * per_row) return;
+    const int b = (int)(i / per_row);
+    const int r = (int)(i - (int64_t)b * per_row);
+    const int g = r / half;
+    const int e = r - g * half;
+    const int pos = a.positions[b];
+    if (pos < 0 || (pos >> kPageShift) >= a.table_stride) return;
+    const int64_t base = block_base(a.addr, a.tables[(int64_t)b * a.table_stride + (pos >> kPageShift)]);
+    const int slot = pos & kPageMask;
+    const int c = g * hd + e;  // channel of the pair's first element
+    const float* kr = static_cast<const float*>(a.k_new) + (int64_t)b * a.kv_new_stride;
+    const float* vr = static_cast<const float*>(a.v_new) + (int64_t)b * a.kv_new_stride;
+    float lo = kr[c], hi = kr[c + half];
+    if (a.rope_cos) {
+        const int p = min(pos, a.rope_max_pos - 1);
+        rope_pair(lo, hi, a.rope_cos[(int64_t)p * half + e], a.rope_sin[(int64_t)p * half + e]);
+    }
+    const int kv_dim = a.addr.kv_dim;
+    a.k_pool[base + (int64_t)slot * kv_dim + c] = (half_t)lo;
+    a.k_pool[base + (int64_t)slot * kv_dim + c + half] = (half_t)hi;
+    a.v_pool[base + (int64_t)c * kPageTokens + slot] = (half_t)vr[c];
+    a.v_pool[base + (int64_t)(c + half) * kPageTokens + slot] = (half_t)vr[c + half];
+}
+
 struct DecodeShape {
     int pages;  // pages per wave
     int waves;  // waves per workgroup
@@ -902,10 +981,11 @@ int check_geometry(const char* what, int64_t n_head, int64_t n_kv_head, int64_t 
     CRUCIBLE_CHECK(n_head > 0 && n_kv_head > 0 && n_head % n_kv_head == 0, CRUCIBLE_ERR_INVALID,
                    "%s: n_head %lld must be a positive multiple of n_kv_head %lld", what,
                    (long long)n_head, (long long)n_kv_head);
-    CRUCIBLE_CHECK(head_dim == kHeadDim, CRUCIBLE_ERR_UNSUPPORTED,
-                   "%s: head_dim %lld unsupported (this build implements 64)", what,
-                   (long long)head_dim);
-    CRUCIBLE_CHECK(n_head / n_kv_head <= 16, CRUCIBLE_ERR_UNSUPPORTED,
+    CRUCIBLE_CHECK(head_dim == kHeadDim || generic_head_dim_ok(head_dim),
+                   CRUCIBLE_ERR_UNSUPPORTED,
+                   "%s: head_dim %lld unsupported (a multiple of 8 up to %d)", what,
+                   (long long)head_dim, kGenericMaxHeadDim);
+    CRUCIBLE_CHECK(head_dim != kHeadDim || n_head / n_kv_head <= 16, CRUCIBLE_ERR_UNSUPPORTED,
                    "%s: more than 16 query heads per kv head", what);
     CRUCIBLE_CHECK(kv_dim == n_kv_head * head_dim, CRUCIBLE_ERR_INVALID,
                    "%s: kv_dim %lld != n_kv_head * head_dim", what, (long long)kv_dim);
@@ -938,14 +1018,15 @@ void bind_workspace(DecodeArgs& a, void* ws) {
 }
 
 DecodeArgs common_args(const void* q, const void* k, const void* v, void* out, int out_dtype,
-                       int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t max_seq) {
+                       int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t max_seq,
+                       int64_t head_dim = kHeadDim) {
     DecodeArgs a{};
     a.q = q;
     a.k_pool = static_cast<half_t*>(const_cast<void*>(k));  // written only by the fused append
     a.v_pool = static_cast<half_t*>(const_cast<void*>(v));
     a.out = out;
-    a.q_row_stride = (int32_t)(n_head * kHeadDim);
-    a.out_row_stride = (int32_t)(n_head * kHeadDim);
+    a.q_row_stride = (int32_t)(n_head * head_dim);
+    a.out_row_stride = (int32_t)(n_head * head_dim);
     a.batch = (int)batch;
     a.n_head = (int)n_head;
     a.n_kv_head = (int)n_kv_head;
@@ -953,8 +1034,41 @@ DecodeArgs common_args(const void* q, const void* k, const void* v, void* out, i
     a.max_seq = (int)max_seq;
     a.max_pages = (int)((max_seq + kPageMask) >> kPageShift);
     a.out_f16 = out_dtype == CRUCIBLE_F16;
-    a.scale_log2 = 0.125f * kLog2e;
+    a.scale_log2 = head_dim == kHeadDim ? 0.125f * kLog2e
+                                        : (float)(1.4426950408889634 / std::sqrt((double)head_dim));
     return a;
+}
+
+// head_dim other than 64: decode_generic_kernel over (request, query head). Appends, where
+// the entry has them, are launched before it on the same stream.
+int launch_decode_generic(const DecodeArgs& a, int hd, bool q_f32, hipStream_t stream,
+                          const char* what) {
+    CRUCIBLE_CHECK(a.n_head <= 65535, CRUCIBLE_ERR_INVALID, "%s: n_head %d too large", what,
+                   a.n_head);
+    CRUCIBLE_CHECK(aligned16(a.k_pool) && aligned16(a.v_pool), CRUCIBLE_ERR_INVALID,
+                   "%s: pools must be 16-byte aligned", what);
+    const dim3 grid((unsigned)a.batch, (unsigned)a.n_head);
+    if (q_f32)
+        hipLaunchKernelGGL(decode_generic_kernel<true>, grid, dim3(kGenericThreads), 0, stream, a, hd);
+    else
+        hipLaunchKernelGGL(decode_generic_kernel<false>, grid, dim3(kGenericThreads), 0, stream, a, hd);
+    return fail_launch(what);
+}
+
+// The two appends of the fused entries for head_dim other than 64, f32 or fp16 rows of
+// stride kv_dim: the library's own crucible_cache_store_rows_paged, so the pools get the
+// bytes the separate calls store.
+int append_rows_generic(const DecodeArgs& a, int kv_dtype, int64_t n_layer, int64_t layer,
+                        hipStream_t stream) {
+    for (int kind : {CRUCIBLE_POOL_K, CRUCIBLE_POOL_V}) {
+        const bool k = kind == CRUCIBLE_POOL_K;
+        if (const int rc = crucible_cache_store_rows_paged(
+                k ? a.k_new : a.v_new, kv_dtype, k ? a.k_pool : a.v_pool, kind, a.tables,
+                a.positions, a.batch, a.addr.kv_dim, a.table_stride, n_layer, layer,
+                reinterpret_cast<crucible_stream_t>(stream)))
+            return rc;
+    }
+    return CRUCIBLE_OK;
 }
 
 // Split the request into workgroups, bind the workspace and launch.
@@ -1080,7 +1194,7 @@ extern "C" int crucible_attention_decode_paged(
                    CRUCIBLE_ERR_INVALID, "%s: max_seq %lld must be in 1..table_stride*16", what,
                    (long long)max_seq);
     DecodeArgs a = common_args(q, k_pool, v_pool, out, out_dtype, batch, n_head, n_kv_head,
-                               max_seq);
+                               max_seq, head_dim);
     a.tables = page_tables;
     a.lens = seq_lens;
     a.lens_stride = 1;
@@ -1088,6 +1202,8 @@ extern "C" int crucible_attention_decode_paged(
     a.addr.page_stride = n_layer * kPageTokens * kv_dim;
     a.addr.layer_off = layer * kPageTokens * kv_dim;
     a.table_stride = (int32_t)table_stride;
+    if (head_dim != kHeadDim)
+        return launch_decode_generic(a, (int)head_dim, q_dtype == CRUCIBLE_F32, stream, what);
     return decode_with_workspace(a, q_dtype == CRUCIBLE_F32, workspace, workspace_bytes, stream,
                                  what);
 }
@@ -1116,7 +1232,7 @@ extern "C" int crucible_attention_decode_paged_append(
                    CRUCIBLE_ERR_INVALID, "%s: max_seq %lld must be in 1..table_stride*16", what,
                    (long long)max_seq);
     DecodeArgs a = common_args(q, k_pool, v_pool, out, out_dtype, batch, n_head, n_kv_head,
-                               max_seq);
+                               max_seq, head_dim);
     a.tables = page_tables;
     a.lens = seq_lens;
     a.lens_stride = 1;
@@ -1129,6 +1245,10 @@ extern "C" int crucible_attention_decode_paged_append(
     a.addr.page_stride = n_layer * kPageTokens * kv_dim;
     a.addr.layer_off = layer * kPageTokens * kv_dim;
     a.table_stride = (int32_t)table_stride;
+    if (head_dim != kHeadDim) {
+        if (const int rc = append_rows_generic(a, kv_dtype, n_layer, layer, stream)) return rc;
+        return launch_decode_generic(a, (int)head_dim, q_dtype == CRUCIBLE_F32, stream, what);
+    }
     return decode_with_workspace(a, q_dtype == CRUCIBLE_F32, workspace, workspace_bytes, stream,
                                  what);
 }
@@ -1157,7 +1277,7 @@ extern "C" int crucible_attention_decode_paged_append_noalloc(
                    CRUCIBLE_ERR_INVALID, "%s: max_seq %lld must be in 1..table_stride*16", what,
                    (long long)max_seq);
     DecodeArgs a = common_args(q, k_pool, v_pool, out, out_dtype, batch, n_head, n_kv_head,
-                               max_seq);
+                               max_seq, head_dim);
     a.tables = page_tables;
     a.lens = seq_lens;
     a.lens_stride = 1;
@@ -1170,6 +1290,10 @@ extern "C" int crucible_attention_decode_paged_append_noalloc(
     a.addr.page_stride = n_layer * kPageTokens * kv_dim;
     a.addr.layer_off = layer * kPageTokens * kv_dim;
     a.table_stride = (int32_t)table_stride;
+    if (head_dim != kHeadDim) {  // the generic kernels use no scratch
+        if (const int rc = append_rows_generic(a, kv_dtype, n_layer, layer, stream)) return rc;
+        return launch_decode_generic(a, (int)head_dim, q_dtype == CRUCIBLE_F32, stream, what);
+    }
     CRUCIBLE_CHECK(aligned16(a.q) && aligned16(a.k_pool) && aligned16(a.v_pool) &&
                        aligned16(a.out) && aligned16(a.k_new) && aligned16(a.v_new),
                    CRUCIBLE_ERR_INVALID, "%s: q, pools, out and new rows must be 16-byte aligned",
@@ -1237,7 +1361,7 @@ extern "C" int crucible_attention_decode_qkv_paged_append(
                    CRUCIBLE_ERR_INVALID,
                    "%s: rope tables must cover max_seq positions (16-byte aligned)", what);
     DecodeArgs a = common_args(qkv, k_pool, v_pool, out, out_dtype, batch, n_head, n_kv_head,
-                               max_seq);
+                               max_seq, head_dim);
     a.q_row_stride = (int32_t)qkv_row_stride;
     a.tables = page_tables;
     a.lens = seq_lens;
@@ -1254,6 +1378,15 @@ extern "C" int crucible_attention_decode_qkv_paged_append(
     a.addr.page_stride = n_layer * kPageTokens * kv_dim;
     a.addr.layer_off = layer * kPageTokens * kv_dim;
     a.table_stride = (int32_t)table_stride;
+    if (head_dim != kHeadDim) {
+        const int64_t threads = batch * n_kv_head * (head_dim / 2);
+        CRUCIBLE_CHECK(threads <= (int64_t)INT32_MAX * 256, CRUCIBLE_ERR_INVALID, "%s: too many rows",
+                       what);
+        hipLaunchKernelGGL(append_rope_generic_kernel, dim3((unsigned)((threads + 255) / 256)),
+                           dim3(256), 0, stream, a, (int)head_dim);
+        if (const int rc = fail_launch(what)) return rc;
+        return launch_decode_generic(a, (int)head_dim, true, stream, what);
+    }
     return decode_with_workspace(a, true, workspace, workspace_bytes, stream, what);
 }
 
@@ -1306,12 +1439,14 @@ extern "C" int crucible_attention_decode(const void* q, int q_dtype, const void*
     CRUCIBLE_CHECK(max_seq > 0 && max_seq <= INT32_MAX && layer_base >= 0, CRUCIBLE_ERR_INVALID,
                    "%s: max_seq %lld", what, (long long)max_seq);
     DecodeArgs a = common_args(q, k_cache, v_cache, out, out_dtype, 1, n_head, n_kv_head,
-                               max_seq);
+                               max_seq, head_dim);
     a.lens = params;
     a.lens_off = kParamSeq;
     a.addr.kv_dim = (int32_t)cache_stride;
     a.addr.page_stride = kPageTokens * cache_stride;
     a.addr.layer_off = layer_base;
+    if (head_dim != kHeadDim)
+        return launch_decode_generic(a, (int)head_dim, q_dtype == CRUCIBLE_F32, stream, what);
     return decode_with_workspace(a, q_dtype == CRUCIBLE_F32, workspace, workspace_bytes, stream,
                                  what);
 }
@@ -1333,12 +1468,16 @@ extern "C" int crucible_attention_split(const void* q, int q_dtype, const void* 
     CRUCIBLE_CHECK(capacity > 0 && capacity <= INT32_MAX && layer_base >= 0,
                    CRUCIBLE_ERR_INVALID, "%s: capacity %lld", what, (long long)capacity);
     DecodeArgs a = common_args(q, k_cache, v_cache, out, out_dtype, 1, n_head, n_kv_head,
-                               capacity);
+                               capacity, head_dim);
     a.lens = params;
     a.lens_off = kParamSeq;
     a.addr.kv_dim = (int32_t)cache_stride;
     a.addr.page_stride = kPageTokens * cache_stride;
     a.addr.layer_off = layer_base;
+    // head_dim other than 64: the generic kernel writes the output in one pass (the partial
+    // buffers are left as they are)
+    if (head_dim != kHeadDim)
+        return launch_decode_generic(a, (int)head_dim, q_dtype == CRUCIBLE_F32, stream, what);
     // 128-position chunks as in the reference (gpu.rs:37 ATTN_CHUNK): 4 waves x 2 pages,
     // partials in the caller's buffers, combined by a second kernel.
     const DecodeShape sh{2, 4};

@@ -37,7 +37,9 @@
 // CONTIG tiles are always a single run; an OWNERS tile that straddles two requests
 // makes two passes, each masking the rows of the other request.
 #include "common.hpp"
+#include "generic_attend.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <type_traits>
@@ -957,6 +959,69 @@ void launch_kb(const PrefillArgs& a, int kb, dim3 grid, hipStream_t stream) {
                            a.tables);
 }
 
+// ---------------------------------------------------------------- head_dim other than 64
+// One workgroup per (query head, request) walks the request's rows (grid y, strided) through
+// attend_generic (generic_attend.hpp): each row attends to keys [0, pos] of its owner, read
+// through the same row modes (tile_row) and, for hybrid segments, the chunk's own K/V rows
+// from the segment's absolute start.
+template <bool QF32>
+__global__ __launch_bounds__(kGenericThreads) void prefill_generic_kernel(PrefillArgs a, int hd,
+                                                                          int64_t rows_y) {
+    __shared__ GenericLds lds;
+    const int h = blockIdx.x;
+    const int64_t req = blockIdx.z;
+    const int64_t stride = (int64_t)a.n_head * hd;
+    GenericKeys ks{};
+    ks.k_pool = a.k_pool;
+    ks.v_pool = a.v_pool;
+    ks.addr = a.addr;
+    ks.g = h / a.n_rep;
+    ks.hd = hd;
+    ks.astart = INT32_MAX;
+    if (a.hybrid && a.mode == kSegments) {
+        const int32_t* seg = a.segments + 4 * req;
+        ks.pstart = seg[0];
+        ks.astart = seg[2];
+        ks.cur_k = a.cur_k;
+        ks.cur_v = a.cur_v;
+    }
+    for (int64_t local = blockIdx.y; local < rows_y; local += gridDim.y) {
+        int row, owner, pos;
+        tile_row(a, req, local, row, owner, pos);
+        if (row < 0) continue;  // uniform: the same row for the whole workgroup
+        const int64_t qoff = (int64_t)row * stride + (int64_t)h * hd;
+        for (int d = threadIdx.x; d < hd; d += kGenericThreads)
+            lds.q[d] = QF32 ? static_cast<const float*>(a.q)[qoff + d]
+                            : (float)static_cast<const half_t*>(a.q)[qoff + d];
+        __syncthreads();
+        ks.table = a.tables ? a.tables + (int64_t)owner * a.table_stride : nullptr;
+        attend_generic(lds, ks, pos + 1, a.scale_log2, [&](int d, float v) {
+            if (a.out_f16)
+                static_cast<half_t*>(a.out)[qoff + d] = (half_t)v;
+            else
+                static_cast<float*>(a.out)[qoff + d] = v;
+        });
+    }
+}
+
+int launch_prefill_generic(PrefillArgs a, int hd, int64_t tile_rows_total, int64_t z, bool q_f32,
+                           hipStream_t stream, const char* what) {
+    CRUCIBLE_CHECK(a.n_head <= INT32_MAX && z <= 65535, CRUCIBLE_ERR_INVALID,
+                   "%s: grid too large", what);
+    CRUCIBLE_CHECK(((uintptr_t)a.k_pool & 15) == 0 && ((uintptr_t)a.v_pool & 15) == 0,
+                   CRUCIBLE_ERR_INVALID, "%s: pools must be 16-byte aligned", what);
+    a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)hd));
+    const dim3 grid((unsigned)a.n_head, (unsigned)std::min<int64_t>(tile_rows_total, 65535),
+                    (unsigned)z);
+    if (q_f32)
+        hipLaunchKernelGGL(prefill_generic_kernel<true>, grid, dim3(kGenericThreads), 0, stream, a,
+                           hd, tile_rows_total);
+    else
+        hipLaunchKernelGGL(prefill_generic_kernel<false>, grid, dim3(kGenericThreads), 0, stream,
+                           a, hd, tile_rows_total);
+    return fail_launch(what);
+}
+
 template <int HPW, int QB>
 void launch_hq(const PrefillArgs& a, bool q_f32, int kb, dim3 grid, hipStream_t stream) {
     if (q_f32) launch_kb<HPW, QB, true>(a, kb, grid, stream);
@@ -1055,9 +1120,10 @@ int check_prefill(const char* what, int q_dtype, int out_dtype, int64_t n_head,
     CRUCIBLE_CHECK(n_head > 0 && n_kv_head > 0 && n_head % n_kv_head == 0, CRUCIBLE_ERR_INVALID,
                    "%s: n_head %lld must be a positive multiple of n_kv_head %lld", what,
                    (long long)n_head, (long long)n_kv_head);
-    CRUCIBLE_CHECK(head_dim == kHeadDim, CRUCIBLE_ERR_UNSUPPORTED,
-                   "%s: head_dim %lld unsupported (this build implements 64)", what,
-                   (long long)head_dim);
+    CRUCIBLE_CHECK(head_dim == kHeadDim || generic_head_dim_ok(head_dim),
+                   CRUCIBLE_ERR_UNSUPPORTED,
+                   "%s: head_dim %lld unsupported (a multiple of 8 up to %d)", what,
+                   (long long)head_dim, kGenericMaxHeadDim);
     CRUCIBLE_CHECK(kv_dim == n_kv_head * head_dim, CRUCIBLE_ERR_INVALID,
                    "%s: kv_dim %lld != n_kv_head * head_dim", what, (long long)kv_dim);
     CRUCIBLE_CHECK(n_head <= (1 << 20), CRUCIBLE_ERR_INVALID, "%s: n_head too large", what);
@@ -1113,6 +1179,9 @@ extern "C" int crucible_attention_prefill_paged(const void* q, int q_dtype, cons
     a.rows = rows;
     a.addr.page_stride = n_layer * kPageTokens * kv_dim;
     a.addr.layer_off = layer * kPageTokens * kv_dim;
+    if (head_dim != kHeadDim)
+        return launch_prefill_generic(a, (int)head_dim, rows, 1, q_dtype == CRUCIBLE_F32, stream,
+                                      what);
     return launch_prefill(a, rows, 1, q_dtype == CRUCIBLE_F32, stream, what);
 }
 
@@ -1144,6 +1213,9 @@ extern "C" int crucible_attention_prefill_packed(
     a.table_stride = table_stride;
     a.addr.page_stride = n_layer * kPageTokens * kv_dim;
     a.addr.layer_off = layer * kPageTokens * kv_dim;
+    if (head_dim != kHeadDim)
+        return launch_prefill_generic(a, (int)head_dim, rows, 1, q_dtype == CRUCIBLE_F32, stream,
+                                      what);
     return launch_prefill(a, rows, 1, q_dtype == CRUCIBLE_F32, stream, what);
 }
 
@@ -1178,6 +1250,9 @@ extern "C" int crucible_attention_prefill_tiled(
     a.hybrid = hybrid != 0;
     a.cur_k = static_cast<const float*>(current_k);
     a.cur_v = static_cast<const float*>(current_v);
+    if (head_dim != kHeadDim)
+        return launch_prefill_generic(a, (int)head_dim, max_chunk, requests,
+                                      q_dtype == CRUCIBLE_F32, stream, what);
     return launch_prefill(a, max_chunk, requests, q_dtype == CRUCIBLE_F32, stream, what);
 }
 
@@ -1204,5 +1279,8 @@ extern "C" int crucible_attention_prefill(const void* q, int q_dtype, const void
     a.pos_offset = pos_offset;
     a.addr.page_stride = kPageTokens * cache_stride;
     a.addr.layer_off = layer_base;
+    if (head_dim != kHeadDim)
+        return launch_prefill_generic(a, (int)head_dim, rows, 1, q_dtype == CRUCIBLE_F32, stream,
+                                      what);
     return launch_prefill(a, rows, 1, q_dtype == CRUCIBLE_F32, stream, what);
 }

@@ -865,33 +865,34 @@ __global__ void rope_split_kernel(const float* __restrict__ qkv, int64_t ld, flo
                                   float* k, float* v, const float* __restrict__ cos_t,
                                   const float* __restrict__ sin_t,
                                   const int32_t* __restrict__ positions, int rows, int n_head,
-                                  int n_kv_head, int max_pos) {
+                                  int n_kv_head, int head_dim, int max_pos) {
     const int heads = n_head + 2 * n_kv_head;
+    const int half = head_dim >> 1;
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (int64_t)rows * heads * 32) return;
-    const int i = (int)(idx & 31);
-    const int head = (int)((idx >> 5) % heads);
-    const int row = (int)((idx >> 5) / heads);
-    const float* src = qkv + (int64_t)row * ld + head * 64;
-    const float lo = src[i], hi = src[i + 32];
+    if (idx >= (int64_t)rows * heads * half) return;
+    const int i = (int)(idx % half);
+    const int head = (int)((idx / half) % heads);
+    const int row = (int)((idx / half) / heads);
+    const float* src = qkv + (int64_t)row * ld + (int64_t)head * head_dim;
+    const float lo = src[i], hi = src[i + half];
     float* dst;
-    if (head < n_head) dst = q + ((int64_t)row * n_head + head) * 64;
-    else if (head < n_head + n_kv_head) dst = k + ((int64_t)row * n_kv_head + head - n_head) * 64;
-    else dst = v + ((int64_t)row * n_kv_head + head - n_head - n_kv_head) * 64;
+    if (head < n_head) dst = q + ((int64_t)row * n_head + head) * head_dim;
+    else if (head < n_head + n_kv_head) dst = k + ((int64_t)row * n_kv_head + head - n_head) * head_dim;
+    else dst = v + ((int64_t)row * n_kv_head + head - n_head - n_kv_head) * head_dim;
     if (head >= n_head + n_kv_head) {
         dst[i] = lo;
-        dst[i + 32] = hi;
+        dst[i + half] = hi;
         return;
     }
     const int pos = positions[row];
     if (pos < 0 || pos >= max_pos) {
-        dst[i] = dst[i + 32] = __builtin_nanf("");
+        dst[i] = dst[i + half] = __builtin_nanf("");
         return;
     }
-    const float c = cos_t[(int64_t)pos * 32 + i];
-    const float s = sin_t[(int64_t)pos * 32 + i];
+    const float c = cos_t[(int64_t)pos * half + i];
+    const float s = sin_t[(int64_t)pos * half + i];
     dst[i] = lo * c - hi * s;
-    dst[i + 32] = lo * s + hi * c;
+    dst[i + half] = lo * s + hi * c;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -1091,18 +1092,18 @@ extern "C" int crucible_rope_split_qkv(const float* qkv, int64_t ld, float* q, f
     const char* what = "crucible_rope_split_qkv";
     CRUCIBLE_CHECK(qkv && q && k && v && cos_table && sin_table && positions,
                    CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
-    CRUCIBLE_CHECK(head_dim == 64, CRUCIBLE_ERR_UNSUPPORTED,
-                   "%s: head_dim %lld unsupported (this build implements 64)", what,
+    CRUCIBLE_CHECK(head_dim > 0 && head_dim % 2 == 0 && head_dim <= 4096, CRUCIBLE_ERR_UNSUPPORTED,
+                   "%s: head_dim %lld unsupported (an even number up to 4096)", what,
                    (long long)head_dim);
     CRUCIBLE_CHECK(n_head > 0 && n_kv_head > 0 && n_head <= 4096 && n_kv_head <= 4096 &&
-                       ld >= (n_head + 2 * n_kv_head) * 64 && max_pos > 0 &&
+                       ld >= (n_head + 2 * n_kv_head) * head_dim && max_pos > 0 &&
                        max_pos <= INT32_MAX && rows >= 0 && rows <= (1 << 24),
                    CRUCIBLE_ERR_INVALID, "%s: bad shape", what);
     if (rows == 0) return CRUCIBLE_OK;
-    const int64_t threads = rows * (n_head + 2 * n_kv_head) * 32;
+    const int64_t threads = rows * (n_head + 2 * n_kv_head) * (head_dim / 2);
     hipLaunchKernelGGL(rope_split_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        reinterpret_cast<hipStream_t>(stream), qkv, ld, q, k, v, cos_table,
                        sin_table, positions, (int)rows, (int)n_head, (int)n_kv_head,
-                       (int)max_pos);
+                       (int)head_dim, (int)max_pos);
     return fail_launch(what);
 }

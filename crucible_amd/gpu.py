@@ -219,7 +219,7 @@ class Gpu:
                                           n_kv_head, head_dim, table_stride, n_layer, layer,
                                           kv_dim, max_seq, workspace=None):
         """The fused step fed from the fused q/k/v rows, with RoPE of q and k at positions[b]
-        (rope tables [max_pos][32] f32, or None for no rotation)."""
+        (rope tables [max_pos][head_dim/2] f32, or None for no rotation)."""
         _need(qkv, "qkv", dtype=torch.float32)
         row_stride = qkv.shape[1]
         _need(qkv, "qkv", numel=batch * row_stride)
@@ -365,19 +365,21 @@ class Gpu:
         _lib.check(self.lib.crucible_rmsnorm_rows(_ptr(x), n, _ptr(w), float(eps), _ptr(out), n,
                                                   rows, n, self._stream()))
 
-    def rope_split_qkv(self, qkv, q, k, v, cos, sin, positions, n_head, n_kv_head):
-        """Split [q | k | v] rows and rotate q, k at positions[row] (ops.rs:124-135)."""
+    def rope_split_qkv(self, qkv, q, k, v, cos, sin, positions, n_head, n_kv_head,
+                       head_dim=64):
+        """Split [q | k | v] rows and rotate q, k at positions[row] (ops.rs:124-135); cos/sin
+        tables [max_pos][head_dim/2]."""
         rows, ld = qkv.shape
         _need(qkv, "qkv", dtype=torch.float32)
-        _need(q, "q", dtype=torch.float32, numel=rows * n_head * 64)
-        _need(k, "k", dtype=torch.float32, numel=rows * n_kv_head * 64)
-        _need(v, "v", dtype=torch.float32, numel=rows * n_kv_head * 64)
+        _need(q, "q", dtype=torch.float32, numel=rows * n_head * head_dim)
+        _need(k, "k", dtype=torch.float32, numel=rows * n_kv_head * head_dim)
+        _need(v, "v", dtype=torch.float32, numel=rows * n_kv_head * head_dim)
         _need(cos, "cos", dtype=torch.float32)
         _need(sin, "sin", dtype=torch.float32, numel=cos.numel())
         _need(positions, "positions", dtype=torch.int32, numel=rows)
         _lib.check(self.lib.crucible_rope_split_qkv(
             _ptr(qkv), ld, _ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(positions), rows,
-            n_head, n_kv_head, 64, cos.shape[0], self._stream()))
+            n_head, n_kv_head, head_dim, cos.shape[0], self._stream()))
 
     # ------------------------------------------------------------- greedy selection
     def argmax_rows(self, x, out, rows, cols):

@@ -134,8 +134,14 @@ int crucible_cache_store_packed_paged(const void* src, int src_dtype, void* pool
 
 /* ------------------------------------------------------------------ decode
  * q is [batch][n_head * head_dim] (q_dtype), out is [batch][n_head * head_dim]
- * (out_dtype). head_dim must be 64 and n_head a multiple of n_kv_head with
- * n_head / n_kv_head <= 16. Query head h reads KV head h / (n_head / n_kv_head).
+ * (out_dtype). n_head is a multiple of n_kv_head; query head h reads KV head
+ * h / (n_head / n_kv_head). head_dim 64 (every preset) runs the MFMA kernels, with
+ * n_head / n_kv_head <= 16. Any other head_dim that is a multiple of 8 up to 256 runs a
+ * generic kernel (one workgroup per request and query head, f32 arithmetic, same pool
+ * layout and the same results to the tolerance of f32 accumulation); it uses no
+ * workspace, the fused entries run their appends as two cache_store_rows_paged launches
+ * (RoPE rows: one append launch) before it, and attention_split leaves its partial
+ * buffers untouched. The same holds for the prefill entries below.
  * The split-K partials live in a caller-provided workspace of at least
  * crucible_attention_decode_workspace_bytes(...) bytes (no allocation here),
  * 16-byte aligned. It starts with a fixed region of 65536 u32 counters, one per
@@ -221,9 +227,10 @@ int crucible_attention_decode_paged_append_noalloc(
 /* The same fused step fed straight from the fused q/k/v projection, with the RoPE of
  * the reference's decode step (rope_rows before the K append and on q, gpu_model.rs:1424-1444;
  * RopeTable::apply, ops.rs:124-135) applied in the same launch (§8f rank 2). Row b of qkv
- * (f32, row stride qkv_row_stride, a multiple of 4) holds q (n_head*64), k (kv_dim), v
- * (kv_dim). q and k are rotated at positions[b] with rope_cos/rope_sin ([rope_max_pos][32]
- * f32, 16-byte aligned, rope_max_pos >= max_seq; both NULL: no rotation), each product
+ * (f32, row stride qkv_row_stride, a multiple of 4) holds q (n_head*head_dim), k (kv_dim),
+ * v (kv_dim). q and k are rotated at positions[b] with rope_cos/rope_sin
+ * ([rope_max_pos][head_dim/2] f32, 16-byte aligned, rope_max_pos >= max_seq; both NULL: no
+ * rotation), each product
  * and difference rounded on its own. k and v are appended at positions[b] and attention
  * runs over seq_lens[b] keys. Bit-identical to crucible_rope_split_qkv followed by
  * crucible_attention_decode_paged_append. */
@@ -367,8 +374,9 @@ int crucible_linear_swiglu_f64acc(const float* x, int64_t ldx, const float* norm
 int crucible_rmsnorm_rows(const float* x, int64_t ldx, const float* w, float eps, float* out,
                           int64_t ldo, int64_t rows, int64_t n, crucible_stream_t stream);
 
-/* Split fused [q | k | v] rows (n_head, n_kv_head, n_kv_head heads of head_dim) into
- * contiguous q [rows][n_head*64], k and v [rows][n_kv_head*64], rotating q and k at
+/* Split fused [q | k | v] rows (n_head, n_kv_head, n_kv_head heads of head_dim, any even
+ * head_dim) into contiguous q [rows][n_head*head_dim], k and v [rows][n_kv_head*head_dim],
+ * rotating q and k at
  * positions[row] (RopeTable::apply, ops.rs:124-135; rope_rows_f32, kernels.cu:1677-1706).
  * cos/sin tables are [max_pos][head_dim/2] f32. A position outside [0, max_pos) writes
  * NaN rows. */

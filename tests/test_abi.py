@@ -44,11 +44,17 @@ def _status_and_msg(rc):
 def test_invalid_arguments_are_rejected_before_launch():
     lib = _lib.load()
     fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
-    # head_dim 128 is outside this build
-    rc = lib.crucible_attention_decode_paged(fake, 1, fake, fake, fake, 0, fake, fake, 1, 12, 3,
-                                             128, 64, 12, 0, 384, 1024, fake, 1 << 20, None)
-    assert rc == _lib.ERR_UNSUPPORTED
-    assert "head_dim" in _lib.last_error()[1]
+    # head_dim 64 runs the MFMA kernels, other multiples of 8 up to 256 the generic ones;
+    # 100 (not a multiple of 8) and 264 (past 256) are outside this build
+    for hd in (100, 264):
+        rc = lib.crucible_attention_decode_paged(fake, 1, fake, fake, fake, 0, fake, fake, 1, 12,
+                                                 3, hd, 64, 12, 0, 3 * hd, 1024, fake, 1 << 20,
+                                                 None)
+        assert rc == _lib.ERR_UNSUPPORTED
+        assert "head_dim" in _lib.last_error()[1]
+        rc = lib.crucible_attention_prefill_paged(fake, 1, fake, fake, fake, 0, fake, 10, 12, 3,
+                                                  hd, 12, 0, 3 * hd, 1024, fake, None)
+        assert rc == _lib.ERR_UNSUPPORTED
     # layer outside n_layer
     rc = lib.crucible_attention_decode_paged(fake, 1, fake, fake, fake, 0, fake, fake, 1, 12, 3,
                                              64, 64, 12, 12, 192, 1024, fake, 1 << 20, None)
@@ -104,9 +110,9 @@ def test_decode_step_glue_validates_before_launch():
     # zero rows: nothing to do
     assert lib.crucible_linear_f64acc(fake, 128, None, 1e-6, fake, 64, 128, None, fake, 64, 0,
                                       None) == 0
-    # RoPE split: head_dim 128 is outside this build, ld too small
+    # RoPE split: an odd head_dim has no pairs, ld too small
     rc = lib.crucible_rope_split_qkv(fake, 1152, fake, fake, fake, fake, fake, fake, 16, 12, 3,
-                                     128, 1024, None)
+                                     63, 1024, None)
     assert rc == _lib.ERR_UNSUPPORTED
     rc = lib.crucible_rope_split_qkv(fake, 1000, fake, fake, fake, fake, fake, fake, 16, 12, 3,
                                      64, 1024, None)

@@ -147,8 +147,16 @@ __device__ __forceinline__ void mask_tile_blocks(float4_t (&st)[4], int lim) {
 // in the LDS form, see tile_key; keys 4 grp .. +3 of each 16-key block in the direct
 // form). Returns the lane's sum of P.
 //
+//
+// P16 (the single-operand precision): P is one fp16 operand, p rounded to nearest even
+// (v_cvt_pk_f16_f32), about 2^-12 relative per element, and pl is left untouched; the PV
+// product then takes one MFMA per dim block and key half instead of two. l still sums the
+// unrounded p, so the rounding errors of the weights stay unbiased.
+template <bool P16 = false>
 __device__ __forceinline__ float tile_p(const float4_t (&st)[4], float scale, float mu,
                                         half8_t (&pb)[2], half8_t (&pl)[2]) {
+    typedef float float2_t __attribute__((ext_vector_type(2)));
+    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
     u32x4_t hw[2], lw[2];
     float part[4];
 #pragma unroll
@@ -157,19 +165,28 @@ __device__ __forceinline__ float tile_p(const float4_t (&st)[4], float scale, fl
 #pragma unroll
         for (int r = 0; r < 4; ++r) pf[r] = fast_exp2(__builtin_fmaf(st[kb][r], scale, -mu));
         part[kb] = (pf[0] + pf[1]) + (pf[2] + pf[3]);
-        const uint32_t h01 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pf[0], pf[1]));
-        const uint32_t h23 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pf[2], pf[3]));
-        uint32_t lo01, lo23;
-        split_lo4(pf, h01, h23, lo01, lo23);
-        hw[kb >> 1][(kb & 1) * 2] = h01;
-        hw[kb >> 1][(kb & 1) * 2 + 1] = h23;
-        lw[kb >> 1][(kb & 1) * 2] = lo01;
-        lw[kb >> 1][(kb & 1) * 2 + 1] = lo23;
+        if constexpr (P16) {
+            hw[kb >> 1][(kb & 1) * 2] = __builtin_bit_cast(
+                uint32_t, __builtin_convertvector((float2_t{pf[0], pf[1]}), half2_t));
+            hw[kb >> 1][(kb & 1) * 2 + 1] = __builtin_bit_cast(
+                uint32_t, __builtin_convertvector((float2_t{pf[2], pf[3]}), half2_t));
+        } else {
+            const uint32_t h01 =
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pf[0], pf[1]));
+            const uint32_t h23 =
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pf[2], pf[3]));
+            uint32_t lo01, lo23;
+            split_lo4(pf, h01, h23, lo01, lo23);
+            hw[kb >> 1][(kb & 1) * 2] = h01;
+            hw[kb >> 1][(kb & 1) * 2 + 1] = h23;
+            lw[kb >> 1][(kb & 1) * 2] = lo01;
+            lw[kb >> 1][(kb & 1) * 2 + 1] = lo23;
+        }
     }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
         pb[ks] = __builtin_bit_cast(half8_t, hw[ks]);
-        pl[ks] = __builtin_bit_cast(half8_t, lw[ks]);
+        if constexpr (!P16) pl[ks] = __builtin_bit_cast(half8_t, lw[ks]);
     }
     return (part[0] + part[1]) + (part[2] + part[3]);
 }
@@ -272,7 +289,8 @@ __device__ __forceinline__ void tile_row(const PrefillArgs& a, int64_t req, int6
 // `tables` is passed on its own, read-only and unaliased, so the page-id loads of the
 // tile loop compile to scalar loads (lgkmcnt) that never wait on the in-flight tiles.
 // KB: LDS ring depth in key tiles (4 or 6): KB / 2 - 1 pairs of tiles load ahead.
-template <int HPW, int QB, bool QF32, int KB>
+// P16: P as one fp16 operand (tile_p), one PV MFMA per dim block and key half.
+template <int HPW, int QB, bool QF32, int KB, bool P16>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                                                       const int32_t* __restrict__ tables) {
     constexpr int RS = 4 / HPW;          // row slices per workgroup
@@ -548,7 +566,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                         mask_tile(st[qb], in_run[qb] ? my_pos[qb] - kbase - 8 * grp : -1);
                 }
                 half8_t pb[QB][2];
-                half8_t pl[QB][2];  // P = hi + lo: the product keeps ~22 bits of P
+                half8_t pl[QB][2];  // P = hi + lo: the product keeps ~22 bits of P (not P16)
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) {
                     const float tm = tile_max(st[qb]) * a.scale_log2;  // base-2 units
@@ -567,7 +585,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                         m[qb] = mn;
                     }
                     const float mu = (m[qb] == -INFINITY) ? 0.0f : m[qb];
-                    l[qb] += tile_p(st[qb], a.scale_log2, mu, pb[qb], pl[qb]);
+                    l[qb] += tile_p<P16>(st[qb], a.scale_log2, mu, pb[qb], pl[qb]);
                 }
                 // O^T[dim][q] += V^T[dim][32 keys] . P^T[32 keys][q], key halves ks = 0, 1
                 // (keys past the run's end were zeroed in LDS above). Keys 32 ks + 8 grp .. +7
@@ -584,7 +602,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
 #pragma unroll
                         for (int qb = 0; qb < QB; ++qb) {
                             acc[qb][db] = mfma_16x16x32(va, pb[qb][ks], acc[qb][db]);
-                            acc[qb][db] = mfma_16x16x32(va, pl[qb][ks], acc[qb][db]);
+                            if constexpr (!P16)
+                                acc[qb][db] = mfma_16x16x32(va, pl[qb][ks], acc[qb][db]);
                         }
                     }
                 }
@@ -671,7 +690,7 @@ constexpr int kDirectWaves = 8;
 // (384 workgroups) is resident at once instead of in two rounds.
 // HYB: the hybrid instantiation (keys of the segment's own chunk from cur_k / cur_v); the
 // pool-only one carries none of that code (its registers stay within the cap).
-template <bool QF32, bool HYB>
+template <bool QF32, bool HYB, bool P16>
 __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
     PrefillArgs a, const int32_t* __restrict__ tables) {
     __shared__ int s_owner[16];
@@ -887,7 +906,7 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
             }
             const float mu = (m == -INFINITY) ? 0.0f : m;
             half8_t pb[2], pl[2];
-            l += tile_p(st, a.scale_log2, mu, pb, pl);
+            l += tile_p<P16>(st, a.scale_log2, mu, pb, pl);
             if (kbase + kKeyTile > hist_end) {  // the run's last tile: zero keys past its end
 #pragma unroll
                 for (int db = 0; db < 4; ++db)
@@ -905,7 +924,7 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
                     const half4_t v0 = va[db][ks][0], v1 = va[db][ks][1];
                     const half8_t vv = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
                     acc[db] = mfma_16x16x32(vv, pb[ks], acc[db]);
-                    acc[db] = mfma_16x16x32(vv, pl[ks], acc[db]);
+                    if constexpr (!P16) acc[db] = mfma_16x16x32(vv, pl[ks], acc[db]);
                 }
         }
         if (a.mode != kOwners) break;  // a single run
@@ -949,14 +968,14 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
 
 int heads_per_wg(int n_rep) { return (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1; }
 
-template <int HPW, int QB, bool QF32>
+template <int HPW, int QB, bool QF32, bool P16>
 void launch_kb(const PrefillArgs& a, int kb, dim3 grid, hipStream_t stream) {
     if (kb == 6)
-        hipLaunchKernelGGL((prefill_kernel<HPW, QB, QF32, 6>), grid, dim3(kThreads), 0, stream, a,
-                           a.tables);
+        hipLaunchKernelGGL((prefill_kernel<HPW, QB, QF32, 6, P16>), grid, dim3(kThreads), 0,
+                           stream, a, a.tables);
     else
-        hipLaunchKernelGGL((prefill_kernel<HPW, QB, QF32, 4>), grid, dim3(kThreads), 0, stream, a,
-                           a.tables);
+        hipLaunchKernelGGL((prefill_kernel<HPW, QB, QF32, 4, P16>), grid, dim3(kThreads), 0,
+                           stream, a, a.tables);
 }
 
 // ---------------------------------------------------------------- head_dim other than 64
@@ -1023,9 +1042,15 @@ int launch_prefill_generic(PrefillArgs a, int hd, int64_t tile_rows_total, int64
 }
 
 template <int HPW, int QB>
-void launch_hq(const PrefillArgs& a, bool q_f32, int kb, dim3 grid, hipStream_t stream) {
-    if (q_f32) launch_kb<HPW, QB, true>(a, kb, grid, stream);
-    else launch_kb<HPW, QB, false>(a, kb, grid, stream);
+void launch_hq(const PrefillArgs& a, bool q_f32, bool p16, int kb, dim3 grid,
+               hipStream_t stream) {
+    if (q_f32) {
+        if (p16) launch_kb<HPW, QB, true, true>(a, kb, grid, stream);
+        else launch_kb<HPW, QB, true, false>(a, kb, grid, stream);
+    } else {
+        if (p16) launch_kb<HPW, QB, false, true>(a, kb, grid, stream);
+        else launch_kb<HPW, QB, false, false>(a, kb, grid, stream);
+    }
 }
 
 // tile_rows_total: rows spanned by grid.y (max_chunk or rows); z: requests.
@@ -1065,6 +1090,9 @@ int launch_prefill(const PrefillArgs& a_in, int64_t tile_rows_total, int64_t z, 
         return a.heavy_first ? dim3((unsigned)n) : dim3((unsigned)gx, (unsigned)gy, (unsigned)z);
     };
     const LdsGrid lg = lds_grid(a, tile_rows_total, z);
+    // Precision of P in the PV product: one fp16 operand (P16, the default) or fp16 hi + lo
+    // (about 22 bits, when the tuning key asks for it).
+    const bool p16 = tuning(CRUCIBLE_TUNE_PREFILL_P16) != 0;
     // The register-direct form when the LDS form would leave CUs without a workgroup
     // (short prompts: config 1 is 96 workgroups); the LDS form, which reads each K/V tile
     // once per 64 rows instead of once per 16, when its grid fills the chip.
@@ -1078,8 +1106,14 @@ int launch_prefill(const PrefillArgs& a_in, int64_t tile_rows_total, int64_t z, 
                        (long long)z);
         const dim3 grid = make_grid(a.n_head, gy, false);
         auto go = [&](auto qf, auto hyb) {
-            hipLaunchKernelGGL((prefill_direct_kernel<decltype(qf)::value, decltype(hyb)::value>),
-                               grid, dim3(kDirectWaves * 64), 0, stream, a, a.tables);
+            if (p16)
+                hipLaunchKernelGGL(
+                    (prefill_direct_kernel<decltype(qf)::value, decltype(hyb)::value, true>), grid,
+                    dim3(kDirectWaves * 64), 0, stream, a, a.tables);
+            else
+                hipLaunchKernelGGL(
+                    (prefill_direct_kernel<decltype(qf)::value, decltype(hyb)::value, false>), grid,
+                    dim3(kDirectWaves * 64), 0, stream, a, a.tables);
         };
         if (q_f32) {
             if (a.hybrid) go(std::true_type{}, std::true_type{});
@@ -1101,14 +1135,14 @@ int launch_prefill(const PrefillArgs& a_in, int64_t tile_rows_total, int64_t z, 
                    (long long)z);
     const dim3 grid = make_grid(gx, gy, true);
     if (hpw == 4) {
-        if (qb == 2) launch_hq<4, 2>(a, q_f32, kb, grid, stream);
-        else launch_hq<4, 1>(a, q_f32, kb, grid, stream);
+        if (qb == 2) launch_hq<4, 2>(a, q_f32, p16, kb, grid, stream);
+        else launch_hq<4, 1>(a, q_f32, p16, kb, grid, stream);
     } else if (hpw == 2) {
-        if (qb == 2) launch_hq<2, 2>(a, q_f32, kb, grid, stream);
-        else launch_hq<2, 1>(a, q_f32, kb, grid, stream);
+        if (qb == 2) launch_hq<2, 2>(a, q_f32, p16, kb, grid, stream);
+        else launch_hq<2, 1>(a, q_f32, p16, kb, grid, stream);
     } else {
-        if (qb == 2) launch_hq<1, 2>(a, q_f32, kb, grid, stream);
-        else launch_hq<1, 1>(a, q_f32, kb, grid, stream);
+        if (qb == 2) launch_hq<1, 2>(a, q_f32, p16, kb, grid, stream);
+        else launch_hq<1, 1>(a, q_f32, p16, kb, grid, stream);
     }
     return fail_launch(what);
 }

@@ -87,7 +87,8 @@ enum crucible_tuning_key {
     CRUCIBLE_TUNE_PREFILL_BUFS = 6,        /* prefill LDS ring depth in key tiles: 4, 6 */
     CRUCIBLE_TUNE_LINEAR_TILE = 7,         /* projection tiles: 4 or 16 columns (decode), 32 (prompt rows) */
     CRUCIBLE_TUNE_DECODE_COMBINE_WIDTH = 8, /* decode splits merged per round trip: 8, 16 */
-    CRUCIBLE_TUNE_COUNT = 9
+    CRUCIBLE_TUNE_PREFILL_P16 = 9,         /* prefill P operand: 1 one fp16 (default), 0 fp16 hi + lo */
+    CRUCIBLE_TUNE_COUNT = 10
 };
 int crucible_attn_set_tuning(int key, int value);
 /* Current value of a key (-1: automatic, or an unknown key). */
@@ -266,6 +267,11 @@ int crucible_attention_split(const void* q, int q_dtype, const void* k_cache,
 /* ------------------------------------------------------------------ prefill
  * Causal attention for query rows whose keys are already in the pool. q is
  * [rows][n_head * head_dim], out likewise. Row r sees keys [0, pos_r].
+ * Arithmetic (head_dim 64): QK^T and PV on fp16 MFMAs with f32 accumulation, softmax in
+ * f32. P enters the PV product as one fp16 operand rounded to nearest even, so an output
+ * moves by at most 2^-11 sum_i w_i |v_i| from exact softmax weights (max-abs 4.4e-4 over
+ * the reference's corpus); CRUCIBLE_TUNE_PREFILL_P16 = 0 carries P as fp16 hi + lo (about
+ * 22 bits) for two PV products per block instead of one.
  */
 
 /* Replaces Gpu::attention_prefill_paged (gpu.rs:1502-1549; kernels.cu:1927-1936):

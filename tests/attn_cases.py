@@ -198,6 +198,17 @@ def oracle_out(fx: Fixture, q=None) -> np.ndarray:
                                        layer=LAYER)
 
 
+def oracle_abs_v(fx: Fixture, q=None) -> np.ndarray:
+    """The same attention over |V| (fp16 sign bits cleared): per output element the weighted
+    mean sum_i w_i |v_i| of its row's softmax weights, which bounds what rounding the weights
+    can move it by (gates.element_gate's P16 term)."""
+    q = fx.q if q is None else q
+    return oracle.attention_paged_rows(q, fx.k_pool, fx.v_pool & np.uint16(0x7FFF), fx.tables,
+                                       fx.positions + 1, table_index=fx.owners, n_head=HEADS,
+                                       n_kv_head=KV_HEADS, head_dim=HD, table_stride=STRIDE,
+                                       n_layer=LAYERS, layer=LAYER)
+
+
 def random_pools(rng, n_pages, n_layer, kv_dim, scale=1.0):
     n = n_pages * n_layer * 16 * kv_dim
     k = oracle.f32_to_f16_bits(rng.standard_normal(n).astype(np.float32) * scale)

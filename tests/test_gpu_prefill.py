@@ -8,7 +8,9 @@ compared with the f64 oracle on every element under the reference's element gate
 exact: future-page poison leaves outputs bit-identical (:597-632), descriptor composition,
 order and page reuse leave each request's bits unchanged (:639-682), and output rows outside
 the written range keep their sentinel (:23, :271-287). Both prefill kernels (LDS-tiled and
-register-direct) run every test.
+register-direct) run every test in both precisions of P: the default single fp16 operand
+(P16, gated with the rounding term 2^-11 sum w|v| added to the element gate) and the fp16
+hi + lo pair (about 22 bits, the reference's gate as it stands).
 """
 import numpy as np
 import pytest
@@ -21,12 +23,26 @@ from gates import element_gate
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(autouse=True, params=["lds", "direct"])
+_P16 = [True]  # precision of the running test's prefill_form
+
+
+@pytest.fixture(autouse=True, params=["lds", "direct", "lds-hilo", "direct-hilo"])
 def prefill_form(request, tune):
-    """Every test runs through both prefill kernels: the LDS-tiled form and the
-    register-direct form (the library picks one by grid size; the override forces it)."""
-    tune(prefill_direct=1 if request.param == "direct" else 0)
-    return request.param
+    """Every test runs through both prefill kernels, the LDS-tiled form and the
+    register-direct form (the library picks one by grid size; the override forces it), with
+    P as one fp16 operand (the default) and as fp16 hi + lo."""
+    form = request.param
+    _P16[0] = not form.endswith("-hilo")
+    tune(prefill_direct=1 if form.startswith("direct") else 0, prefill_p16=int(_P16[0]))
+    return form
+
+
+def gate(got, want, what, fx=None, q=None, vabs=None, out_f16=False):
+    """element_gate with the P16 rounding term when the running form carries P16 (vabs from
+    the oracle over |V| of fx, or given)."""
+    if _P16[0] and vabs is None:
+        vabs = A.oracle_abs_v(fx, q=q)
+    return element_gate(got, want, what, out_f16=out_f16, vabs=vabs if _P16[0] else None)
 
 
 def _dev(a, dev):
@@ -80,12 +96,13 @@ CASES = A.cases()
 def test_corpus_segments_and_owners_match_oracle(gpu, dev, case):
     fx = A.fixture(case)
     want = A.oracle_out(fx)
+    vabs = A.oracle_abs_v(fx) if _P16[0] else None
     d = Device(fx, dev)
     errs = []
     for runner in (run_segments, run_owners):
         d.reset()
         runner(gpu, d)
-        errs.append(element_gate(d.result(), want, f"{case.name} {runner.__name__}"))
+        errs.append(gate(d.result(), want, f"{case.name} {runner.__name__}", vabs=vabs))
     print(f"{case.name}: segments {errs[0]:.3e} owners {errs[1]:.3e}")
 
 
@@ -94,8 +111,9 @@ _FUZZ_ORACLE = {}
 
 
 def _fuzz_oracle():
-    """f64 oracle outputs of the 64 fuzz cases, computed once per session on up to 16 host
-    threads (the C oracle releases the interpreter lock)."""
+    """f64 oracle outputs of the 64 fuzz cases, and of the same cases over |V| (the P16
+    term), computed once per session on up to 16 host threads (the C oracle releases the
+    interpreter lock)."""
     if not _FUZZ_ORACLE:
         import concurrent.futures
         import os
@@ -103,7 +121,8 @@ def _fuzz_oracle():
         workers = max(1, min(16, len(os.sched_getaffinity(0))))
         with concurrent.futures.ThreadPoolExecutor(workers) as ex:
             outs = list(ex.map(lambda c: A.oracle_out(A.fixture(c)), FUZZ))
-        _FUZZ_ORACLE.update({c.name: o for c, o in zip(FUZZ, outs)})
+            absv = list(ex.map(lambda c: A.oracle_abs_v(A.fixture(c)), FUZZ))
+        _FUZZ_ORACLE.update({c.name: (o, a) for c, o, a in zip(FUZZ, outs, absv)})
     return _FUZZ_ORACLE
 
 
@@ -121,8 +140,9 @@ def test_fuzz_corpus_matches_oracle(gpu, dev):
         for runner in (run_segments, run_owners):
             d.reset()
             runner(gpu, d)
-            worst = max(worst, element_gate(d.result(), want_all[case.name],
-                                            f"{case.name} {runner.__name__}"))
+            want, vabs = want_all[case.name]
+            worst = max(worst, gate(d.result(), want, f"{case.name} {runner.__name__}",
+                                    vabs=vabs))
     print(f"fuzz corpus ({len(FUZZ)} cases): max-abs {worst:.3e}")
 
 
@@ -186,7 +206,8 @@ def test_single_sequence_params_and_contiguous_forms(gpu, dev):
                                     A.HEADS, A.KV_HEADS, A.HD, A.LAYERS, A.LAYER, A.KD,
                                     A.CONTEXT, params)
         got = d.result()[:rows]
-        element_gate(got, want[:rows], f"{case.name} params form")
+        gate(got, want[:rows], f"{case.name} params form",
+             vabs=A.oracle_abs_v(fx)[:rows] if _P16[0] else None)
         # contiguous cache holding the same history for that request at layer 1
         cap = A.CONTEXT
         k_c = np.zeros(A.LAYERS * cap * A.KD, np.uint16)
@@ -248,7 +269,7 @@ def test_fp16_query_and_fp16_output(gpu, dev):
                                 len(case.slices), fx.max_chunk, A.STRIDE, A.HEADS, A.KV_HEADS,
                                 A.HD, A.LAYERS, A.LAYER, A.KD)
     torch.cuda.synchronize()
-    element_gate(out16.float().cpu().numpy(), want, "fp16 query and output", out_f16=True)
+    gate(out16.float().cpu().numpy(), want, "fp16 query and output", fx=fx, q=q16, out_f16=True)
 
 
 def _packed_config_check(gpu, dev, cfg, seed):
@@ -283,7 +304,14 @@ def _packed_config_check(gpu, dev, cfg, seed):
                                        positions + 1, table_index=owners, n_head=cfg.n_head,
                                        n_kv_head=cfg.n_kv_head, head_dim=64, table_stride=stride,
                                        n_layer=cfg.n_layer, layer=0)
-    err = element_gate(out.cpu().numpy(), want, cfg.name)
+    vabs = None
+    if _P16[0]:
+        vabs = oracle.attention_paged_rows(oracle.f16_bits_to_f32(q), kp, vp & np.uint16(0x7FFF),
+                                           cfg.tables, positions + 1, table_index=owners,
+                                           n_head=cfg.n_head, n_kv_head=cfg.n_kv_head,
+                                           head_dim=64, table_stride=stride, n_layer=cfg.n_layer,
+                                           layer=0)
+    err = gate(out.cpu().numpy(), want, cfg.name, vabs=vabs)
     print(f"{cfg.name}: max-abs {err:.3e}")
 
 

@@ -60,6 +60,7 @@ constexpr TuneKey kTuneKeys[CRUCIBLE_TUNE_COUNT] = {
     {"CRUCIBLE_LINEAR_TILE", 4, 32},          // projection tiles: 4, 16 or 32 (see below)
     {"CRUCIBLE_DECODE_COMBINE_WIDTH", 8, 16}, // splits merged per round trip: 8 or 16
     {"CRUCIBLE_PREFILL_P16", 0, 1},           // prefill P operand: fp16 hi + lo / one fp16
+    {"CRUCIBLE_PREFILL_M32", 0, 1},           // prefill 32-row waves on 32x32 MFMAs off / on
 };
 
 bool tune_value_ok(int key, int v) {
@@ -84,7 +85,7 @@ int parse_env(int key, const char* s) {
     const long v = std::strtol(s, &end, 10);
     if (end == s || *end != '\0') return -1;
     if (key == CRUCIBLE_TUNE_PREFILL_DIRECT || key == CRUCIBLE_TUNE_PREFILL_HEAVY_FIRST ||
-        key == CRUCIBLE_TUNE_PREFILL_P16)
+        key == CRUCIBLE_TUNE_PREFILL_P16 || key == CRUCIBLE_TUNE_PREFILL_M32)
         return v != 0;
     return tune_value_ok(key, (int)v) ? (int)v : -1;
 }

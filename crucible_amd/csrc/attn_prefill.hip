@@ -674,6 +674,419 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
     }
 }
 
+// ---------------------------------------------------------------- 32-row waves on 32x32 MFMAs
+//
+// The LDS form with 32 query rows per wave (the QB = 2 shape) on v_mfma_f32_32x32x16_f16:
+// the same workgroup (4 slots x 2 key-half waves), LDS ring, page staging and merge as
+// prefill_kernel, with the tile's products as 32x32 blocks. A 32x32x16 MFMA holds the
+// SIMD's issue port for a smaller share of its cycles than two 16x16x32 ones of the same
+// work, so more of the softmax's VALU work fits beside it.
+//
+// Operand layouts (measured on gfx950): lane L supplies A[m = L & 31][k = 8 (L >> 5) .. +7]
+// and B[k = 8 (L >> 5) .. +7][n = L & 31]; result element i of lane L is
+// D[m = 8 (i >> 2) + 4 (L >> 5) + (i & 3)][n = L & 31]. Lane L serves query row L & 31 of
+// its wave; the half hh = L >> 5 picks which keys (S^T) or dims (O^T) of that row it holds.
+//   S^T[32 keys][32 rows] = K[32 keys][64] . Q^T[64][32 rows]     4 MFMAs per 32-key block
+//   O^T[32 dims][32 rows] += V^T[32 dims][16 keys] . P^T[16 keys][32 rows]
+//                                                    2 dim blocks x 4 16-key steps per tile
+typedef float float16v_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float16v_t mfma_32x32x16(half8_t a, half8_t b, float16v_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Key of S^T row m within a 32-key block: m = 8 I + 4 h + r holds key 16 (I >> 1) + 8 h +
+// 4 (I & 1) + r. Result element i of a lane in half hh is then key 16 (i >> 3) + 8 hh + (i & 7),
+// so elements 8 s .. 8 s + 7 are keys 16 s + 8 hh .. +7: exactly the k range that lane supplies
+// to the PV product of 16-key step s, read straight from the accumulator.
+__device__ __forceinline__ int key32(int m) {
+    return 16 * (m >> 4) + 8 * ((m >> 2) & 1) + 4 * ((m >> 3) & 1) + (m & 3);
+}
+
+// Row max of a lane's 32 scores (two 32-key blocks), then over the two halves holding the same
+// row (v_permlane32_swap). Two asm blocks (operand count); the first opens with 24 wait states
+// for the 32x32 MFMA results it reads, which also covers the second block's inputs.
+__device__ __forceinline__ float tile_max32(const float16v_t& s0, const float16v_t& s1) {
+    float r, t;
+    asm("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\t"
+        "v_max3_f32 %0, %1, %2, %3\n\t"
+        "v_max3_f32 %0, %0, %4, %5\n\t"
+        "v_max3_f32 %0, %0, %6, %7\n\t"
+        "v_max3_f32 %0, %0, %8, %9\n\t"
+        "v_max3_f32 %0, %0, %10, %11\n\t"
+        "v_max3_f32 %0, %0, %12, %13\n\t"
+        "v_max3_f32 %0, %0, %14, %15\n\t"
+        "v_max_f32 %0, %0, %16"
+        : "=&v"(r)
+        : "v"(s0[0]), "v"(s0[1]), "v"(s0[2]), "v"(s0[3]), "v"(s0[4]), "v"(s0[5]), "v"(s0[6]),
+          "v"(s0[7]), "v"(s0[8]), "v"(s0[9]), "v"(s0[10]), "v"(s0[11]), "v"(s0[12]),
+          "v"(s0[13]), "v"(s0[14]), "v"(s0[15]));
+    asm("v_max3_f32 %0, %0, %2, %3\n\t"
+        "v_max3_f32 %0, %0, %4, %5\n\t"
+        "v_max3_f32 %0, %0, %6, %7\n\t"
+        "v_max3_f32 %0, %0, %8, %9\n\t"
+        "v_max3_f32 %0, %0, %10, %11\n\t"
+        "v_max3_f32 %0, %0, %12, %13\n\t"
+        "v_max3_f32 %0, %0, %14, %15\n\t"
+        "v_max3_f32 %0, %0, %16, %17\n\t"
+        "v_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\t"
+        "v_permlane32_swap_b32 %0, %1\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32 %0, %0, %1"
+        : "+v"(r), "=&v"(t)
+        : "v"(s1[0]), "v"(s1[1]), "v"(s1[2]), "v"(s1[3]), "v"(s1[4]), "v"(s1[5]), "v"(s1[6]),
+          "v"(s1[7]), "v"(s1[8]), "v"(s1[9]), "v"(s1[10]), "v"(s1[11]), "v"(s1[12]),
+          "v"(s1[13]), "v"(s1[14]), "v"(s1[15]));
+    return r;
+}
+
+// Sum of a value over the two halves holding the same row (lanes L and L ^ 32).
+__device__ __forceinline__ float half_sum2(float x) {
+    float t;
+    asm("s_nop 0\n\t"
+        "v_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\t"
+        "v_permlane32_swap_b32 %0, %1\n\t"
+        "s_nop 1\n\t"
+        "v_add_f32 %0, %0, %1"
+        : "+v"(x), "=&v"(t));
+    return x;
+}
+
+// P of one 16-key step: p = exp2(s * scale - mu) for accumulator elements 8 s .. +7 of a
+// 32-key block, as the B operand of the PV product (one fp16, RNE, under P16; else fp16 hi +
+// lo as tile_p). Returns the eight values' sum.
+template <bool P16>
+__device__ __forceinline__ float step_p32(const float16v_t& st, int s, float scale, float mu,
+                                          half8_t& pb, half8_t& pl) {
+    typedef float float2_t __attribute__((ext_vector_type(2)));
+    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+    float pf[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pf[j] = fast_exp2(__builtin_fmaf(st[8 * s + j], scale, -mu));
+    u32x4_t hw, lw;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if constexpr (P16) {
+            hw[j] = __builtin_bit_cast(
+                uint32_t, __builtin_convertvector((float2_t{pf[2 * j], pf[2 * j + 1]}), half2_t));
+        } else {
+            hw[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pf[2 * j], pf[2 * j + 1]));
+        }
+    }
+    if constexpr (!P16) {
+        const float lo4[4] = {pf[0], pf[1], pf[2], pf[3]}, hi4[4] = {pf[4], pf[5], pf[6], pf[7]};
+        uint32_t a0, a1, b0, b1;
+        split_lo4(lo4, hw[0], hw[1], a0, a1);
+        split_lo4(hi4, hw[2], hw[3], b0, b1);
+        lw = u32x4_t{a0, a1, b0, b1};
+        pl = __builtin_bit_cast(half8_t, lw);
+    }
+    pb = __builtin_bit_cast(half8_t, hw);
+    return ((pf[0] + pf[1]) + (pf[2] + pf[3])) + ((pf[4] + pf[5]) + (pf[6] + pf[7]));
+}
+
+template <int HPW, bool QF32, int KB, bool P16>
+__global__ __launch_bounds__(kThreads) void prefill32_kernel(PrefillArgs a,
+                                                        const int32_t* __restrict__ tables) {
+    constexpr int RS = 4 / HPW;          // row slices per workgroup
+    constexpr int WROWS = 32;            // rows per wave
+    constexpr int R = RS * WROWS;        // rows per workgroup
+
+    __shared__ half_t s_k[KB][kKeyTile][64];   // [buf][key][dim], 16-byte chunks swizzled
+    __shared__ half_t s_v[KB][64][kKeyTile];   // page-major V^T, as prefill_kernel
+    __shared__ int s_owner[R];
+    __shared__ int s_pos[R];
+    __shared__ int s_row[R];
+    __shared__ uint64_t s_mask[2];
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int qr = lane & 31;   // the wave's query row this lane serves
+    const int hh = lane >> 5;   // which half of the row's keys / dims
+    const int kh = wave >> 2;   // key half: tile 2 i + kh of pair i
+    const int slot = wave & 3;
+    const int rs = slot / HPW;
+    const int hi = slot % HPW;
+
+    const WgPos wp = wg_pos(a);
+    const int groups_per_kv = a.n_rep / HPW;
+    const int g = wp.x / groups_per_kv;
+    const int h = g * a.n_rep + (wp.x % groups_per_kv) * HPW + hi;
+
+    // ---- rows of this tile: (packed row, owner, absolute position); -1 = none
+    int row = -1, owner = 0, pos = 0;
+    if (tid < R) {
+        tile_row(a, wp.req, wp.tile * R + tid, row, owner, pos);
+        s_row[tid] = row;
+        s_owner[tid] = owner;
+        s_pos[tid] = pos;
+    }
+    const uint64_t vmask = __ballot(tid < R && row >= 0);
+    if (wave < 2 && lane == 0) s_mask[wave] = vmask;
+    __syncthreads();
+    const uint64_t mask0 = s_mask[0];
+    const uint64_t mask1 = R > 64 ? s_mask[1] : 0;
+    if (mask0 == 0 && mask1 == 0) return;  // uniform: no row of this tile is valid
+
+    const int64_t ld_q = (int64_t)a.n_head * kHeadDim;
+    const int ri = rs * WROWS + qr;
+    const int my_row = s_row[ri];
+    const int my_pos = s_pos[ri];
+    float m = -INFINITY, l = 0.0f;
+    float16v_t acc[2] = {};
+    half8_t qh[4] = {}, ql[4] = {};
+    // Q^T operand of K step t4: dims 16 t4 + 8 hh .. +7 of this lane's row
+    auto load_queries = [&]() {
+        if (my_row < 0) return;
+        const int64_t off = (int64_t)my_row * ld_q + (int64_t)h * kHeadDim + 8 * hh;
+        if constexpr (QF32) {
+            const float* qp = static_cast<const float*>(a.q) + off;
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float x = qp[16 * t4 + j];
+                    qh[t4][j] = (half_t)x;
+                    ql[t4][j] = (half_t)(x - (float)qh[t4][j]);
+                }
+        } else {
+            const half_t* qp = static_cast<const half_t*>(a.q) + off;
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) qh[t4] = *reinterpret_cast<const half8_t*>(qp + 16 * t4);
+        }
+    };
+
+    const int kv_dim = a.addr.kv_dim;
+    typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+    const int first_valid = mask0 ? __builtin_ctzll(mask0) : 64 + __builtin_ctzll(mask1);
+    const int last_valid = mask1 ? 127 - __builtin_clzll(mask1) : 63 - __builtin_clzll(mask0);
+    const int wlo = rs * WROWS, whi = rs * WROWS + WROWS;
+    const int my_page = wave >> 1;
+    bool first_run = true;
+    int r0 = a.mode == kOwners ? 0 : first_valid;
+    while (r0 < R) {
+        int r1, own, hist_end, wave_last;
+        if (a.mode != kOwners) {
+            r1 = last_valid + 1;
+            own = s_owner[r0];
+            hist_end = s_pos[last_valid] + 1;
+            const int lo = max(r0, wlo), hi2 = min(r1, whi);
+            wave_last = lo < hi2 ? s_pos[hi2 - 1] : -1;
+        } else {
+            while (r0 < R && s_row[r0] < 0) ++r0;
+            if (r0 >= R) break;
+            own = s_owner[r0];
+            r1 = r0 + 1;
+            while (r1 < R && s_row[r1] >= 0 && s_owner[r1] == own) ++r1;
+            hist_end = 0;
+            for (int r = r0; r < r1; ++r) hist_end = max(hist_end, s_pos[r] + 1);
+            wave_last = -1;
+            for (int r = max(r0, wlo); r < min(r1, whi); ++r) wave_last = max(wave_last, s_pos[r]);
+        }
+        r0 = __builtin_amdgcn_readfirstlane(r0);
+        r1 = __builtin_amdgcn_readfirstlane(r1);
+        own = __builtin_amdgcn_readfirstlane(own);
+        hist_end = __builtin_amdgcn_readfirstlane(hist_end);
+        wave_last = __builtin_amdgcn_readfirstlane(wave_last);
+
+        const bool paged = tables != nullptr;
+        const const_i32_ptr table = paged ? (const_i32_ptr)(tables + (int64_t)own * a.table_stride)
+                                          : (const_i32_ptr)a.k_pool;
+        const int n_tiles = (hist_end + kKeyTile - 1) / kKeyTile;
+        const int last_page = (hist_end - 1) >> kPageShift;
+        auto page_of = [&](int t) -> int64_t {
+            const int idx = min(4 * t + my_page, last_page);
+            const int id = table[paged ? idx : 0];
+            return paged ? (int64_t)id : (int64_t)idx;
+        };
+        // the staging of prefill_kernel: wave w moves K rows 8 (w & 1) .. +7 and V^T dims
+        // 32 (w & 1) .. +31 of page w >> 1
+        auto issue = [&](int t, int64_t page) {
+            const int buf = t % KB;
+            const int64_t base = block_base(a.addr, page);
+            {
+                const int krow = 8 * wave + (lane >> 3);
+                const int c = (lane & 7) ^ (krow & 7);
+                const half_t* src = a.k_pool + base + (int64_t)(krow & kPageMask) * kv_dim +
+                                    g * kHeadDim + 8 * c;
+                lds_dma16(src, lds_offset(&s_k[buf][8 * wave][0]));
+            }
+            {
+                const int d = 32 * (wave & 1) + (lane >> 1);
+                const int half = (lane & 1) ^ ((d >> 3) & 1);
+                const half_t* src = a.v_pool + base +
+                                    (int64_t)(g * kHeadDim + d) * kPageTokens + 8 * half;
+                lds_dma16(src, lds_offset(&s_v[buf][0][0] + my_page * 1024 + (wave & 1) * 512));
+            }
+        };
+
+        const bool in_run = my_row >= 0 && ri >= r0 && ri < r1;
+        constexpr int PS = KB / 2;
+        const int n_pairs = (n_tiles + 1) / 2;
+        const int tail_pair = (hist_end % kKeyTile) ? (n_tiles - 1) / 2 : -1;
+#pragma unroll
+        for (int p = 0; p < PS - 1; ++p)
+            if (p < n_pairs) {
+                const int64_t pa = page_of(2 * p), pb = page_of(2 * p + 1);
+                issue(2 * p, pa);
+                issue(2 * p + 1, pb);
+            }
+        if (first_run) {
+            load_queries();
+            __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+            first_run = false;
+        }
+        for (int ip = 0; ip < n_pairs; ++ip) {
+            const int ahead = min(PS - 2, n_pairs - 1 - ip);
+            if (ahead >= 2) __builtin_amdgcn_s_waitcnt(kWaitVm8Lgkm0);
+            else if (ahead == 1) __builtin_amdgcn_s_waitcnt(kWaitVm4Lgkm0);
+            else __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+            if (ip == tail_pair) {
+                const int t = n_tiles - 1;
+                const int d = 32 * (wave & 1) + (lane >> 1);
+                const int half = (lane & 1) ^ ((d >> 3) & 1);
+                const int nv = hist_end - (t * kKeyTile + 16 * my_page + 8 * half);
+                if (nv < 8) {
+                    half8_t* chunk = reinterpret_cast<half8_t*>(
+                        &s_v[t % KB][0][0] + my_page * 1024 + (wave & 1) * 512) + lane;
+                    half8_t v = *chunk;
+#pragma unroll
+                    for (int r = 0; r < 8; ++r)
+                        if (r >= nv) v[r] = (half_t)0.0f;
+                    *chunk = v;
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            }
+            __builtin_amdgcn_s_barrier();
+            if (ip + PS - 1 < n_pairs) {
+                const int tn = 2 * (ip + PS - 1);
+                const int64_t pa = page_of(tn), pb = page_of(tn + 1);
+                issue(tn, pa);
+                issue(tn + 1, pb);
+            }
+            const int t = 2 * ip + kh;
+            const int kbase = t * kKeyTile;
+            if (t < n_tiles && wave_last >= kbase) {
+                const int buf = t % KB;
+                // S^T blocks: st[kb2][i] = S^T[kbase + 32 kb2 + 16 (i >> 3) + 8 hh + (i & 7)][qr]
+                float16v_t st[2];
+#pragma unroll
+                for (int kb2 = 0; kb2 < 2; ++kb2) {
+                    const int krow = 32 * kb2 + key32(qr);
+                    float16v_t c = {};
+#pragma unroll
+                    for (int t4 = 0; t4 < 4; ++t4) {
+                        const half8_t ka = *reinterpret_cast<const half8_t*>(
+                            &s_k[buf][krow][8 * ((2 * t4 + hh) ^ (krow & 7))]);
+                        c = mfma_32x32x16(ka, qh[t4], c);
+                        if constexpr (QF32) c = mfma_32x32x16(ka, ql[t4], c);
+                    }
+                    st[kb2] = c;
+                }
+                // causal mask (a tile every row of the wave sees whole needs none): element i
+                // of block kb2 is visible iff 32 kb2 + 16 (i >> 3) + (i & 7) <= pos - kbase - 8 hh
+                if (!__all(in_run && my_pos >= kbase + kKeyTile - 1)) {
+                    const int lim = in_run ? my_pos - kbase - 8 * hh : -1;
+#pragma unroll
+                    for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i)
+                            st[kb2][i] = (32 * kb2 + 16 * (i >> 3) + (i & 7) <= lim) ? st[kb2][i]
+                                                                                      : -INFINITY;
+                }
+                const float tm = tile_max32(st[0], st[1]) * a.scale_log2;  // base-2 units
+                // lazy rescale, as prefill_kernel
+                const bool grow = tm > m + kLazyLog2;
+                if (__any(grow)) {
+                    const float alpha = grow ? fast_exp2(m - tm) : 1.0f;
+                    const float mn = grow ? tm : m;
+                    l *= alpha;
+                    acc[0] = acc[0] * alpha;
+                    acc[1] = acc[1] * alpha;
+                    m = mn;
+                }
+                const float mu = (m == -INFINITY) ? 0.0f : m;
+                // 16-key steps: keys 32 kb2 + 16 s .. +15 are page 2 kb2 + s of the tile; this
+                // lane's V^T operand is dims d, keys 8 hh .. +7 of that page, one 16-byte read
+#pragma unroll
+                for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        half8_t pb, pl;
+                        l += step_p32<P16>(st[kb2], s, a.scale_log2, mu, pb, pl);
+                        const int pg = 2 * kb2 + s;
+#pragma unroll
+                        for (int db2 = 0; db2 < 2; ++db2) {
+                            const int d = 32 * db2 + qr;
+                            const half8_t va = *reinterpret_cast<const half8_t*>(
+                                &s_v[buf][0][0] + pg * 1024 + d * 16 + 8 * (hh ^ ((d >> 3) & 1)));
+                            acc[db2] = mfma_32x32x16(va, pb, acc[db2]);
+                            if constexpr (!P16) acc[db2] = mfma_32x32x16(va, pl, acc[db2]);
+                        }
+                    }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+        __builtin_amdgcn_s_barrier();
+        if (a.mode != kOwners) break;
+        r0 = r1;
+    }
+
+    // ---- merge the key halves through the idle ring: acc (4 slots x 64 lanes x 32 floats,
+    // 32 KiB) in the K ring, m and l in the V ring, lane-major
+    static_assert(4 * 32 * 64 * sizeof(float) <= sizeof(s_k), "merge buffer");
+    float* s_macc = reinterpret_cast<float*>(&s_k[0][0][0]);
+    float* s_ml = reinterpret_cast<float*>(&s_v[0][0][0]);
+    if (kh == 1) {
+        float* p = s_macc + slot * 32 * 64 + lane;
+#pragma unroll
+        for (int db2 = 0; db2 < 2; ++db2)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) p[(16 * db2 + i) * 64] = acc[db2][i];
+        float* q = s_ml + slot * 2 * 64 + lane;
+        q[0] = m;
+        q[64] = l;
+    }
+    __syncthreads();
+    if (kh == 1) return;
+    {
+        const float* p = s_macc + slot * 32 * 64 + lane;
+        const float* q = s_ml + slot * 2 * 64 + lane;
+        const float m1 = q[0], l1 = q[64];
+        const float mx = fmaxf(m, m1);
+        const float mu = mx == -INFINITY ? 0.0f : mx;
+        const float w0 = fast_exp2(m - mu), w1 = fast_exp2(m1 - mu);
+        l = l * w0 + l1 * w1;
+#pragma unroll
+        for (int db2 = 0; db2 < 2; ++db2)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[db2][i] = acc[db2][i] * w0 + p[(16 * db2 + i) * 64] * w1;
+    }
+
+    // ---- normalise and write: element i of block db2 is dim 32 db2 + 8 (i >> 2) + 4 hh + (i & 3)
+    const float lt = half_sum2(l);
+    if (my_row < 0) return;
+    const float inv = 1.0f / lt;
+    const int64_t off = (int64_t)my_row * ld_q + (int64_t)h * kHeadDim + 4 * hh;
+#pragma unroll
+    for (int db2 = 0; db2 < 2; ++db2)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+            const float4_t o = {acc[db2][4 * i4] * inv, acc[db2][4 * i4 + 1] * inv,
+                                acc[db2][4 * i4 + 2] * inv, acc[db2][4 * i4 + 3] * inv};
+            const int64_t at = off + 32 * db2 + 8 * i4;
+            if (a.out_f16) {
+                const half4_t hv = {(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
+                *reinterpret_cast<half4_t*>(static_cast<half_t*>(a.out) + at) = hv;
+            } else {
+                *reinterpret_cast<float4_t*>(static_cast<float*>(a.out) + at) = o;
+            }
+        }
+}
+
 // ---------------------------------------------------------------- register-direct form
 //
 // Workgroup = 16 query rows of one head; its 8 waves split the causal key range, wave w
@@ -1041,9 +1454,30 @@ int launch_prefill_generic(PrefillArgs a, int hd, int64_t tile_rows_total, int64
     return fail_launch(what);
 }
 
+template <int HPW, bool QF32, bool P16>
+void launch_kb32(const PrefillArgs& a, int kb, dim3 grid, hipStream_t stream) {
+    if (kb == 6)
+        hipLaunchKernelGGL((prefill32_kernel<HPW, QF32, 6, P16>), grid, dim3(kThreads), 0, stream,
+                           a, a.tables);
+    else
+        hipLaunchKernelGGL((prefill32_kernel<HPW, QF32, 4, P16>), grid, dim3(kThreads), 0, stream,
+                           a, a.tables);
+}
+
 template <int HPW, int QB>
 void launch_hq(const PrefillArgs& a, bool q_f32, bool p16, int kb, dim3 grid,
                hipStream_t stream) {
+    // 32 rows per wave: the 32x32-MFMA kernel unless CRUCIBLE_TUNE_PREFILL_M32 = 0
+    if (QB == 2 && tuning(CRUCIBLE_TUNE_PREFILL_M32) != 0) {
+        if (q_f32) {
+            if (p16) launch_kb32<HPW, true, true>(a, kb, grid, stream);
+            else launch_kb32<HPW, true, false>(a, kb, grid, stream);
+        } else {
+            if (p16) launch_kb32<HPW, false, true>(a, kb, grid, stream);
+            else launch_kb32<HPW, false, false>(a, kb, grid, stream);
+        }
+        return;
+    }
     if (q_f32) {
         if (p16) launch_kb<HPW, QB, true, true>(a, kb, grid, stream);
         else launch_kb<HPW, QB, true, false>(a, kb, grid, stream);

@@ -88,7 +88,8 @@ enum crucible_tuning_key {
     CRUCIBLE_TUNE_LINEAR_TILE = 7,         /* projection tiles: 4 or 16 columns (decode), 32 (prompt rows) */
     CRUCIBLE_TUNE_DECODE_COMBINE_WIDTH = 8, /* decode splits merged per round trip: 8, 16 */
     CRUCIBLE_TUNE_PREFILL_P16 = 9,         /* prefill P operand: 1 one fp16 (default), 0 fp16 hi + lo */
-    CRUCIBLE_TUNE_COUNT = 10
+    CRUCIBLE_TUNE_PREFILL_M32 = 10,        /* prefill 32-row waves on 32x32 MFMAs: 1 (default), 0 */
+    CRUCIBLE_TUNE_COUNT = 11
 };
 int crucible_attn_set_tuning(int key, int value);
 /* Current value of a key (-1: automatic, or an unknown key). */

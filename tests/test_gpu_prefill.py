@@ -10,7 +10,9 @@ order and page reuse leave each request's bits unchanged (:639-682), and output 
 the written range keep their sentinel (:23, :271-287). Both prefill kernels (LDS-tiled and
 register-direct) run every test in both precisions of P: the default single fp16 operand
 (P16, gated with the rounding term 2^-11 sum w|v| added to the element gate) and the fp16
-hi + lo pair (about 22 bits, the reference's gate as it stands).
+hi + lo pair (about 22 bits, the reference's gate as it stands); the LDS-tiled form runs
+with 16 rows per wave and with 32 (the 32x32-MFMA kernel, and once over the corpus the
+16x16 kernel of that shape).
 """
 import numpy as np
 import pytest
@@ -26,14 +28,17 @@ pytestmark = pytest.mark.gpu
 _P16 = [True]  # precision of the running test's prefill_form
 
 
-@pytest.fixture(autouse=True, params=["lds", "direct", "lds-hilo", "direct-hilo"])
+@pytest.fixture(autouse=True, params=["lds", "lds32", "direct", "lds-hilo", "lds32-hilo",
+                                        "direct-hilo"])
 def prefill_form(request, tune):
-    """Every test runs through both prefill kernels, the LDS-tiled form and the
-    register-direct form (the library picks one by grid size; the override forces it), with
-    P as one fp16 operand (the default) and as fp16 hi + lo."""
+    """Every test runs through every prefill kernel: the LDS-tiled form with 16 rows per wave
+    and with 32 (the 32x32-MFMA kernel), and the register-direct form (the library picks one
+    by grid size; the overrides force it), each with P as one fp16 operand (the default) and
+    as fp16 hi + lo."""
     form = request.param
     _P16[0] = not form.endswith("-hilo")
-    tune(prefill_direct=1 if form.startswith("direct") else 0, prefill_p16=int(_P16[0]))
+    tune(prefill_direct=1 if form.startswith("direct") else 0, prefill_p16=int(_P16[0]),
+         prefill_qb=2 if form.startswith("lds32") else 1 if form.startswith("lds") else None)
     return form
 
 
@@ -313,6 +318,23 @@ def _packed_config_check(gpu, dev, cfg, seed):
                                            layer=0)
     err = gate(out.cpu().numpy(), want, cfg.name, vabs=vabs)
     print(f"{cfg.name}: max-abs {err:.3e}")
+
+
+def test_qb2_on_16x16_mfma_matches_oracle(gpu, dev, tune, prefill_form):
+    """32 rows per wave on 16x16 MFMAs (CRUCIBLE_TUNE_PREFILL_M32 = 0, the other kernel for
+    that shape) over the corpus, both row modes, in the running form's precision."""
+    if not prefill_form.startswith("lds32"):
+        pytest.skip("the 32-row shape only")
+    tune(prefill_m32=0)
+    for case in CASES:
+        fx = A.fixture(case)
+        want = A.oracle_out(fx)
+        vabs = A.oracle_abs_v(fx) if _P16[0] else None
+        d = Device(fx, dev)
+        for runner in (run_segments, run_owners):
+            d.reset()
+            runner(gpu, d)
+            gate(d.result(), want, f"{case.name} {runner.__name__} (16x16, 32 rows)", vabs=vabs)
 
 
 def test_config1_causal_prefill_512(gpu, dev):

@@ -20,8 +20,9 @@ cpu_baseline = the reference's CPU attention path (gather + torch SDPA, fp32) on
          cores, on a bounded sample of the same workload.
 extras = the same step as the reference's three launches per layer and as attention
          alone, batch-1 decode (config 2), the MHA stress variant of config 3, the causal
-         (config 1) and packed (config 4) prefill kernels, and end-to-end greedy decoding of
-         the random-init 120m model at batch 16 (config 5, tok/s).
+         (config 1) and packed (config 4) prefill kernels, prefill of 2k..8k-token
+         sequences (the MFMA rate once a launch is compute-heavy), and end-to-end greedy
+         decoding of the random-init 120m model at batch 16 (config 5, tok/s).
 """
 from __future__ import annotations
 
@@ -49,12 +50,12 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true")
-    p.add_argument("--extras", default="decode,prefill,e2e",
+    p.add_argument("--extras", default="decode,prefill,pscale,e2e",
                    help="comma list of extra groups to run: decode (the other decode "
-                        "shapes), prefill (configs 1 and 4), e2e (config 5), scale (the "
-                        "fused decode at batch 32..256 with config 3's length "
-                        "distribution, and prefill of 2k..8k-token sequences; not in the "
-                        "default set), pscale (only the prefill part of scale)")
+                        "shapes), prefill (configs 1 and 4), pscale (prefill of 2k..8k-token "
+                        "sequences), e2e (config 5), scale (pscale plus the fused decode at "
+                        "batch 32..256 with config 3's length distribution; not in the "
+                        "default set)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run 5 more plain 256 MiB device copies (PMC traffic calibration)")
 
@@ -315,8 +316,11 @@ def bench_prefill(gpu, dev, cfg, launches: int = 50, q_dtype=None, cpu_inputs=No
             vs.append(gather_rows(v_pool, d_tab[i], int(n), 1, 0, kv_dim, True))
         cpu_inputs.update(q=q.float().cpu().numpy(), k=torch.cat(ks).float().cpu().numpy(),
                           v=torch.cat(vs).float().cpu().numpy())
+    from crucible_amd import _lib
+    p16 = _lib.load().crucible_attn_get_tuning(_lib.TUNE_KEYS["prefill_p16"]) != 0
     return {"workload": cfg.name, "n_head": cfg.n_head, "n_kv_head": cfg.n_kv_head,
             "q_dtype": str(q.dtype).replace("torch.", ""),
+            "p_operand": "one fp16 (RNE)" if p16 else "fp16 hi + lo",
             "seq_lens": [int(x) for x in cfg.seq_lens], "flops": cfg.flops(),
             "us_per_launch": round(avg * 1e3, 3),
             "us_per_launch_eager": round(eager * 1e3, 3), "us_median_eager": round(ms[len(ms) // 2] * 1e3, 3),
@@ -599,7 +603,8 @@ def main():
                                     ("seq8192_12h", [8192], 12, 12),
                                     ("packed8x2048_16h4kv", [2048] * 8, 16, 4)):
             r = bench_prefill(gpu, dev, W.prefill_sequences(name, lens, nh, nkv), launches=10)
-            pscale[name] = {k: r[k] for k in ("us_per_launch", "tflops", "frac_of_mfma_f16_peak")}
+            pscale[name] = {k: r[k] for k in ("us_per_launch", "tflops", "frac_of_mfma_f16_peak",
+                                              "p_operand")}
             torch.cuda.empty_cache()
         extras["prefill_scale"] = pscale
     if "prefill" in groups:

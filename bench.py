@@ -445,6 +445,38 @@ def copy_bandwidth(dev, mib: int = 256, reps: int = 10):
     return 2 * (mib << 20) / (ms * 1e-3) / 1e9
 
 
+def launch_floor_us(dev, launches: int = 12, reps: int = 50):
+    """Time per launch of a one-element fill kernel, `launches` back to back in one HIP
+    graph and replayed as the decode step is: what any kernel of a captured step costs
+    before it does any work (dispatch, wave launch, end-of-kernel release)."""
+    import torch
+
+    x = torch.zeros(1, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        x.fill_(1.0)
+    stream.wait_stream(side)
+    torch.cuda.synchronize(dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(launches):
+            x.fill_(1.0)
+    for _ in range(5):
+        g.replay()
+    torch.cuda.synchronize(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    us = e0.elapsed_time(e1) * 1e3 / (reps * launches)
+    del g
+    return us
+
+
 # What the decode kernel is built from: its translation unit, the headers it includes and
 # the build script that holds its compiler flags.
 DECODE_SOURCES = ("crucible_amd/csrc/attn_decode.hip", "crucible_amd/csrc/common.hpp",
@@ -524,6 +556,8 @@ def main():
     kernel = decode_kernel_name(gpu, 16, 12, args.kv_heads, 2048, 1)
     copy_gbs = copy_bandwidth(dev)
     log(f"device copy: {copy_gbs:.1f} GB/s (read + write)")
+    floor_us = launch_floor_us(dev)
+    log(f"launch floor: {floor_us:.2f} us per launch of a one-element kernel in a graph")
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": pmc_traffic(kernel),
@@ -533,6 +567,7 @@ def main():
                 "algorithmic_bytes_per_launch": int(bytes_per_launch),
                 "copy_gbs": round(copy_gbs, 1),
                 "frac_of_copy": round(achieved / copy_gbs, 4),
+                "launch_floor_us": round(floor_us, 3),
                 "source_sha": source_sha()}
     del step_graphs
 

@@ -58,6 +58,12 @@ def parse_args():
                         "default set)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run 5 more plain 256 MiB device copies (PMC traffic calibration)")
+    p.add_argument("--phases", action="store_true",
+                   help="diagnostic: run config 3 on the stamped twin of the library "
+                        "(libcrucible_attn_stamps.so) and print where the fused decode "
+                        "launch's time goes, per phase, instead of the bench line")
+    p.add_argument("--phase-reps", type=int, default=28,
+                   help="--phases: replayed steps whose last launch is read")
 
     return p.parse_args()
 
@@ -445,6 +451,101 @@ def copy_bandwidth(dev, mib: int = 256, reps: int = 10):
     return 2 * (mib << 20) / (ms * 1e-3) / 1e9
 
 
+PHASES = ("prologue", "loads", "compute", "merge", "publish", "counter", "combine")
+
+
+def decode_phases(gpu, dev, args, log):
+    """Per-workgroup phase stamps of the fused config-3 decode launch (the stamped library).
+
+    Each replay of a step graph runs the 12 layer launches back to back; the stamps left
+    afterwards are those of the last one. Per workgroup, from its slots (StampSlot in
+    attn_decode.hip): start skew (entry against the launch's first entry), prologue (entry
+    to the lengths and page ids in and the K/V loads issued), loads (to wave 0's pages
+    resident), compute (wave 0's products issued), merge (to every wave past the LDS
+    merge), publish (partial acknowledged, or the output stored for a one-split unit),
+    counter (split counter returned) and, for the combining workgroup, combine (output
+    stored). `chain` is the launch's first entry to its last stamp.
+    """
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from crucible_amd import _lib
+    from crucible_amd import workloads as W
+
+    fn = gpu.lib.crucible_debug_decode_stamps
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                   ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]
+    fn.restype = ctypes.c_int
+    khz, slots = ctypes.c_int(0), ctypes.c_int(0)
+    _lib.check(fn(None, 0, 1, ctypes.byref(khz), ctypes.byref(slots)))
+    rows = 8192
+    buf = np.zeros((rows, slots.value), np.uint64)
+
+    b16 = DecodeBench(gpu, dev, batch=16, n_head=12, n_kv_head=args.kv_heads, n_layer=12,
+                      n_pages=8192, max_seq=2048, rotations=7, seed=W.BASE_SEED + 2)
+    graphs = b16.capture("fused")
+    ms, ev, _ = b16.time_steps(graphs, 60, 10)
+    kernel = decode_kernel_name(gpu, 16, 12, args.kv_heads, 2048, 1)
+    log(f"stamped build: {ev * 1e3 / 12:.2f} us per launch (events), kernel {kernel}")
+    us_per_tick = 1e3 / khz.value
+    launches = []
+    for rep in range(args.phase_reps):
+        _lib.check(fn(None, 0, 1, ctypes.byref(khz), ctypes.byref(slots)))
+        graphs[rep % len(graphs)].replay()
+        torch.cuda.synchronize(dev)
+        _lib.check(fn(buf.ctypes.data, rows, 0, ctypes.byref(khz), ctypes.byref(slots)))
+        launches.append(buf.copy())
+    out = summarize_stamps(launches, us_per_tick)
+    return {"kernel": kernel, "clock_khz": khz.value, "stamped_us_per_launch": round(ev * 1e3 / 12, 3),
+            **out}
+
+
+def summarize_stamps(launches, us_per_tick: float) -> dict:
+    """Phase durations (median, p90, max over workgroups and launches) from stamp rows of
+    one launch each (uint64 [rows][9]: StampSlot order, slot 8 the meta word), and the
+    phases of each launch's last-finishing workgroup."""
+    import numpy as np
+
+    per = {k: [] for k in ("skew",) + PHASES + ("chain",)}
+    crit = []
+    n_wg = 0
+    for buf in launches:
+        meta = buf[:, 8]
+        kind = (meta >> np.uint64(52)) & np.uint64(0xF)
+        n_active = ((meta >> np.uint64(32)) & np.uint64(0xFFFF)).astype(np.int64)
+        last = ((meta >> np.uint64(48)) & np.uint64(1)).astype(bool)
+        att = (buf[:, 0] != 0) & (kind == 0) & (buf[:, 5] != 0)
+        n_wg = int(att.sum())
+        t = buf[att, :8].astype(np.int64)
+        multi = n_active[att] > 1
+        comb = multi & last[att]
+        t0 = t[:, 0].min()
+        # a one-split unit stops at slot 5, a non-combining split at slot 6 (later slots
+        # may hold an earlier launch's values)
+        end = np.where(comb, t[:, 7], np.where(multi, t[:, 6], t[:, 5]))
+        d = np.diff(t, axis=1) * us_per_tick  # slots 0..7 -> the 7 phases
+        per["skew"] += list((t[:, 0] - t0) * us_per_tick)
+        for i, name in enumerate(PHASES[:5]):
+            per[name] += list(d[:, i])
+        per["counter"] += list(d[multi, 5])
+        per["combine"] += list(d[comb, 6])
+        per["chain"].append(float((end.max() - t0) * us_per_tick))
+        w = int(np.argmax(end))
+        n_ph = 7 if comb[w] else 6 if multi[w] else 5
+        crit.append({"skew": round(float((t[w, 0] - t0) * us_per_tick), 2),
+                     **{PHASES[i]: round(float(d[w, i]), 2) for i in range(n_ph)}})
+    summary = {}
+    for k, v in per.items():
+        a = np.asarray(v, np.float64)
+        summary[k] = {"median_us": round(float(np.median(a)), 3),
+                      "p90_us": round(float(np.percentile(a, 90)), 3),
+                      "max_us": round(float(a.max()), 3), "n": int(a.size)}
+    return {"launches_read": len(launches), "workgroups_per_launch": n_wg,
+            "phases": summary, "critical_workgroup": crit[:8]}
+
+
 def launch_floor_us(dev, launches: int = 12, reps: int = 50):
     """Time per launch of a one-element fill kernel, `launches` back to back in one HIP
     graph and replayed as the decode step is: what any kernel of a captured step costs
@@ -519,6 +620,9 @@ def main():
     import numpy as np  # noqa: F401
     import torch
 
+    if args.phases:  # bind the stamped twin before anything loads the product library
+        from crucible_amd import _build, _lib
+        _lib.load(_build.STAMPS_LIB_PATH)
     from crucible_amd import workloads as W
     from crucible_amd.gpu import Gpu, tuning_state
 
@@ -533,6 +637,9 @@ def main():
         print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
     log(f"{gpu.version()} on {torch.cuda.get_device_name(0)}")
+    if args.phases:
+        print(json.dumps(decode_phases(gpu, dev, args, log)), flush=True)
+        return
     b16 = DecodeBench(gpu, dev, batch=16, n_head=12, n_kv_head=args.kv_heads, n_layer=12,
                       n_pages=8192, max_seq=2048, rotations=7, seed=W.BASE_SEED + 2)
     log(f"config 3: {b16.rotations} rotations, lens of rotation 0: {b16.lens[0].tolist()}")

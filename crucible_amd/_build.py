@@ -1,7 +1,10 @@
 """Build the gfx950 shared library.
 
 ``build_library()`` compiles every source under ``csrc/`` with hipcc for gfx950 into
-``crucible_amd/libcrucible_attn.so`` (objects under ``crucible_amd/_build/``).
+``crucible_amd/libcrucible_attn.so`` (objects under ``crucible_amd/_build/``). It also links
+``libcrucible_attn_stamps.so``, a diagnostic twin in which the decode source is compiled with
+``-DCRUCIBLE_STAMPS`` (per-workgroup phase timestamps, read by ``bench.py --phases``); the
+product path never loads it.
 """
 from __future__ import annotations
 
@@ -14,6 +17,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB_PATH = os.path.join(HERE, "libcrucible_attn.so")
+STAMPS_LIB_PATH = os.path.join(HERE, "libcrucible_attn_stamps.so")
+STAMPS_SOURCE = "attn_decode.hip"
 
 ARCH = "gfx950"
 DEVICE_SOURCES = ["kv_append.hip", "attn_decode.hip", "attn_prefill.hip", "argmax.hip",
@@ -43,6 +48,18 @@ def _run(cmd):
     return proc
 
 
+def _compile_cmd(hipcc, src, obj, defines=()):
+    lang = ["-x", "hip"] if src.endswith(".cpp") else []
+    return [hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), *defines, *lang, "-c",
+            os.path.join(CSRC, src), "-o", obj]
+
+
+def _link(hipcc, objs, path):
+    tmp = path + ".tmp"
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
+    os.replace(tmp, path)
+
+
 def build_library(jobs: int = 8) -> str:
     os.makedirs(BUILD, exist_ok=True)
     hipcc = _hipcc()
@@ -51,14 +68,15 @@ def build_library(jobs: int = 8) -> str:
     for src in DEVICE_SOURCES:
         obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
-        lang = ["-x", "hip"] if src.endswith(".cpp") else []
-        cmds.append([hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), *lang, "-c",
-                     os.path.join(CSRC, src), "-o", obj])
+        cmds.append(_compile_cmd(hipcc, src, obj))
+    stamps_obj = os.path.join(BUILD, os.path.splitext(STAMPS_SOURCE)[0] + "_stamps.o")
+    cmds.append(_compile_cmd(hipcc, STAMPS_SOURCE, stamps_obj, ["-DCRUCIBLE_STAMPS"]))
     with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         list(ex.map(_run, cmds))
-    tmp = LIB_PATH + ".tmp"
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
-    os.replace(tmp, LIB_PATH)
+    _link(hipcc, objs, LIB_PATH)
+    stamps_objs = [stamps_obj if os.path.basename(o) == os.path.splitext(STAMPS_SOURCE)[0] + ".o"
+                   else o for o in objs]
+    _link(hipcc, stamps_objs, STAMPS_LIB_PATH)
     return LIB_PATH
 
 

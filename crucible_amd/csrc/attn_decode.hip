@@ -91,6 +91,70 @@ struct DecodeArgs {
 };
 
 
+#ifdef CRUCIBLE_STAMPS
+// Phase stamps, compiled only into the diagnostic libcrucible_attn_stamps.so (built from
+// this file with -DCRUCIBLE_STAMPS; the product library has none of this). Thread 0 of each
+// workgroup of decode_kernel records s_memrealtime (the chip-wide constant-rate clock)
+// when it reaches the end of a phase, in row `workgroup id` of g_decode_stamps; the last
+// slot holds what the workgroup served. stamp_after first waits for every memory
+// operation its wave has in flight, so the phase's loads or stores are complete; that wait
+// also holds back loads the product overlaps with the phase, so a stamped launch runs a
+// little longer than the product's.
+constexpr int kStampRows = 8192;
+enum StampSlot {
+    kStampStart,      // kernel entry
+    kStampPrologue,   // lengths and page ids in, the wave's K/V loads issued
+    kStampLoads,      // wave 0's K/V pages resident
+    kStampCompute,    // wave 0's QK, softmax and PV products issued
+    kStampMerged,     // every wave past the LDS merge barrier
+    kStampPublished,  // split partial acknowledged (or, for one split, the output stored)
+    kStampCounted,    // split counter returned
+    kStampCombined,   // the combining workgroup's output stored
+    kStampMeta,       // b | g << 16 | s << 24 | n_active << 32 | last << 48 | kind << 52
+    kStampSlots
+};
+__device__ uint64_t g_decode_stamps[kStampRows][kStampSlots];
+
+__device__ __forceinline__ unsigned stamp_row() {
+    return blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+}
+
+__device__ __forceinline__ void stamp_store(int slot, uint64_t t) {
+    if (threadIdx.x == 0 && stamp_row() < kStampRows) g_decode_stamps[stamp_row()][slot] = t;
+}
+
+__device__ __forceinline__ void stamp_now(int slot) {
+    asm volatile("" ::: "memory");
+    stamp_store(slot, __builtin_amdgcn_s_memrealtime());
+}
+
+__device__ __forceinline__ void stamp_after(int slot) {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    stamp_now(slot);
+}
+
+__device__ __forceinline__ void stamp_meta(int b, int g, int s, int n_active, int last, int kind) {
+    if (threadIdx.x == 0 && stamp_row() < kStampRows)
+        g_decode_stamps[stamp_row()][kStampMeta] =
+            (uint64_t)(b & 0xffff) | (uint64_t)(g & 0xff) << 16 | (uint64_t)(s & 0xff) << 24 |
+            (uint64_t)(n_active & 0xffff) << 32 | (uint64_t)(last & 1) << 48 |
+            (uint64_t)(kind & 0xf) << 52;
+}
+// The entry time is taken into a scalar at entry and stored with the next stamp (a
+// divergent store at the kernel's first instruction upsets the preloaded arguments).
+#define CRUCIBLE_STAMP_TAKE(var) const uint64_t var = __builtin_amdgcn_s_memrealtime()
+#define CRUCIBLE_STAMP_STORE(slot, var) stamp_store(slot, var)
+#define CRUCIBLE_STAMP_NOW(slot) stamp_now(slot)
+#define CRUCIBLE_STAMP_AFTER(slot) stamp_after(slot)
+#define CRUCIBLE_STAMP_META(...) stamp_meta(__VA_ARGS__)
+#else
+#define CRUCIBLE_STAMP_TAKE(var) ((void)0)
+#define CRUCIBLE_STAMP_STORE(slot, var) ((void)0)
+#define CRUCIBLE_STAMP_NOW(slot) ((void)0)
+#define CRUCIBLE_STAMP_AFTER(slot) ((void)0)
+#define CRUCIBLE_STAMP_META(...) ((void)0)
+#endif
+
 __device__ __forceinline__ int request_len(const DecodeArgs& a, int b) {
     const int len = a.lens[b * a.lens_stride + a.lens_off];
     return len < a.max_seq ? len : a.max_seq;  // never index past the table
@@ -416,6 +480,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
     a.batch = batch;
     a.lens_stride = lens_stride;
     a.lens_off = lens_off;
+    CRUCIBLE_STAMP_TAKE(t_start);
     static_assert(!ROPE || (QF32 && APPEND), "RoPE is fused for f32 rows with the append");
     __shared__ float4_t s_acc[WAVES][16][17];  // [wave][col][dim/4], padded
     __shared__ float s_m[WAVES][16];
@@ -440,7 +505,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
         CompactUnit u;
         const bool found = a.batch <= 64 ? compact_find<1, APPEND>(a, lane, u)
                                          : compact_find<kCompactPerLane, APPEND>(a, lane, u);
-        if (!found) return;  // uniform: no unit for this workgroup
+        if (!found) {  // uniform: no unit for this workgroup
+            CRUCIBLE_STAMP_META(0, 0, 0, 0, 0, 2);
+            return;
+        }
         const int bl = u.lane;
         const int qs = u.set;
         const int k = u.k;
@@ -536,7 +604,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
         apos = pos;
     const int n_pages = len > 0 ? (len + kPageMask) >> kPageShift : 0;
     const bool attend = u_begin < n_pages;
-    if (!attend && apos < 0) return;
+    if (!attend && apos < 0) {
+        CRUCIBLE_STAMP_META(b, g, s, 0, 0, 3);
+        return;
+    }
     // index of the appended row's page among this wave's pages (wave-uniform), or -1
     const int aidx = (apos >= 0 && (apos >> kPageShift) >= wp0 && (apos >> kPageShift) < wp0 + PAGES)
                          ? (apos >> kPageShift) - wp0 : -1;
@@ -553,6 +624,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
             for (int i = 0; i < PAGES; ++i)
                 if (i == aidx) store_new_row(a, nr, block_base(a.addr, page[i]), g, col, grp, aslot);
         }
+        CRUCIBLE_STAMP_META(b, g, s, 0, 0, 1);
         return;
     }
     const int n_active = (n_pages + (1 << a.split_shift) - 1) >> a.split_shift;
@@ -583,6 +655,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
                 va[i][db] = *reinterpret_cast<const half4_t*>(vp + db * 16 * kPageTokens);
         }
     }
+    CRUCIBLE_STAMP_STORE(kStampStart, t_start);
+    CRUCIBLE_STAMP_NOW(kStampPrologue);
+    CRUCIBLE_STAMP_AFTER(kStampLoads);
     if constexpr (ROPE) {
         // rotate the query, then split it into fp16 hi + lo as the plain f32 path does
 #pragma unroll
@@ -709,6 +784,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
     }
     m *= scale;  // the wave merge and the partials work in log2-scaled units
     l = group_sum4(l);
+    CRUCIBLE_STAMP_NOW(kStampCompute);
 
     // Merge the waves' states: acc[db][r] = O^T[16*db + 4*grp + r][col].
     if (grp == 0) {
@@ -718,6 +794,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
 #pragma unroll
     for (int db = 0; db < 4; ++db) s_acc[wave][col][4 * db + grp] = acc[db];
     __syncthreads();
+    CRUCIBLE_STAMP_NOW(kStampMerged);
 
     const int t = threadIdx.x;
     const int ccol = t >> 4;  // query head within the group
@@ -755,7 +832,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
             __builtin_amdgcn_s_waitcnt(0);
         }
     }
-    if (n_active == 1 || a.counters == nullptr) return;  // uniform across the workgroup
+    CRUCIBLE_STAMP_AFTER(kStampPublished);
+    if (n_active == 1 || a.counters == nullptr) {  // uniform across the workgroup
+        CRUCIBLE_STAMP_META(b, g, s, n_active, n_active == 1, 0);
+        return;
+    }
 
     __syncthreads();
     if (t == 0) {
@@ -765,10 +846,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
         if (last)  // ready for the next launch
             __hip_atomic_store(&a.counters[bg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = last;
+        CRUCIBLE_STAMP_AFTER(kStampCounted);
+        CRUCIBLE_STAMP_META(b, g, s, n_active, last, 0);
     }
     __syncthreads();
     if (!s_last) return;
     if (owner) combine_partials<CW>(a, b, hh, d4, n_active);
+    CRUCIBLE_STAMP_AFTER(kStampCombined);
 }
 
 // Second-pass combine for callers that own the partials without a counter
@@ -1492,3 +1576,32 @@ extern "C" int crucible_attention_split(const void* q, int q_dtype, const void* 
     a.po_bytes = (uint32_t)((size_t)n_head * a.n_splits * kHeadDim * sizeof(float));
     return launch_decode(a, sh, q_dtype == CRUCIBLE_F32, stream, what);
 }
+
+#ifdef CRUCIBLE_STAMPS
+// Diagnostic build only: copy the first `rows` rows of the phase stamps (*slots u64 each,
+// in StampSlot order) to `host`, then zero them on the device if `clear`. The clock's rate
+// in kHz goes to *clock_khz. Synchronous: it waits for the device first.
+extern "C" int crucible_debug_decode_stamps(uint64_t* host, int64_t rows, int clear,
+                                            int* clock_khz, int* slots) {
+    using namespace crucible;
+    const char* what = "crucible_debug_decode_stamps";
+    CRUCIBLE_CHECK(rows >= 0 && rows <= kStampRows && (rows == 0 || host) && clock_khz && slots,
+                   CRUCIBLE_ERR_INVALID, "%s: %lld rows (at most %d)", what, (long long)rows,
+                   kStampRows);
+    *slots = kStampSlots;
+    int dev = 0;
+    void* p = nullptr;
+    const size_t bytes = (size_t)rows * kStampSlots * sizeof(uint64_t);
+    const bool ok =
+        hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(clock_khz, hipDeviceAttributeWallClockRate, dev) == hipSuccess &&
+        hipDeviceSynchronize() == hipSuccess &&
+        (rows == 0 || hipMemcpyFromSymbol(host, HIP_SYMBOL(g_decode_stamps), bytes, 0,
+                                          hipMemcpyDeviceToHost) == hipSuccess) &&
+        (!clear || (hipGetSymbolAddress(&p, HIP_SYMBOL(g_decode_stamps)) == hipSuccess &&
+                    hipMemset(p, 0, sizeof(g_decode_stamps)) == hipSuccess &&
+                    hipDeviceSynchronize() == hipSuccess));
+    CRUCIBLE_CHECK(ok, CRUCIBLE_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(hipGetLastError()));
+    return CRUCIBLE_OK;
+}
+#endif

@@ -28,9 +28,10 @@ HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                "-Wall", "-Wno-unused-function"]
 # Per-source additions. The decode kernel's leading scalar arguments (the prologue's table,
-# length and position pointers, batch and length indexing: 6 arguments, 9 SGPRs) are
-# preloaded into SGPRs at wave launch, so its first loads do not wait for the argument block.
-EXTRA_FLAGS = {"attn_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=6"]}
+# length and position pointers, batch and length indexing, the unit plan: 7 arguments, 11
+# SGPRs) are preloaded into SGPRs at wave launch, so its first loads do not wait for the
+# argument block.
+EXTRA_FLAGS = {"attn_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=7"]}
 
 
 def _hipcc() -> str:

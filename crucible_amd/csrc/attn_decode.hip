@@ -73,6 +73,7 @@ struct DecodeArgs {
     float* pm;                   // [batch][n_head][n_splits]
     float* pl;                   // [batch][n_head][n_splits]
     uint32_t* counters;          // [batch * n_kv_head]; nullptr: combine in a second kernel
+    int32_t* plan;               // compact order's unit plan (kPlanUnits entries); nullptr: none
     PoolAddr addr;
     uint32_t po_bytes;           // size of po (buffer-resource bound)
     int kv_new_f16;
@@ -389,19 +390,30 @@ struct CompactUnit {
     int k, g, lane, set, len, pos, n_active, split_append;
 };
 
+// Lane L's requests L + 64 q: raw lengths (0 past the batch) and append positions (-1).
 template <int NQ, bool APPEND>
-__device__ __forceinline__ bool compact_find(const DecodeArgs& a, int lane, CompactUnit& u) {
-    int lc[NQ], na[NQ], sap[NQ], un[NQ], pv[NQ];
+__device__ __forceinline__ void compact_load(const DecodeArgs& a, int lane, int (&lv)[NQ],
+                                             int (&pv)[NQ]) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
         const int rq = lane + 64 * q;
-        int lv = 0;
+        lv[q] = 0;
         pv[q] = -1;
         if (rq < a.batch) {
-            lv = a.lens[rq * a.lens_stride + a.lens_off];
+            lv[q] = a.lens[rq * a.lens_stride + a.lens_off];
             if constexpr (APPEND) pv[q] = a.positions[rq];
         }
-        lc[q] = lv < a.max_seq ? lv : a.max_seq;  // never index past the table
+    }
+}
+
+template <int NQ, bool APPEND>
+__device__ __forceinline__ bool compact_search(const DecodeArgs& a, int lane, const int (&lv)[NQ],
+                                               const int (&pvl)[NQ], CompactUnit& u) {
+    int lc[NQ], na[NQ], sap[NQ], un[NQ], pv[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        pv[q] = pvl[q];
+        lc[q] = lv[q] < a.max_seq ? lv[q] : a.max_seq;  // never index past the table
         const int np = lc[q] > 0 ? (lc[q] + kPageMask) >> kPageShift : 0;
         na[q] = (np + (1 << a.split_shift) - 1) >> a.split_shift;
         sap[q] = (APPEND && pv[q] >= 0 && pv[q] < (a.max_pages << kPageShift))
@@ -460,6 +472,54 @@ __device__ __forceinline__ bool compact_find(const DecodeArgs& a, int lane, Comp
     return true;
 }
 
+template <int NQ, bool APPEND>
+__device__ __forceinline__ bool compact_find(const DecodeArgs& a, int lane, CompactUnit& u) {
+    int lv[NQ], pv[NQ];
+    compact_load<NQ, APPEND>(a, lane, lv, pv);
+    return compact_search<NQ, APPEND>(a, lane, lv, pv, u);
+}
+
+// The unit plan of the compact order. Every launch of a decode step sees the same lengths,
+// positions and tables, and so the same units; the search above costs a round trip for the
+// lengths before the one for the page ids. Entry i of the plan (in the workspace) records
+// what workgroup i found: its unit, the page ids of every wave and the lengths and
+// positions it was computed from. A later launch loads its entry in the same round trip as
+// the lengths and, if the recorded lengths, positions and geometry equal the current ones,
+// takes the unit and page ids from it; it still loads the page ids from the table beside
+// the K/V loads and reissues those loads if any id changed, so a table rewritten between
+// launches is always honoured. Otherwise it searches and rewrites its entry. Entry i is
+// read and written only by workgroup i of a launch (read before it is written), and a
+// launch sees the previous launch's entries (ordered on the stream); the entry is read
+// through the scalar cache, which is never asked for it again in the same launch.
+// Layout (int32): [0] id + 1 (0: never written), [1..9] geometry, [10] kind (0: past the
+// last unit, 1: a unit), [11..15] request, kv head, split, length, position; [32..63] page
+// ids, PAGES per wave; [64..127] raw lengths; [128..191] positions (batch <= 64).
+constexpr int kPlanUnits = 2048;
+constexpr int kPlanEntryInts = 192;
+constexpr int kPlanIds = 32;
+constexpr int kPlanLens = 64;
+constexpr int kPlanPos = 128;
+constexpr size_t kPlanBytes = (size_t)kPlanUnits * kPlanEntryInts * sizeof(int32_t);
+constexpr int kPlanMaxBatch = 64;
+
+constexpr int kPlanGeo = 9;
+constexpr int kPlanHead = 16;  // [0] id + 1, [1..9] geometry, [10] kind, [11..15] b g s len pos
+
+// What a plan entry's unit depends on besides the lengths and positions: the launch shape
+// (the kernel's append flag and pages and waves per split included).
+template <int PAGES, int WAVES, bool APPEND>
+__device__ __forceinline__ void plan_geometry(const DecodeArgs& a, int (&g)[kPlanGeo]) {
+    g[0] = a.batch;
+    g[1] = a.n_kv_head;
+    g[2] = a.split_shift;
+    g[3] = a.max_pages;
+    g[4] = a.max_seq;
+    g[5] = a.lens_stride;
+    g[6] = a.lens_off;
+    g[7] = a.table_stride;
+    g[8] = (APPEND ? 1 : 0) | PAGES << 1 | WAVES << 8;
+}
+
 // ORDER: how workgroup ids map to (split, kv head, request): kOrderSplit, grid (split,
 // kv head, request); kOrderRequest, grid (kv head, request, split); kOrderCompact, a 1-D
 // grid over the units that have work, found from the lengths (batch <= 256).
@@ -470,16 +530,17 @@ template <int PAGES, int WAVES, bool QF32, bool APPEND, bool PAGED, int ORDER, b
 __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
     const int32_t* __restrict__ tables, const int32_t* __restrict__ lens,
     const int32_t* __restrict__ positions, int batch, int lens_stride, int lens_off,
-    DecodeArgs a) {
+    int32_t* plan, DecodeArgs a) {
     // The leading arguments repeat what the prologue's first loads need (they are also in
     // `a`): the library is built with kernarg preloading, so they arrive in SGPRs and the
-    // length / page-id loads issue without waiting for the argument block to be fetched.
+    // length / plan / page-id loads issue without waiting for the argument block.
     a.tables = tables;
     a.lens = lens;
     a.positions = positions;
     a.batch = batch;
     a.lens_stride = lens_stride;
     a.lens_off = lens_off;
+    a.plan = plan;
     CRUCIBLE_STAMP_TAKE(t_start);
     static_assert(!ROPE || (QF32 && APPEND), "RoPE is fused for f32 rows with the append");
     __shared__ float4_t s_acc[WAVES][16][17];  // [wave][col][dim/4], padded
@@ -497,38 +558,128 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
     int s, g, b, len, pos = -1;
     int pid[PAGES] = {};  // this wave's page ids, through the scalar cache
     int u_begin, u_end;   // the unit's logical pages
+    typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+    bool planned = false;  // unit and page ids taken from the plan (compact order)
     if constexpr (ORDER == kOrderCompact) {
         // Workgroup i serves the i-th unit (compact_find), so the units take the lowest
         // workgroup ids and a launch whose units fit the CUs gets one CU per unit; the ids
         // past the last unit return at once. The page ids follow the lengths in a second
-        // round trip. One request per lane up to batch 64 keeps the search short there.
+        // round trip, unless the unit plan (batch <= 64, paged pools) holds this
+        // workgroup's unit for the current lengths: then one round trip loads both.
         CompactUnit u;
-        const bool found = a.batch <= 64 ? compact_find<1, APPEND>(a, lane, u)
-                                         : compact_find<kCompactPerLane, APPEND>(a, lane, u);
+        bool found;
+        if (a.batch <= kPlanMaxBatch) {
+            int lv[1], pv[1];
+            compact_load<1, APPEND>(a, lane, lv, pv);
+            const bool use_plan = PAGED && a.plan != nullptr && blockIdx.x < kPlanUnits;
+            int eh[kPlanHead] = {};
+            int epid[PAGES] = {};
+            int snap_l = 0, snap_p = -1;
+            if (use_plan) {  // uniform; issued beside the length loads
+                const int32_t* e = a.plan + (size_t)blockIdx.x * kPlanEntryInts;
+                const const_i32_ptr es = (const_i32_ptr)e;
+#pragma unroll
+                for (int j = 0; j < kPlanHead; ++j) eh[j] = es[j];
+#pragma unroll
+                for (int i = 0; i < PAGES; ++i) epid[i] = es[kPlanIds + wave * PAGES + i];
+                snap_l = e[kPlanLens + lane];
+                if constexpr (APPEND) snap_p = e[kPlanPos + lane];
+            }
+            int geo[kPlanGeo];
+            plan_geometry<PAGES, WAVES, APPEND>(a, geo);
+            bool ok = use_plan && eh[0] == (int)blockIdx.x + 1;
+#pragma unroll
+            for (int j = 0; j < kPlanGeo; ++j) ok = ok && eh[1 + j] == geo[j];
+            const bool lane_same = lane >= a.batch || (snap_l == lv[0] && snap_p == pv[0]);
+            planned = ok && __ballot(!lane_same) == 0;
+            if (planned) {
+                found = eh[10] != 0;
+                b = eh[11];
+                g = eh[12];
+                s = eh[13];
+                len = eh[14];
+                if constexpr (APPEND) pos = eh[15];
+#pragma unroll
+                for (int i = 0; i < PAGES; ++i) pid[i] = epid[i];
+            } else {
+                found = compact_search<1, APPEND>(a, lane, lv, pv, u);
+                if (found) {
+                    g = u.g;
+                    b = u.lane;
+                    len = u.len;
+                    if constexpr (APPEND) pos = u.pos;
+                    s = u.k < u.n_active ? u.k : u.split_append;
+                    if constexpr (PAGED) {
+                        const const_i32_ptr row =
+                            (const_i32_ptr)(a.tables + (int64_t)b * a.table_stride);
+                        const int i0 = (s << a.split_shift) + wave * PAGES;
+#pragma unroll
+                        for (int i = 0; i < PAGES; ++i) {
+                            pid[i] = row[min(i0 + i, a.max_pages - 1)];
+                            asm volatile("" : "+s"(pid[i]));  // issued here, not behind a branch
+                        }
+                    }
+                }
+                if (use_plan) {
+                    // Record the unit for the next launch (vector stores: this entry is
+                    // read again only by a later launch).
+                    int32_t* e = a.plan + (size_t)blockIdx.x * kPlanEntryInts;
+                    if (wave == 0) {
+                        int v = 0;
+                        if (lane == 0) v = (int)blockIdx.x + 1;
+#pragma unroll
+                        for (int j = 0; j < kPlanGeo; ++j)
+                            if (lane == 1 + j) v = geo[j];
+                        if (lane == 10) v = found ? 1 : 0;
+                        if (found) {
+                            if (lane == 11) v = b;
+                            if (lane == 12) v = g;
+                            if (lane == 13) v = s;
+                            if (lane == 14) v = len;
+                            if (lane == 15) v = pos;
+                        }
+                        if (lane < kPlanHead) e[lane] = v;
+                        if (lane < a.batch) {
+                            e[kPlanLens + lane] = lv[0];
+                            e[kPlanPos + lane] = pv[0];
+                        }
+                    }
+                    if (found) {
+                        int v = 0;
+#pragma unroll
+                        for (int i = 0; i < PAGES; ++i)
+                            if (lane == i) v = pid[i];
+                        if (lane < PAGES) e[kPlanIds + wave * PAGES + lane] = v;
+                    }
+                }
+            }
+        } else {
+            found = compact_find<kCompactPerLane, APPEND>(a, lane, u);
+            if (found) {
+                g = u.g;
+                b = u.lane + 64 * u.set;
+                len = u.len;
+                if constexpr (APPEND) pos = u.pos;
+                s = u.k < u.n_active ? u.k : u.split_append;
+                // The page ids are uniform per wave: scalar loads (the table in the
+                // constant address space: nothing writes it during the launch), which do
+                // not queue behind the vector loads of workgroups already streaming pages
+                // on this CU.
+                if constexpr (PAGED) {
+                    const const_i32_ptr row =
+                        (const_i32_ptr)(a.tables + (int64_t)b * a.table_stride);
+                    const int i0 = (s << a.split_shift) + wave * PAGES;
+#pragma unroll
+                    for (int i = 0; i < PAGES; ++i) {
+                        pid[i] = row[min(i0 + i, a.max_pages - 1)];
+                        asm volatile("" : "+s"(pid[i]));  // issued here, not behind a branch
+                    }
+                }
+            }
+        }
         if (!found) {  // uniform: no unit for this workgroup
             CRUCIBLE_STAMP_META(0, 0, 0, 0, 0, 2);
             return;
-        }
-        const int bl = u.lane;
-        const int qs = u.set;
-        const int k = u.k;
-        g = u.g;
-        b = bl + 64 * qs;
-        len = u.len;
-        if constexpr (APPEND) pos = u.pos;
-        s = k < u.n_active ? k : u.split_append;
-        // The page ids are uniform per wave: scalar loads (the table in the constant
-        // address space: nothing writes it during the launch), which do not queue behind
-        // the vector loads of workgroups already streaming pages on this CU.
-        if constexpr (PAGED) {
-            typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
-            const const_i32_ptr row = (const_i32_ptr)(a.tables + (int64_t)b * a.table_stride);
-            const int i0 = (s << a.split_shift) + wave * PAGES;
-#pragma unroll
-            for (int i = 0; i < PAGES; ++i) {
-                pid[i] = row[min(i0 + i, a.max_pages - 1)];
-                asm volatile("" : "+s"(pid[i]));  // issued here, not behind a branch
-            }
         }
     } else {
         // Grid (kv head, request, split), request-major: every request's first splits are
@@ -541,7 +692,6 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
         s = ORDER == kOrderRequest ? blockIdx.z : blockIdx.x;
         g = ORDER == kOrderRequest ? blockIdx.x : blockIdx.y;
         b = ORDER == kOrderRequest ? blockIdx.y : blockIdx.z;
-        typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
         const int len_raw = ((const_i32_ptr)a.lens)[b * a.lens_stride + a.lens_off];
         if constexpr (PAGED) {
             const const_i32_ptr row = (const_i32_ptr)(a.tables + (int64_t)b * a.table_stride);
@@ -616,8 +766,25 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
     // the appended K row use the same ones)
     RopeCS rc{};
     if constexpr (ROPE) rc = load_rope(a, pos, grp);
+    // A planned unit's page ids against the table: the table's ids, loaded now (scalar
+    // loads, beside the K/V loads issued with the plan's ids); true if any differs, with
+    // pid and page then holding the table's.
+    auto table_changed = [&]() -> bool {
+        const const_i32_ptr row = (const_i32_ptr)(a.tables + (int64_t)b * a.table_stride);
+        const int i0 = (s << a.split_shift) + wave * PAGES;
+        bool changed = false;
+#pragma unroll
+        for (int i = 0; i < PAGES; ++i) {
+            const int t = row[min(i0 + i, a.max_pages - 1)];
+            changed = changed || t != pid[i];
+            pid[i] = t;
+            page[i] = (int64_t)t;
+        }
+        return changed;
+    };
     if (!attend) {
         // append only: the row lies past the attended length
+        if (PAGED && planned) (void)table_changed();
         if (aidx >= 0) {
             const NewRow nr = finish_row<ROPE>(a, load_row_raw(a, b, g, col, grp), col, rc);
 #pragma unroll
@@ -642,7 +809,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
     half8_t ka[PAGES][2];
     half4_t va[PAGES][4];
     const int kv_dim = a.addr.kv_dim;
-    if (wp0 < wp_end) {
+    auto load_pages = [&]() {
 #pragma unroll
         for (int i = 0; i < PAGES; ++i) {
             const int64_t base = block_base(a.addr, wp0 + i < wp_end ? page[i] : page[0]);
@@ -654,7 +821,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
             for (int db = 0; db < 4; ++db)
                 va[i][db] = *reinterpret_cast<const half4_t*>(vp + db * 16 * kPageTokens);
         }
-    }
+    };
+    if (wp0 < wp_end) load_pages();
+    // A planned unit checks its page ids while the pages load; if the table changed since
+    // the plan was made (wave-uniform), the pages load again from the table's ids.
+    if (PAGED && planned && table_changed() && wp0 < wp_end) load_pages();
     CRUCIBLE_STAMP_STORE(kStampStart, t_start);
     CRUCIBLE_STAMP_NOW(kStampPrologue);
     CRUCIBLE_STAMP_AFTER(kStampLoads);
@@ -975,7 +1146,7 @@ bool wide_combine(const DecodeArgs& a) {
 }
 
 // The decode kernel's arguments: the preloaded prologue values, then the block.
-#define DECODE_ARGS(a) (a).tables, (a).lens, (a).positions, (a).batch, (a).lens_stride, (a).lens_off, (a)
+#define DECODE_ARGS(a) (a).tables, (a).lens, (a).positions, (a).batch, (a).lens_stride, (a).lens_off, (a).plan, (a)
 
 template <bool QF32, bool APPEND, bool PAGED, bool ROPE = false>
 bool launch_shape(const DecodeArgs& a, DecodeShape sh, int order, dim3 grid,
@@ -1079,7 +1250,8 @@ int check_geometry(const char* what, int64_t n_head, int64_t n_kv_head, int64_t 
 
 // Workspace: a fixed region of kMaxCounters u32 combine counters (index b * n_kv_head + g,
 // the same place for every batch size, so calls of different batch sizes can share one
-// workspace), then partial o, m, l for every (request, query head, split).
+// workspace), then the compact order's unit plan (kPlanBytes, also at a fixed place), then
+// partial o, m, l for every (request, query head, split).
 constexpr int64_t kMaxCounters = 65536;
 constexpr size_t kCounterBytes = kMaxCounters * sizeof(uint32_t);
 
@@ -1088,12 +1260,13 @@ size_t partial_floats(int64_t batch, int64_t n_head, int64_t n_splits) {
 }
 
 size_t workspace_need(int64_t batch, int64_t n_head, int64_t n_splits) {
-    return kCounterBytes + partial_floats(batch, n_head, n_splits) * sizeof(float);
+    return kCounterBytes + kPlanBytes + partial_floats(batch, n_head, n_splits) * sizeof(float);
 }
 
 void bind_workspace(DecodeArgs& a, void* ws) {
     a.counters = static_cast<uint32_t*>(ws);
-    float* f = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
+    a.plan = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + kCounterBytes);
+    float* f = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes + kPlanBytes);
     const size_t n = (size_t)a.batch * a.n_head * a.n_splits;
     a.po = f;
     a.pm = f + n * kHeadDim;

@@ -149,7 +149,15 @@ int crucible_cache_store_packed_paged(const void* src, int src_dtype, void* pool
  * 16-byte aligned. It starts with a fixed region of 65536 u32 counters, one per
  * (request, kv head) (so batch * n_kv_head <= 65536), that order the in-kernel
  * combine of the splits: zero the workspace once when it is allocated; every
- * launch leaves the counters zeroed again. Calls of any batch size may share one
+ * launch leaves the counters zeroed again. A unit plan follows, also at a fixed
+ * place (1.5 MiB): launches of batch <= 64 in the compact grid order record there
+ * which (request, kv head, split) each workgroup served and its page ids, with
+ * the lengths, positions and launch shape they came from; a later launch on the
+ * same workspace whose lengths, positions and shape are equal loads its unit in
+ * the round trip that loads the lengths instead of searching for it. Page ids
+ * are still read from the table on every launch (beside the page loads, which
+ * are reissued if an id changed), so a rewritten table is always honoured; the
+ * plan only saves the search. Calls of any batch size may share one
  * workspace, one launch at a time (launches that share it must be ordered, e.g.
  * on one stream). Two launches that run at once on one workspace (two streams
  * without an event between them) race on the counters and partials: a split can

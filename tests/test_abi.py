@@ -83,10 +83,11 @@ def test_invalid_arguments_are_rejected_before_launch():
 
 def test_workspace_size_formula():
     lib = _lib.load()
-    # a fixed 65536-counter region (256 KiB), then the worst case of 4-page splits:
-    # ceil(ceil(2048/16)/4) = 32 splits, 66 floats per (b, h, split)
+    # a fixed 65536-counter region (256 KiB), the unit plan (2048 entries of 192 int32,
+    # 1.5 MiB), then the worst case of 4-page splits: ceil(ceil(2048/16)/4) = 32 splits,
+    # 66 floats per (b, h, split)
     assert lib.crucible_attention_decode_workspace_bytes(16, 12, 2048) == (
-        65536 * 4 + 16 * 12 * 32 * 66 * 4)
+        65536 * 4 + 2048 * 192 * 4 + 16 * 12 * 32 * 66 * 4)
     assert lib.crucible_attention_decode_workspace_bytes(0, 12, 2048) == 0
 
 

@@ -463,3 +463,86 @@ def test_qkv_entry_without_rope_equals_plain_fused_append(gpu, dev):
     torch.cuda.synchronize()
     assert torch.equal(k1, k2) and torch.equal(v1, v2)
     assert torch.equal(out1, out2)
+
+
+PLAN_OFFSET = 65536 * 4          # the unit plan follows the counters in the workspace
+PLAN_ENTRY_INTS = 192
+
+
+def test_unit_plan_reuse_equals_a_fresh_search(gpu, dev):
+    """The compact order's unit plan: a launch whose lengths, positions and geometry equal
+    the previous launch's takes its unit and page ids from the workspace instead of
+    searching. Every call here runs twice, once on a warm workspace (whose plan the earlier
+    calls left) and once on a fresh one (nothing planned): outputs and pools must agree bit
+    for bit. The sequence covers a repeated call (planned), a table rewritten under equal
+    lengths (the page-id check reloads the pages from the new ids, attended and
+    append-only units), a changed length, changed append positions, the decode-only kernel
+    on the fused kernel's plan and back, and a smaller batch."""
+    rng = np.random.default_rng(2026)
+    n_head, n_kv, n_layer, layer, stride = 12, 3, 2, 1, 128
+    batch, max_seq, kv = 16, 2048, n_kv * 64
+    n_pages = batch * stride + 64
+    kp0, vp0 = random_pools(rng, n_pages, n_layer, kv)
+    lens = rng.integers(64, max_seq, batch).astype(np.int32)
+    tables = disjoint_tables(rng, n_pages, lens + 1, stride)
+    q = _dev(rng.standard_normal((batch, n_head * 64)).astype(np.float16), dev)
+    k_new = _dev(rng.standard_normal((batch, kv)).astype(np.float32), dev)
+    v_new = _dev(rng.standard_normal((batch, kv)).astype(np.float32), dev)
+    nbytes = gpu.lib.crucible_attention_decode_workspace_bytes(batch, n_head, max_seq)
+    warm = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    pools = {"warm": (_dev(kp0, dev), _dev(vp0, dev)), "fresh": (_dev(kp0, dev), _dev(vp0, dev))}
+
+    def run(tab, ln, pos, b=batch, fused=True):
+        outs = {}
+        for name in ("warm", "fresh"):
+            ws = warm if name == "warm" else torch.zeros_like(warm)
+            k, v = pools[name]
+            out = torch.full((b, n_head * 64), SENTINEL, device=dev)
+            args = (_dev(tab[:b], dev), _dev(pos[:b], dev), _dev(ln[:b], dev))
+            if fused:
+                gpu.attention_decode_paged_append(q[:b], k_new[:b], v_new[:b], k, v, out,
+                                                  args[0], args[1], args[2], b, n_head, n_kv,
+                                                  64, stride, n_layer, layer, kv, max_seq,
+                                                  workspace=ws)
+            else:
+                gpu.attention_decode_paged(q[:b], k, v, out, args[0], args[2], b, n_head, n_kv,
+                                           64, stride, n_layer, layer, kv, max_seq, workspace=ws)
+            torch.cuda.synchronize()
+            outs[name] = out.cpu()
+        assert torch.equal(outs["warm"].view(torch.int32), outs["fresh"].view(torch.int32))
+        for (kw, vw), (kf, vf) in [(pools["warm"], pools["fresh"])]:
+            assert torch.equal(kw.view(torch.int16), kf.view(torch.int16))
+            assert torch.equal(vw.view(torch.int16), vf.view(torch.int16))
+        return outs["warm"]
+
+    ln = lens + 1
+    pos = lens.copy()
+    first = run(tables, ln, pos)
+    entry0 = warm[PLAN_OFFSET:PLAN_OFFSET + 4 * PLAN_ENTRY_INTS].view(torch.int32).cpu()
+    assert int(entry0[0]) == 1 and int(entry0[1]) == batch  # the plan was written
+    again = run(tables, ln, pos)
+    assert torch.equal(first.view(torch.int32), again.view(torch.int32))
+    # a rewritten table under equal lengths: request 3's pages move to unused pages (with
+    # other contents), including the page its row is appended to
+    used = set(int(x) for b in range(batch) for x in tables[b, :-(-int(ln[b]) // 16)])
+    free = [p for p in range(n_pages) if p not in used]
+    t2 = tables.copy()
+    n3 = -(-int(ln[3]) // 16)
+    t2[3, :n3] = free[:n3]
+    run(t2, ln, pos)
+    run(t2, ln, pos)
+    # a changed length, then changed append positions under equal lengths
+    ln2 = ln.copy()
+    ln2[5] -= 17
+    run(t2, ln2, pos)
+    pos2 = pos.copy()
+    pos2[7] = min(int(ln2[7]) + 300, stride * 16 - 1)  # past the attended keys' splits
+    t2[7, pos2[7] // 16] = free[n3]                     # its page: an unused one
+    run(t2, ln2, pos2)
+    run(t2, ln2, pos2)
+    # the decode-only kernel on the fused kernel's plan, then the fused kernel again
+    run(t2, ln2, pos2, fused=False)
+    run(t2, ln2, pos2)
+    # a smaller batch on the same workspace
+    run(t2, ln2, pos2, b=11)
+    run(t2, ln2, pos2, b=11)

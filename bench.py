@@ -58,10 +58,11 @@ def parse_args():
                         "default set)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run 5 more plain 256 MiB device copies (PMC traffic calibration)")
-    p.add_argument("--phases", action="store_true",
-                   help="diagnostic: run config 3 on the stamped twin of the library "
-                        "(libcrucible_attn_stamps.so) and print where the fused decode "
-                        "launch's time goes, per phase, instead of the bench line")
+    p.add_argument("--phases", nargs="?", const="decode", choices=("decode", "config4"),
+                   help="diagnostic: run config 3 (decode, the default) or config 4 (the "
+                        "16-row LDS prefill) on the stamped twin of the library "
+                        "(libcrucible_attn_stamps.so) and print where a launch's time goes, "
+                        "per phase, instead of the bench line")
     p.add_argument("--phase-reps", type=int, default=28,
                    help="--phases: replayed steps whose last launch is read")
 
@@ -250,12 +251,9 @@ def gather_rows(pool, table_row, n, n_layer, layer, kv_dim, v_kind):
     return blocks.reshape(n_pages * 16, kv_dim)[:n]
 
 
-def bench_prefill(gpu, dev, cfg, launches: int = 50, q_dtype=None, cpu_inputs=None):
-    """Time the segment-form prefill kernel (gpu.rs:1606-1751 path) on config 1 or 4:
-    `launches` back-to-back launches replayed from one HIP graph (us_per_launch, the
-    figure TFLOP/s uses, timed like the decode step), and eager launches each bracketed by
-    events (us_per_launch_eager). The query is fp16 (the kernel's MFMA input type) unless
-    q_dtype says otherwise."""
+def prefill_runner(gpu, dev, cfg, q_dtype=None):
+    """Device inputs of a prefill config and a closure that launches its segment-form
+    prefill once; returns (run, q, k_pool, v_pool, tables)."""
     import numpy as np
     import torch
 
@@ -279,6 +277,19 @@ def bench_prefill(gpu, dev, cfg, launches: int = 50, q_dtype=None, cpu_inputs=No
                                     len(cfg.seq_lens), max_chunk, stride, cfg.n_head,
                                     cfg.n_kv_head, 64, 1, 0, kv_dim)
 
+    return run, q, k_pool, v_pool, d_tab
+
+
+def bench_prefill(gpu, dev, cfg, launches: int = 50, q_dtype=None, cpu_inputs=None):
+    """Time the segment-form prefill kernel (gpu.rs:1606-1751 path) on config 1 or 4:
+    `launches` back-to-back launches replayed from one HIP graph (us_per_launch, the
+    figure TFLOP/s uses, timed like the decode step), and eager launches each bracketed by
+    events (us_per_launch_eager). The query is fp16 (the kernel's MFMA input type) unless
+    q_dtype says otherwise."""
+    import torch
+
+    run, q, k_pool, v_pool, d_tab = prefill_runner(gpu, dev, cfg, q_dtype)
+    kv_dim = cfg.kv_dim
     for _ in range(5):
         run()
     torch.cuda.synchronize(dev)
@@ -546,6 +557,89 @@ def summarize_stamps(launches, us_per_tick: float) -> dict:
             "phases": summary, "critical_workgroup": crit[:8]}
 
 
+PREFILL_PHASES = ("rows", "first_pair", "loop", "merge", "write")
+
+
+def prefill_phases(gpu, dev, args, log):
+    """Per-workgroup phase stamps of config 4's prefill launch (the 16-row LDS kernel on the
+    stamped library). A graph of 12 back-to-back launches is replayed; the stamps left are
+    the last launch's. Per workgroup with rows (slots of PStampSlot in attn_prefill.hip):
+    start skew, rows (entry to the tile's rows resolved), first_pair (to the first pair of
+    key tiles in LDS: page ids, tile loads and query loads), loop (the rest of the tile
+    loop), merge (key halves merged), write (output stored), and `wait`, the part of
+    first_pair + loop its wave spent waiting for key tiles. Reported over all workgroups and
+    over the heaviest (most tile pairs), whose chain bounds the launch."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from crucible_amd import _lib
+    from crucible_amd import workloads as W
+
+    fn = gpu.lib.crucible_debug_prefill_stamps
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                   ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]
+    fn.restype = ctypes.c_int
+    khz, slots = ctypes.c_int(0), ctypes.c_int(0)
+    _lib.check(fn(None, 0, 1, ctypes.byref(khz), ctypes.byref(slots)))
+    rows = 8192
+    buf = np.zeros((rows, slots.value), np.uint64)
+    cfg = W.config4_packed()
+    timing = bench_prefill(gpu, dev, cfg, launches=12)
+    log(f"stamped build: {timing['us_per_launch']} us per launch (graph replay)")
+    run = prefill_runner(gpu, dev, cfg)[0]
+    stream = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        run()
+    stream.wait_stream(side)
+    torch.cuda.synchronize(dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(12):
+            run()
+    us = 1e3 / khz.value
+    per = {k: [] for k in ("skew",) + PREFILL_PHASES + ("wait", "chain")}
+    heavy = {k: [] for k in ("skew",) + PREFILL_PHASES + ("wait",)}
+    n_wg = 0
+    for _ in range(args.phase_reps):
+        _lib.check(fn(None, 0, 1, ctypes.byref(khz), ctypes.byref(slots)))
+        g.replay()
+        torch.cuda.synchronize(dev)
+        _lib.check(fn(buf.ctypes.data, rows, 0, ctypes.byref(khz), ctypes.byref(slots)))
+        live = (buf[:, 0] != 0) & (buf[:, 5] != 0)
+        t = buf[live, :6].astype(np.int64)
+        wait = buf[live, 6].astype(np.int64)
+        pairs = (buf[live, 7] >> np.uint64(48)).astype(np.int64)
+        n_wg = int(live.sum())
+        t0 = t[:, 0].min()
+        d = np.diff(t, axis=1) * us
+        hv = pairs == pairs.max()
+        for sel, dst in ((np.ones_like(hv), per), (hv, heavy)):
+            dst["skew"] += list((t[sel, 0] - t0) * us)
+            for i, name in enumerate(PREFILL_PHASES):
+                dst[name] += list(d[sel, i])
+            dst["wait"] += list(wait[sel] * us)
+        per["chain"].append(float((t[:, 5].max() - t0) * us))
+    del g
+
+    def stats(dct):
+        out = {}
+        for k, v in dct.items():
+            a = np.asarray(v, np.float64)
+            out[k] = {"median_us": round(float(np.median(a)), 3),
+                      "p90_us": round(float(np.percentile(a, 90)), 3),
+                      "max_us": round(float(a.max()), 3), "n": int(a.size)}
+        return out
+
+    return {"kernel": "prefill_kernel<4, 1, false, 4, true>", "workload": cfg.name,
+            "clock_khz": khz.value, "stamped_us_per_launch": timing["us_per_launch"],
+            "launches_read": args.phase_reps, "workgroups_per_launch": n_wg,
+            "max_pairs": int(pairs.max()), "phases": stats(per), "heaviest": stats(heavy)}
+
+
 def launch_floor_us(dev, launches: int = 12, reps: int = 50):
     """Time per launch of a one-element fill kernel, `launches` back to back in one HIP
     graph and replayed as the decode step is: what any kernel of a captured step costs
@@ -638,7 +732,8 @@ def main():
 
     log(f"{gpu.version()} on {torch.cuda.get_device_name(0)}")
     if args.phases:
-        print(json.dumps(decode_phases(gpu, dev, args, log)), flush=True)
+        fn = decode_phases if args.phases == "decode" else prefill_phases
+        print(json.dumps(fn(gpu, dev, args, log)), flush=True)
         return
     b16 = DecodeBench(gpu, dev, batch=16, n_head=12, n_kv_head=args.kv_heads, n_layer=12,
                       n_pages=8192, max_seq=2048, rotations=7, seed=W.BASE_SEED + 2)

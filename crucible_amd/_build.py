@@ -2,9 +2,9 @@
 
 ``build_library()`` compiles every source under ``csrc/`` with hipcc for gfx950 into
 ``crucible_amd/libcrucible_attn.so`` (objects under ``crucible_amd/_build/``). It also links
-``libcrucible_attn_stamps.so``, a diagnostic twin in which the decode source is compiled with
-``-DCRUCIBLE_STAMPS`` (per-workgroup phase timestamps, read by ``bench.py --phases``); the
-product path never loads it.
+``libcrucible_attn_stamps.so``, a diagnostic twin in which the decode and prefill sources are
+compiled with ``-DCRUCIBLE_STAMPS`` (per-workgroup phase timestamps, read by
+``bench.py --phases``); the product path never loads it.
 """
 from __future__ import annotations
 
@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB_PATH = os.path.join(HERE, "libcrucible_attn.so")
 STAMPS_LIB_PATH = os.path.join(HERE, "libcrucible_attn_stamps.so")
-STAMPS_SOURCE = "attn_decode.hip"
+STAMPS_SOURCES = ("attn_decode.hip", "attn_prefill.hip")
 
 ARCH = "gfx950"
 DEVICE_SOURCES = ["kv_append.hip", "attn_decode.hip", "attn_prefill.hip", "argmax.hip",
@@ -70,14 +70,15 @@ def build_library(jobs: int = 8) -> str:
         obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
         cmds.append(_compile_cmd(hipcc, src, obj))
-    stamps_obj = os.path.join(BUILD, os.path.splitext(STAMPS_SOURCE)[0] + "_stamps.o")
-    cmds.append(_compile_cmd(hipcc, STAMPS_SOURCE, stamps_obj, ["-DCRUCIBLE_STAMPS"]))
+    stamped = {}
+    for src in STAMPS_SOURCES:
+        stem = os.path.splitext(src)[0]
+        stamped[stem + ".o"] = os.path.join(BUILD, stem + "_stamps.o")
+        cmds.append(_compile_cmd(hipcc, src, stamped[stem + ".o"], ["-DCRUCIBLE_STAMPS"]))
     with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         list(ex.map(_run, cmds))
     _link(hipcc, objs, LIB_PATH)
-    stamps_objs = [stamps_obj if os.path.basename(o) == os.path.splitext(STAMPS_SOURCE)[0] + ".o"
-                   else o for o in objs]
-    _link(hipcc, stamps_objs, STAMPS_LIB_PATH)
+    _link(hipcc, [stamped.get(os.path.basename(o), o) for o in objs], STAMPS_LIB_PATH)
     return LIB_PATH
 
 

@@ -56,6 +56,49 @@ constexpr int kWaitVm0Lgkm0 = 0x0070;
 constexpr int kWaitVm4Lgkm0 = 0x0074;
 constexpr int kWaitVm8Lgkm0 = 0x0078;
 constexpr int kThreads = 512;  // 8 waves: 4 row/head slots x 2 tile parities
+
+#ifdef CRUCIBLE_STAMPS
+// Phase stamps of the 16-row LDS kernel (prefill_kernel), compiled only into the
+// diagnostic libcrucible_attn_stamps.so. Thread 0 of each workgroup (wave 0: key half 0 of
+// the first slot) records s_memrealtime at the end of each phase in row `workgroup id`,
+// and the time its wave spent in the tile loop's waits for key tiles (the wait for its own
+// tile loads plus the barrier that makes every wave's loads visible).
+constexpr int kPStampRows = 8192;
+enum PStampSlot {
+    kPStart,      // kernel entry
+    kPRows,       // rows of the tile resolved (after the first barrier)
+    kPFirst,      // first pair of key tiles in LDS (after the loop's first barrier)
+    kPLoop,       // tile loop done
+    kPMerged,     // key halves merged
+    kPWritten,    // output stored (acknowledged)
+    kPWait,       // ticks waited for key tiles inside the loop
+    kPMeta,       // grid tile | request << 16 | x << 32 | pairs << 48
+    kPSlots
+};
+__device__ uint64_t g_prefill_stamps[kPStampRows][kPSlots];
+
+__device__ __forceinline__ unsigned pstamp_row() {
+    return blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+}
+__device__ __forceinline__ void pstamp_store(int slot, uint64_t v) {
+    if (threadIdx.x == 0 && pstamp_row() < kPStampRows) g_prefill_stamps[pstamp_row()][slot] = v;
+}
+__device__ __forceinline__ uint64_t pstamp_clock() {
+    asm volatile("" ::: "memory");
+    return __builtin_amdgcn_s_memrealtime();
+}
+#define CRUCIBLE_PSTAMP_CLOCK() pstamp_clock()
+#define CRUCIBLE_PSTAMP(slot, v) pstamp_store(slot, v)
+#define CRUCIBLE_PSTAMP_AFTER(slot)                                  \
+    do {                                                             \
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); \
+        pstamp_store(slot, pstamp_clock());                          \
+    } while (0)
+#else
+#define CRUCIBLE_PSTAMP_CLOCK() uint64_t(0)
+#define CRUCIBLE_PSTAMP(slot, v) ((void)0)
+#define CRUCIBLE_PSTAMP_AFTER(slot) ((void)0)
+#endif
 constexpr float kLazyLog2 = 8.0f;  // running-max slack (log2 units) before a rescale
 
 // Hand-written instructions and the hazards the compiler cannot see. The compiler inserts
@@ -296,6 +339,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
     constexpr int RS = 4 / HPW;          // row slices per workgroup
     constexpr int WROWS = 16 * QB;       // rows per wave
     constexpr int R = RS * WROWS;        // rows per workgroup
+    [[maybe_unused]] const uint64_t t_entry = CRUCIBLE_PSTAMP_CLOCK();
+    [[maybe_unused]] uint64_t t_wait = 0;
 
     // ring of key tiles, 128-byte rows whose 16-byte chunks are XOR-swizzled by row
     __shared__ half_t s_k[KB][kKeyTile][64];   // [buf][key][dim]
@@ -338,6 +383,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
     const uint64_t mask0 = s_mask[0];
     const uint64_t mask1 = R > 64 ? s_mask[1] : 0;
     if (mask0 == 0 && mask1 == 0) return;  // uniform: no row of this tile is valid
+    CRUCIBLE_PSTAMP(kPStart, t_entry);
+    CRUCIBLE_PSTAMP(kPRows, CRUCIBLE_PSTAMP_CLOCK());
 
     // ---- per-lane query state for each 16-row block (the query rows load after the first
     // run's leading tiles are issued, below, so the two round trips overlap)
@@ -395,6 +442,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
     // 32 (w & 1) .. +31 of that page (below), so each wave needs one page id per tile.
     const int my_page = wave >> 1;
     bool first_run = true;
+#ifdef CRUCIBLE_STAMPS
+    bool first_pair_stamp = true;
+    int stamp_pairs = 0;
+#endif
     int r0 = a.mode == kOwners ? 0 : first_valid;
     while (r0 < R) {
         int r1, owner, hist_end, wave_last;
@@ -479,6 +530,9 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
         // a slot runs half of the tiles and the two halves' softmax chains overlap.
         constexpr int PS = KB / 2;  // pair slots in the ring
         const int n_pairs = (n_tiles + 1) / 2;
+#ifdef CRUCIBLE_STAMPS
+        stamp_pairs += n_pairs;
+#endif
         // the pair holding the run's last tile when that tile is partial, else none
         const int tail_pair = (hist_end % kKeyTile) ? (n_tiles - 1) / 2 : -1;
 #pragma unroll
@@ -500,6 +554,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
             // loads each) and its LDS reads of pair ip - 1; the barrier then makes every
             // wave's loads visible and frees pair ip - 1's buffers for pair ip + PS - 1.
             const int ahead = min(PS - 2, n_pairs - 1 - ip);
+            [[maybe_unused]] const uint64_t t_w0 = CRUCIBLE_PSTAMP_CLOCK();
             if (ahead >= 2) __builtin_amdgcn_s_waitcnt(kWaitVm8Lgkm0);
             else if (ahead == 1) __builtin_amdgcn_s_waitcnt(kWaitVm4Lgkm0);
             else __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
@@ -523,6 +578,16 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             }
             __builtin_amdgcn_s_barrier();
+#ifdef CRUCIBLE_STAMPS
+            {
+                const uint64_t t_w1 = CRUCIBLE_PSTAMP_CLOCK();
+                t_wait += t_w1 - t_w0;
+                if (first_pair_stamp) {
+                    CRUCIBLE_PSTAMP(kPFirst, t_w1);
+                    first_pair_stamp = false;
+                }
+            }
+#endif
             if (ip + PS - 1 < n_pairs) {
                 const int tn = 2 * (ip + PS - 1);
                 const int64_t pa = page_of(tn), pb = page_of(tn + 1);
@@ -616,6 +681,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
         r0 = r1;
     }
 
+    CRUCIBLE_PSTAMP(kPLoop, CRUCIBLE_PSTAMP_CLOCK());
     // ---- merge the key halves: waves 4..7 hand (m, l, acc) to their partner through
     // the (now idle) ring; per lane, both hold the same query column and dims. Lane-major
     // layout keeps the exchange free of bank conflicts: acc (4 x QB x 16 x 64 floats,
@@ -638,6 +704,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
     }
     __syncthreads();
     if (kh == 1) return;
+    CRUCIBLE_PSTAMP(kPMerged, CRUCIBLE_PSTAMP_CLOCK());
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         const float* p = s_macc + (slot * QB + qb) * 16 * 64 + lane;
@@ -672,6 +739,13 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
             }
         }
     }
+#ifdef CRUCIBLE_STAMPS
+    CRUCIBLE_PSTAMP_AFTER(kPWritten);
+    CRUCIBLE_PSTAMP(kPWait, t_wait);
+    CRUCIBLE_PSTAMP(kPMeta, (uint64_t)(wp.tile & 0xffff) | (uint64_t)(wp.req & 0xffff) << 16 |
+                                (uint64_t)(wp.x & 0xffff) << 32 |
+                                (uint64_t)(stamp_pairs & 0xffff) << 48);
+#endif
 }
 
 // ---------------------------------------------------------------- 32-row waves on 32x32 MFMAs
@@ -1752,3 +1826,32 @@ extern "C" int crucible_attention_prefill(const void* q, int q_dtype, const void
                                       what);
     return launch_prefill(a, rows, 1, q_dtype == CRUCIBLE_F32, stream, what);
 }
+
+#ifdef CRUCIBLE_STAMPS
+// Diagnostic build only: copy the first `rows` rows of the 16-row prefill kernel's phase
+// stamps (*slots u64 each, in PStampSlot order) to `host`, then zero them on the device if
+// `clear`. The clock's rate in kHz goes to *clock_khz. Synchronous.
+extern "C" int crucible_debug_prefill_stamps(uint64_t* host, int64_t rows, int clear,
+                                             int* clock_khz, int* slots) {
+    using namespace crucible;
+    const char* what = "crucible_debug_prefill_stamps";
+    CRUCIBLE_CHECK(rows >= 0 && rows <= kPStampRows && (rows == 0 || host) && clock_khz && slots,
+                   CRUCIBLE_ERR_INVALID, "%s: %lld rows (at most %d)", what, (long long)rows,
+                   kPStampRows);
+    *slots = kPSlots;
+    int dev = 0;
+    void* p = nullptr;
+    const size_t bytes = (size_t)rows * kPSlots * sizeof(uint64_t);
+    const bool ok =
+        hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(clock_khz, hipDeviceAttributeWallClockRate, dev) == hipSuccess &&
+        hipDeviceSynchronize() == hipSuccess &&
+        (rows == 0 || hipMemcpyFromSymbol(host, HIP_SYMBOL(g_prefill_stamps), bytes, 0,
+                                          hipMemcpyDeviceToHost) == hipSuccess) &&
+        (!clear || (hipGetSymbolAddress(&p, HIP_SYMBOL(g_prefill_stamps)) == hipSuccess &&
+                    hipMemset(p, 0, sizeof(g_prefill_stamps)) == hipSuccess &&
+                    hipDeviceSynchronize() == hipSuccess));
+    CRUCIBLE_CHECK(ok, CRUCIBLE_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(hipGetLastError()));
+    return CRUCIBLE_OK;
+}
+#endif

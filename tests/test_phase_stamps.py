@@ -1,9 +1,9 @@
 """The stamped diagnostic twin of the library and bench.py's phase summary (CPU only).
 
-libcrucible_attn_stamps.so is the product library with the decode source compiled with
--DCRUCIBLE_STAMPS: it must export everything the header declares plus the stamp reader,
-and the product library must not export the reader. summarize_stamps turns stamp rows into
-phase durations; here it runs on rows built by hand with known phase lengths.
+libcrucible_attn_stamps.so is the product library with the decode and prefill sources
+compiled with -DCRUCIBLE_STAMPS: it must export everything the header declares plus the
+stamp readers, and the product library must not export them. summarize_stamps turns stamp
+rows into phase durations; here it runs on rows built by hand with known phase lengths.
 """
 import ctypes
 import os
@@ -24,8 +24,9 @@ def test_stamped_twin_exports_the_header_and_the_reader():
     twin = ctypes.CDLL(_build.STAMPS_LIB_PATH)
     for name in _lib.SIGNATURES:
         assert hasattr(twin, name), f"stamped library does not export {name}"
-    assert hasattr(twin, "crucible_debug_decode_stamps")
-    assert not hasattr(_lib.load(), "crucible_debug_decode_stamps")
+    for reader in ("crucible_debug_decode_stamps", "crucible_debug_prefill_stamps"):
+        assert hasattr(twin, reader)
+        assert not hasattr(_lib.load(), reader)
 
 
 def _row(t0, phases, b, g, s, n_active, last):

@@ -672,10 +672,10 @@ def launch_floor_us(dev, launches: int = 12, reps: int = 50):
     return us
 
 
-# What the decode kernel is built from: its translation unit, the headers it includes and
-# the build script that holds its compiler flags.
+# What the decode kernel is built from: its translation unit and the headers it includes,
+# plus the compiler flags the build gives that unit (not the rest of the build script).
 DECODE_SOURCES = ("crucible_amd/csrc/attn_decode.hip", "crucible_amd/csrc/common.hpp",
-                  "include/crucible_attn.h", "crucible_amd/_build.py")
+                  "crucible_amd/csrc/generic_attend.hpp", "include/crucible_attn.h")
 
 
 def source_sha() -> str:
@@ -683,10 +683,14 @@ def source_sha() -> str:
     kernel built from exactly these."""
     import hashlib
 
+    from crucible_amd import _build
+
     h = hashlib.sha256()
     for name in DECODE_SOURCES:
         with open(os.path.join(ROOT, name), "rb") as f:
             h.update(name.encode() + b"\0" + f.read())
+    flags = [_build.ARCH, *_build.HIPCC_FLAGS, *_build.EXTRA_FLAGS.get("attn_decode.hip", [])]
+    h.update(b"flags\0" + "\0".join(flags).encode())
     return h.hexdigest()[:16]
 
 

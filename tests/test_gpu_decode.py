@@ -546,3 +546,49 @@ def test_unit_plan_reuse_equals_a_fresh_search(gpu, dev):
     # a smaller batch on the same workspace
     run(t2, ln2, pos2, b=11)
     run(t2, ln2, pos2, b=11)
+
+
+def test_unit_plan_with_the_qkv_rope_entry(gpu, dev):
+    """The unit plan under the fused q/k/v entry (RoPE of q and k, both appends, decode; the
+    compact order at config 3's shape): calls on a warm workspace (the plan of the previous
+    call, then of the fused entry without RoPE, whose plan it shares) equal calls on a
+    zeroed one, bit for bit."""
+    from crucible_amd.gpu_model import rope_tables
+
+    rng = np.random.default_rng(2027)
+    n_head, n_kv, n_layer, layer, stride = 12, 3, 2, 0, 128
+    batch, max_seq, kv = 16, 2048, n_kv * 64
+    n_pages = batch * stride + 16
+    kp0, vp0 = random_pools(rng, n_pages, n_layer, kv)
+    lens = rng.integers(64, max_seq, batch).astype(np.int32)
+    tables = disjoint_tables(rng, n_pages, lens, stride)
+    width = (n_head + 2 * n_kv) * 64
+    qkv = _dev(rng.standard_normal((batch, width)).astype(np.float32), dev)
+    cos, sin = rope_tables(64, max_seq, 10000.0)
+    d_cos, d_sin = _dev(cos, dev), _dev(sin, dev)
+    d_tab, d_len, d_pos = _dev(tables, dev), _dev(lens, dev), _dev(lens - 1, dev)
+    nbytes = gpu.lib.crucible_attention_decode_workspace_bytes(batch, n_head, max_seq)
+    warm = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    pools = {"warm": (_dev(kp0, dev), _dev(vp0, dev)), "fresh": (_dev(kp0, dev), _dev(vp0, dev))}
+
+    def run(rope=True):
+        outs = {}
+        for name in ("warm", "fresh"):
+            ws = warm if name == "warm" else torch.zeros_like(warm)
+            k, v = pools[name]
+            out = torch.full((batch, n_head * 64), SENTINEL, device=dev)
+            gpu.attention_decode_qkv_paged_append(qkv, d_cos if rope else None,
+                                                  d_sin if rope else None, k, v, out, d_tab,
+                                                  d_pos, d_len, batch, n_head, n_kv, 64, stride,
+                                                  n_layer, layer, kv, max_seq, workspace=ws)
+            torch.cuda.synchronize()
+            outs[name] = out.cpu()
+        assert torch.equal(outs["warm"].view(torch.int32), outs["fresh"].view(torch.int32))
+        (kw, vw), (kf, vf) = pools["warm"], pools["fresh"]
+        assert torch.equal(kw.view(torch.int16), kf.view(torch.int16))
+        assert torch.equal(vw.view(torch.int16), vf.view(torch.int16))
+
+    run()
+    run()
+    run(rope=False)
+    run()

@@ -72,7 +72,8 @@ struct DecodeArgs {
     float* po;                   // [batch][n_head][n_splits][64]
     float* pm;                   // [batch][n_head][n_splits]
     float* pl;                   // [batch][n_head][n_splits]
-    uint32_t* counters;          // [batch * n_kv_head]; nullptr: combine in a second kernel
+    uint32_t* counters;          // [batch * n_kv_head] x counter_stride; nullptr: combine in a second kernel
+    int counter_stride;          // u32 between two units' counters (kCounterPad where they fit)
     int32_t* plan;               // compact order's unit plan (kPlanUnits entries); nullptr: none
     PoolAddr addr;
     uint32_t po_bytes;           // size of po (buffer-resource bound)
@@ -1011,11 +1012,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
 
     __syncthreads();
     if (t == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&a.counters[bg], 1u, __ATOMIC_RELAXED,
+        const uint32_t prev = __hip_atomic_fetch_add(&a.counters[bg * a.counter_stride], 1u,
+                                                     __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
         const int last = prev == (uint32_t)(n_active - 1);
         if (last)  // ready for the next launch
-            __hip_atomic_store(&a.counters[bg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&a.counters[bg * a.counter_stride], 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         s_last = last;
         CRUCIBLE_STAMP_AFTER(kStampCounted);
         CRUCIBLE_STAMP_META(b, g, s, n_active, last, 0);
@@ -1254,6 +1257,16 @@ int check_geometry(const char* what, int64_t n_head, int64_t n_kv_head, int64_t 
 // partial o, m, l for every (request, query head, split).
 constexpr int64_t kMaxCounters = 65536;
 constexpr size_t kCounterBytes = kMaxCounters * sizeof(uint32_t);
+// Every split of a launch increments its unit's counter with an agent-scope atomic, and
+// atomics to one 64-byte line queue behind each other: 16 units' counters packed in a line
+// cost config 3 about 0.35 us a launch. Where the region holds them at one per line, each
+// unit's counter gets a line of its own; every launch leaves its counters zero, so calls on
+// one workspace may space them differently.
+constexpr int kCounterPad = 16;  // u32 per 64-byte line
+
+int counter_stride(int64_t units, int64_t capacity) {
+    return units * kCounterPad <= capacity ? kCounterPad : 1;
+}
 
 size_t partial_floats(int64_t batch, int64_t n_head, int64_t n_splits) {
     return (size_t)batch * n_head * n_splits * (kHeadDim + 2);
@@ -1265,6 +1278,7 @@ size_t workspace_need(int64_t batch, int64_t n_head, int64_t n_splits) {
 
 void bind_workspace(DecodeArgs& a, void* ws) {
     a.counters = static_cast<uint32_t*>(ws);
+    a.counter_stride = counter_stride((int64_t)a.batch * a.n_kv_head, kMaxCounters);
     a.plan = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + kCounterBytes);
     float* f = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes + kPlanBytes);
     const size_t n = (size_t)a.batch * a.n_head * a.n_splits;
@@ -1574,6 +1588,7 @@ extern "C" int crucible_attention_decode_paged_append_noalloc(
         void* ptr = scratch_ptr(stream, what);
         if (!ptr) return CRUCIBLE_ERR_LAUNCH;
         a.counters = static_cast<uint32_t*>(ptr);
+        a.counter_stride = counter_stride((int64_t)a.batch * a.n_kv_head, kScratchCounters);
         float* f = reinterpret_cast<float*>(static_cast<char*>(ptr) + kScratchCounterBytes);
         const size_t n = (size_t)a.batch * a.n_head * a.n_splits;
         a.po = f;

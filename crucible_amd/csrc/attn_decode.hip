@@ -492,9 +492,14 @@ __device__ __forceinline__ bool compact_find(const DecodeArgs& a, int lane, Comp
 // read and written only by workgroup i of a launch (read before it is written), and a
 // launch sees the previous launch's entries (ordered on the stream); the entry is read
 // through the scalar cache, which is never asked for it again in the same launch.
-// Layout (int32): [0] id + 1 (0: never written), [1..9] geometry, [10] kind (0: past the
-// last unit, 1: a unit), [11..15] request, kv head, split, length, position; [32..63] page
-// ids, PAGES per wave; [64..127] raw lengths; [128..191] positions (batch <= 64).
+// The recorded page ids are loaded from before they are checked, so an entry is taken only
+// for the same table (its address is part of the geometry): the ids were read from it, and
+// a table holds page ids of the pools it is used with. (A table used with a pool that has
+// fewer pages than the pool its ids were recorded for breaks that; the header says so.)
+// Layout (int32): [0] id + 1 (0: never written), [1..7] geometry, [8] kind << 31 | split
+// << 7 | request (kind 0: past the last unit, 1: a unit), [9..11] kv head, length,
+// position; [32..63] page ids, PAGES per wave; [64..127] raw lengths; [128..191] positions
+// (batch <= 64). The unit and geometry fit in the entry's first 64 bytes, one scalar line.
 constexpr int kPlanUnits = 2048;
 constexpr int kPlanEntryInts = 192;
 constexpr int kPlanIds = 32;
@@ -503,22 +508,32 @@ constexpr int kPlanPos = 128;
 constexpr size_t kPlanBytes = (size_t)kPlanUnits * kPlanEntryInts * sizeof(int32_t);
 constexpr int kPlanMaxBatch = 64;
 
-constexpr int kPlanGeo = 9;
-constexpr int kPlanHead = 16;  // [0] id + 1, [1..9] geometry, [10] kind, [11..15] b g s len pos
+constexpr int kPlanGeo = 7;
+constexpr int kPlanKind = 1 + kPlanGeo;
+constexpr int kPlanHead = 16;  // [0] id + 1, [1..7] geometry, [8] kind|s|b, [9..11] g len pos
 
 // What a plan entry's unit depends on besides the lengths and positions: the launch shape
-// (the kernel's append flag and pages and waves per split included).
+// (the kernel's append flag and pages and waves per split included), and the table's
+// address, so that the recorded page ids were read from this table.
 template <int PAGES, int WAVES, bool APPEND>
 __device__ __forceinline__ void plan_geometry(const DecodeArgs& a, int (&g)[kPlanGeo]) {
-    g[0] = a.batch;
+    // packed exactly where the fields fit (plan_fits checks the ranges)
+    g[0] = a.batch | a.split_shift << 7 | a.lens_stride << 12 | a.lens_off << 13 |
+           ((APPEND ? 1 : 0) | PAGES << 1 | WAVES << 4) << 21;
     g[1] = a.n_kv_head;
-    g[2] = a.split_shift;
-    g[3] = a.max_pages;
-    g[4] = a.max_seq;
-    g[5] = a.lens_stride;
-    g[6] = a.lens_off;
-    g[7] = a.table_stride;
-    g[8] = (APPEND ? 1 : 0) | PAGES << 1 | WAVES << 8;
+    g[2] = a.max_pages;
+    g[3] = a.max_seq;
+    g[4] = a.table_stride;
+    const uint64_t t = (uintptr_t)a.tables;  // a preloaded argument: no wait for the block
+    g[5] = (int)(uint32_t)t;
+    g[6] = (int)(uint32_t)(t >> 32);
+}
+
+// Whether plan_geometry packs this launch exactly: batch <= 64, split_shift < 32, lens
+// stride 0 or 1, lens offset < 256.
+__device__ __forceinline__ bool plan_fits(const DecodeArgs& a) {
+    return a.batch <= kPlanMaxBatch && a.split_shift < 32 && (a.lens_stride & ~1) == 0 &&
+           a.lens_off >= 0 && a.lens_off < 256;
 }
 
 // ORDER: how workgroup ids map to (split, kv head, request): kOrderSplit, grid (split,
@@ -572,6 +587,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
         if (a.batch <= kPlanMaxBatch) {
             int lv[1], pv[1];
             compact_load<1, APPEND>(a, lane, lv, pv);
+            // only preloaded values here: the entry's loads must not wait for the argument
+            // block (plan_fits reads it, at the check below)
             const bool use_plan = PAGED && a.plan != nullptr && blockIdx.x < kPlanUnits;
             int eh[kPlanHead] = {};
             int epid[PAGES] = {};
@@ -588,18 +605,18 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
             }
             int geo[kPlanGeo];
             plan_geometry<PAGES, WAVES, APPEND>(a, geo);
-            bool ok = use_plan && eh[0] == (int)blockIdx.x + 1;
+            bool ok = use_plan && eh[0] == (int)blockIdx.x + 1 && plan_fits(a);
 #pragma unroll
             for (int j = 0; j < kPlanGeo; ++j) ok = ok && eh[1 + j] == geo[j];
             const bool lane_same = lane >= a.batch || (snap_l == lv[0] && snap_p == pv[0]);
             planned = ok && __ballot(!lane_same) == 0;
             if (planned) {
-                found = eh[10] != 0;
-                b = eh[11];
-                g = eh[12];
-                s = eh[13];
-                len = eh[14];
-                if constexpr (APPEND) pos = eh[15];
+                found = eh[kPlanKind] < 0;  // the kind bit is the sign bit
+                b = eh[kPlanKind] & 127;
+                s = (eh[kPlanKind] >> 7) & 0xffffff;
+                g = eh[kPlanKind + 1];
+                len = eh[kPlanKind + 2];
+                if constexpr (APPEND) pos = eh[kPlanKind + 3];
 #pragma unroll
                 for (int i = 0; i < PAGES; ++i) pid[i] = epid[i];
             } else {
@@ -631,13 +648,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
 #pragma unroll
                         for (int j = 0; j < kPlanGeo; ++j)
                             if (lane == 1 + j) v = geo[j];
-                        if (lane == 10) v = found ? 1 : 0;
+                        if (lane == kPlanKind)
+                            v = found ? (int)(0x80000000u | (uint32_t)s << 7 | (uint32_t)b) : 0;
                         if (found) {
-                            if (lane == 11) v = b;
-                            if (lane == 12) v = g;
-                            if (lane == 13) v = s;
-                            if (lane == 14) v = len;
-                            if (lane == 15) v = pos;
+                            if (lane == kPlanKind + 1) v = g;
+                            if (lane == kPlanKind + 2) v = len;
+                            if (lane == kPlanKind + 3) v = pos;
                         }
                         if (lane < kPlanHead) e[lane] = v;
                         if (lane < a.batch) {

@@ -158,7 +158,10 @@ int crucible_cache_store_packed_paged(const void* src, int src_dtype, void* pool
  * the round trip that loads the lengths instead of searching for it. Page ids
  * are still read from the table on every launch (beside the page loads, which
  * are reissued if an id changed), so a rewritten table is always honoured; the
- * plan only saves the search. Calls of any batch size may share one
+ * plan only saves the search. An entry is used only for the same table address.
+ * Its page ids are loaded from before they are checked, so a workspace whose plan
+ * was made with one table and pool must be zeroed again (or another workspace
+ * used) before that table serves a pool with fewer pages. Calls of any batch size may share one
  * workspace, one launch at a time (launches that share it must be ordered, e.g.
  * on one stream). Two launches that run at once on one workspace (two streams
  * without an event between them) race on the counters and partials: a split can

@@ -519,7 +519,7 @@ def test_unit_plan_reuse_equals_a_fresh_search(gpu, dev):
     pos = lens.copy()
     first = run(tables, ln, pos)
     entry0 = warm[PLAN_OFFSET:PLAN_OFFSET + 4 * PLAN_ENTRY_INTS].view(torch.int32).cpu()
-    assert int(entry0[0]) == 1 and int(entry0[1]) == batch  # the plan was written
+    assert int(entry0[0]) == 1 and int(entry0[1]) & 127 == batch  # the plan was written
     again = run(tables, ln, pos)
     assert torch.equal(first.view(torch.int32), again.view(torch.int32))
     # a rewritten table under equal lengths: request 3's pages move to unused pages (with
@@ -592,3 +592,46 @@ def test_unit_plan_with_the_qkv_rope_entry(gpu, dev):
     run()
     run(rope=False)
     run()
+
+
+def test_unit_plan_is_not_taken_for_other_pools(gpu, dev):
+    """A plan entry records the table address it was made for: a call with equal lengths
+    and shape on other pools and another table rebuilds it (its entries then hold the new
+    address) and equals a call on a zeroed workspace, bit for bit. Both pools have the same
+    number of pages, so no page id of either table lies outside the other pool."""
+    rng = np.random.default_rng(2028)
+    n_head, n_kv, n_layer, layer, stride = 12, 3, 1, 0, 128
+    batch, max_seq, kv = 16, 2048, n_kv * 64
+    n_pages = batch * stride
+    lens = rng.integers(64, max_seq, batch).astype(np.int32)
+    q = _dev(rng.standard_normal((batch, n_head * 64)).astype(np.float16), dev)
+    k_new = _dev(rng.standard_normal((batch, kv)).astype(np.float32), dev)
+    v_new = _dev(rng.standard_normal((batch, kv)).astype(np.float32), dev)
+    d_len, d_pos = _dev(lens, dev), _dev(lens - 1, dev)
+    nbytes = gpu.lib.crucible_attention_decode_workspace_bytes(batch, n_head, max_seq)
+    warm = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+
+    def call(ws, k, v, tab):
+        out = torch.full((batch, n_head * 64), SENTINEL, device=dev)
+        gpu.attention_decode_paged_append(q, k_new, v_new, k, v, out, tab, d_pos, d_len, batch,
+                                          n_head, n_kv, 64, stride, n_layer, layer, kv, max_seq,
+                                          workspace=ws)
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    pools = []
+    for _ in range(2):
+        kp, vp = random_pools(rng, n_pages, n_layer, kv)
+        pools.append((_dev(kp, dev), _dev(vp, dev), _dev(disjoint_tables(rng, n_pages, lens, stride), dev)))
+    ka, va, ta = pools[0]
+    kb, vb, tb = pools[1]
+    call(warm, ka, va, ta)
+    kb2, vb2 = kb.clone(), vb.clone()
+    got = call(warm, kb, vb, tb)
+    want = call(torch.zeros_like(warm), kb2, vb2, tb)
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+    assert torch.equal(kb.view(torch.int16), kb2.view(torch.int16))
+    # the entry's words 6 and 7: the table address it was made for
+    e = warm[PLAN_OFFSET:PLAN_OFFSET + 4 * PLAN_ENTRY_INTS].view(torch.int32).cpu().numpy()
+    w = [int(x) & 0xFFFFFFFF for x in e[6:8]]
+    assert w[0] | w[1] << 32 == tb.data_ptr()

@@ -41,6 +41,63 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
 METRIC = "paged-attn decode HBM GB/s (% peak); prefill attn TFLOP/s; 120M tok/s at b16"
 
 
+MFMA_PEAK_CLOCK_MHZ = 2400.0  # the clock the published dense MFMA peak assumes
+
+_SMI = {}
+
+
+def power_envelope() -> dict:
+    """The power and clock envelope of GPU 0 at this moment, from amdsmi: enforced power cap
+    and maximum gfx clock (what the reference records with every benchmark, nvidia-smi's
+    enforced.power.limit and clocks.max.sm; engine/src/gpu.rs:2159-2186, main.rs:1285-1305),
+    plus the current and recently averaged gfx clock, socket power and hotspot temperature.
+    Fields that the driver does not report are left out; an unavailable amdsmi gives
+    {"error": ...}. Powers in W, clocks in MHz, temperatures in C."""
+    try:
+        import amdsmi
+        if "h" not in _SMI:
+            amdsmi.amdsmi_init()
+            _SMI["h"] = amdsmi.amdsmi_get_processor_handles()[0]
+        h = _SMI["h"]
+    except Exception as e:  # noqa: BLE001 - the envelope is a report, never a failure
+        return {"error": f"amdsmi unavailable: {e}"[:200]}
+    out = {}
+
+    def num(v):
+        return v if isinstance(v, (int, float)) and v not in (0xFFFF, 0xFFFFFFFF) else None
+
+    try:
+        clk = amdsmi.amdsmi_get_clock_info(h, amdsmi.AmdSmiClkType.GFX)
+        out["gfx_clk_mhz"] = num(clk.get("clk"))
+        out["gfx_clk_max_mhz"] = num(clk.get("max_clk"))
+    except Exception as e:  # noqa: BLE001
+        out["clock_error"] = str(e)[:120]
+    try:
+        m = amdsmi.amdsmi_get_gpu_metrics_info(h)
+        out["gfx_clk_avg_mhz"] = num(m.get("average_gfxclk_frequency"))
+        out["socket_power_w"] = num(m.get("current_socket_power")) or num(
+            m.get("average_socket_power"))
+        out["hotspot_c"] = num(m.get("temperature_hotspot"))
+    except Exception as e:  # noqa: BLE001
+        out["metrics_error"] = str(e)[:120]
+    try:
+        cap = amdsmi.amdsmi_get_power_cap_info(h)
+        pc = num(cap.get("power_cap"))
+        out["power_cap_w"] = round(pc / 1e6, 1) if pc and pc > 1e5 else pc  # reported in uW
+    except Exception as e:  # noqa: BLE001
+        out["power_cap_error"] = str(e)[:120]
+    return {k: v for k, v in out.items() if v is not None}
+
+
+def clock_scaled_fraction(tflops: float, env: dict):
+    """The MFMA fraction against the peak at the clock the envelope read (the published
+    2.5 PFLOP/s assumes 2.4 GHz), or None without a clock reading."""
+    mhz = env.get("gfx_clk_avg_mhz") or env.get("gfx_clk_mhz")
+    if not mhz:
+        return None
+    return round(tflops / (MFMA_F16_PEAK_TFLOPS * mhz / MFMA_PEAK_CLOCK_MHZ), 5)
+
+
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -326,6 +383,7 @@ def bench_prefill(gpu, dev, cfg, launches: int = 50, q_dtype=None, cpu_inputs=No
     avg = e0.elapsed_time(e1) / (4 * launches)
     del g
     tflops = cfg.flops() / (avg * 1e-3) / 1e12
+    env = power_envelope()  # right after the timed replays
     if cpu_inputs is not None:  # the rows this run used, for the CPU baseline beside it
         ks, vs = [], []
         for i, n in enumerate(cfg.seq_lens):
@@ -334,14 +392,16 @@ def bench_prefill(gpu, dev, cfg, launches: int = 50, q_dtype=None, cpu_inputs=No
         cpu_inputs.update(q=q.float().cpu().numpy(), k=torch.cat(ks).float().cpu().numpy(),
                           v=torch.cat(vs).float().cpu().numpy())
     from crucible_amd import _lib
-    p16 = _lib.load().crucible_attn_get_tuning(_lib.TUNE_KEYS["prefill_p16"]) != 0
+    p16 = _lib.load().crucible_attn_get_tuning(_lib.TUNE_KEYS["prefill_p16"]) == 1
     return {"workload": cfg.name, "n_head": cfg.n_head, "n_kv_head": cfg.n_kv_head,
             "q_dtype": str(q.dtype).replace("torch.", ""),
             "p_operand": "one fp16 (RNE)" if p16 else "fp16 hi + lo",
             "seq_lens": [int(x) for x in cfg.seq_lens], "flops": cfg.flops(),
             "us_per_launch": round(avg * 1e3, 3),
             "us_per_launch_eager": round(eager * 1e3, 3), "us_median_eager": round(ms[len(ms) // 2] * 1e3, 3),
-            "tflops": round(tflops, 3), "frac_of_mfma_f16_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 5)}
+            "tflops": round(tflops, 3), "frac_of_mfma_f16_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 5),
+            "gfx_clk_mhz": env.get("gfx_clk_avg_mhz") or env.get("gfx_clk_mhz"),
+            "frac_of_mfma_f16_peak_at_clock": clock_scaled_fraction(tflops, env)}
 
 
 # ---------------------------------------------------------------- end to end (config 5)
@@ -735,6 +795,8 @@ def main():
         print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
     log(f"{gpu.version()} on {torch.cuda.get_device_name(0)}")
+    envelope_start = power_envelope()
+    log(f"power envelope: {envelope_start}")
     if args.phases:
         fn = decode_phases if args.phases == "decode" else prefill_phases
         print(json.dumps(fn(gpu, dev, args, log)), flush=True)
@@ -748,6 +810,7 @@ def main():
     # headline: the whole step (12 fused append + decode launches), timed steps
     ms_per_step, ev_ms_per_step, step_bytes = b16.time_steps(step_graphs, args.steps,
                                                              args.warmup)
+    envelope_headline = power_envelope()  # right after the timed steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"timed {args.steps} steps: {ms_per_step:.4f} ms/step (events {ev_ms_per_step:.4f}), "
         f"{value:.1f} GB/s")
@@ -845,7 +908,8 @@ def main():
                                     ("packed8x2048_16h4kv", [2048] * 8, 16, 4)):
             r = bench_prefill(gpu, dev, W.prefill_sequences(name, lens, nh, nkv), launches=10)
             pscale[name] = {k: r[k] for k in ("us_per_launch", "tflops", "frac_of_mfma_f16_peak",
-                                              "p_operand")}
+                                              "p_operand", "gfx_clk_mhz",
+                                              "frac_of_mfma_f16_peak_at_clock")}
             torch.cuda.empty_cache()
         extras["prefill_scale"] = pscale
     if "prefill" in groups:
@@ -898,6 +962,8 @@ def main():
                    "n_layer": 12, "page_tokens": 16, "pool_pages": 8192,
                    "rotations": b16.rotations, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
         "roofline": roofline,
+        "envelope": {"start": envelope_start, "after_headline": envelope_headline,
+                     "end": power_envelope()},
         "cpu_baseline": cpu,
         "extras": extras,
     }

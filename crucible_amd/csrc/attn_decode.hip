@@ -41,6 +41,7 @@
 #include "common.hpp"
 #include "generic_attend.hpp"
 
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -493,11 +494,12 @@ __device__ __forceinline__ bool compact_find(const DecodeArgs& a, int lane, Comp
 // launch sees the previous launch's entries (ordered on the stream); the entry is read
 // through the scalar cache, which is never asked for it again in the same launch.
 // The recorded page ids are loaded from before they are checked, so an entry is taken only
-// for the same table (its address is part of the geometry): the ids were read from it, and
-// a table holds page ids of the pools it is used with. (A table used with a pool that has
-// fewer pages than the pool its ids were recorded for breaks that; the header says so.)
-// Layout (int32): [0] id + 1 (0: never written), [1..7] geometry, [8] kind << 31 | split
-// << 7 | request (kind 0: past the last unit, 1: a unit), [9..11] kv head, length,
+// for the same table and the same two pools (their addresses are part of the geometry): the
+// ids were read from that table, and a table holds page ids of the pools it is used with.
+// (Only a pool freed and allocated again smaller at the same address, with a table at its
+// old address, escapes the check; the header says so.)
+// Layout (int32): [0] id + 1 (0: never written), [1..11] geometry, [12] kind << 31 | split
+// << 7 | request (kind 0: past the last unit, 1: a unit), [13..15] kv head, length,
 // position; [32..63] page ids, PAGES per wave; [64..127] raw lengths; [128..191] positions
 // (batch <= 64). The unit and geometry fit in the entry's first 64 bytes, one scalar line.
 constexpr int kPlanUnits = 2048;
@@ -508,13 +510,15 @@ constexpr int kPlanPos = 128;
 constexpr size_t kPlanBytes = (size_t)kPlanUnits * kPlanEntryInts * sizeof(int32_t);
 constexpr int kPlanMaxBatch = 64;
 
-constexpr int kPlanGeo = 7;
+constexpr int kPlanGeo = 11;
 constexpr int kPlanKind = 1 + kPlanGeo;
-constexpr int kPlanHead = 16;  // [0] id + 1, [1..7] geometry, [8] kind|s|b, [9..11] g len pos
+constexpr int kPlanHead = 16;  // [0] id + 1, [1..11] geometry, [12] kind|s|b, [13..15] g len pos
+static_assert(kPlanKind + 4 == kPlanHead, "the unit and geometry fill one 64-byte line");
 
 // What a plan entry's unit depends on besides the lengths and positions: the launch shape
-// (the kernel's append flag and pages and waves per split included), and the table's
-// address, so that the recorded page ids were read from this table.
+// (the kernel's append flag and pages and waves per split included), the table's address,
+// so that the recorded page ids were read from this table, and the pools' addresses, so
+// that they are page ids of these pools.
 template <int PAGES, int WAVES, bool APPEND>
 __device__ __forceinline__ void plan_geometry(const DecodeArgs& a, int (&g)[kPlanGeo]) {
     // packed exactly where the fields fit (plan_fits checks the ranges)
@@ -527,6 +531,12 @@ __device__ __forceinline__ void plan_geometry(const DecodeArgs& a, int (&g)[kPla
     const uint64_t t = (uintptr_t)a.tables;  // a preloaded argument: no wait for the block
     g[5] = (int)(uint32_t)t;
     g[6] = (int)(uint32_t)(t >> 32);
+    // From the argument block, which the check waits for anyway (plan_fits, g[1..4]).
+    const uint64_t kp = (uintptr_t)a.k_pool, vp = (uintptr_t)a.v_pool;
+    g[7] = (int)(uint32_t)kp;
+    g[8] = (int)(uint32_t)(kp >> 32);
+    g[9] = (int)(uint32_t)vp;
+    g[10] = (int)(uint32_t)(vp >> 32);
 }
 
 // Whether plan_geometry packs this launch exactly: batch <= 64, split_shift < 32, lens
@@ -1407,14 +1417,16 @@ __global__ __launch_bounds__(256) void clear_counters_kernel(uint32_t* c, int n)
 
 constexpr int kMaxDevices = 64;
 struct ScratchSlot {
-    std::once_flag once;
-    void* ptr = nullptr;
-    hipError_t err = hipSuccess;
+    std::mutex mu;
+    std::atomic<void*> ptr{nullptr};
 };
 ScratchSlot g_scratch[kMaxDevices];
 
 // The device address of this GPU's `scratch`, looked up (and its counters cleared on
-// `stream`) the first time a device is used; nullptr with the error message set on failure.
+// `stream`) the first time a device is used; nullptr with the error message set on failure,
+// in which case the next call on that device tries again. Under stream capture the clear is
+// recorded into the graph instead of running; that is harmless, because the counters are
+// zero at load and every launch leaves them zero.
 void* scratch_ptr(hipStream_t stream, const char* what) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
@@ -1424,25 +1436,26 @@ void* scratch_ptr(hipStream_t stream, const char* what) {
         return nullptr;
     }
     ScratchSlot& slot = g_scratch[dev];
-    std::call_once(slot.once, [&] {
-        void* p = nullptr;
-        slot.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (slot.err != hipSuccess) {
-            (void)hipGetLastError();
-            return;
-        }
+    if (void* p = slot.ptr.load(std::memory_order_acquire)) return p;
+    std::lock_guard<std::mutex> lock(slot.mu);
+    if (void* p = slot.ptr.load(std::memory_order_relaxed)) return p;
+    void* p = nullptr;
+    hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err == hipSuccess) {
         hipLaunchKernelGGL(clear_counters_kernel, dim3((kScratchCounters + 255) / 256),
                            dim3(256), 0, stream, static_cast<uint32_t*>(p),
                            (int)kScratchCounters);
-        slot.err = hipGetLastError();
-        if (slot.err == hipSuccess) slot.ptr = p;
-    });
-    if (!slot.ptr) {
+        err = hipGetLastError();
+    } else {
+        (void)hipGetLastError();
+    }
+    if (err != hipSuccess) {
         set_error(CRUCIBLE_ERR_LAUNCH, "%s: device scratch unavailable on device %d: %s", what,
-                  dev, hipGetErrorString(slot.err));
+                  dev, hipGetErrorString(err));
         return nullptr;
     }
-    return slot.ptr;
+    slot.ptr.store(p, std::memory_order_release);
+    return p;
 }
 
 }  // namespace

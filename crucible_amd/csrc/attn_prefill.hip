@@ -1306,18 +1306,25 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
             const int kbase = t * kKeyTile;
             if (wave_last < kbase) break;  // later tiles lie above the diagonal too
             int64_t pg[4];
+            // Hybrid: a page wholly at or past the segment's absolute start holds only chunk
+            // keys, which come from current_k/v below; neither its table entry nor the pool
+            // is read for it, as in the reference (kernels.cu:2012-2016). Uniform per page.
+            bool from_pool[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int idx = min(t * 4 + j, last_page);  // clamped: in bounds, masked later
-                pg[j] = block_base(a.addr, table ? (int64_t)table[idx] : (int64_t)idx);
+                from_pool[j] = !HYB || idx * kPageTokens < d_astart;
+                pg[j] = from_pool[j] ? block_base(a.addr, table ? (int64_t)table[idx] : (int64_t)idx)
+                                     : 0;
             }
             // K operand of key block kb: key 16 kb + col (page kb of the tile), channels
             // 8 grp .. +7 and 32 + 8 grp .. +7; V^T operand of channel 16 db + col: slots
             // 4 grp .. +3 of pages 2 ks and 2 ks + 1 (keys 32 ks + 4 grp .. and +16).
-            half8_t ka[4][2];
-            half4_t va[4][2][2];
+            half8_t ka[4][2] = {};
+            half4_t va[4][2][2] = {};
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
+                if (!from_pool[kb]) continue;
                 const half_t* kp = a.k_pool + pg[kb] + (int64_t)col * kv_dim + g * kHeadDim + 8 * grp;
                 ka[kb][0] = *reinterpret_cast<const half8_t*>(kp);
                 ka[kb][1] = *reinterpret_cast<const half8_t*>(kp + 32);
@@ -1328,6 +1335,7 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
                 for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
                     for (int hf = 0; hf < 2; ++hf) {
+                        if (!from_pool[2 * ks + hf]) continue;
                         const half_t* vp = a.v_pool + pg[2 * ks + hf] +
                                            (int64_t)(g * kHeadDim + 16 * db + col) * kPageTokens +
                                            4 * grp;
@@ -1598,9 +1606,10 @@ int launch_prefill(const PrefillArgs& a_in, int64_t tile_rows_total, int64_t z, 
         return a.heavy_first ? dim3((unsigned)n) : dim3((unsigned)gx, (unsigned)gy, (unsigned)z);
     };
     const LdsGrid lg = lds_grid(a, tile_rows_total, z);
-    // Precision of P in the PV product: one fp16 operand (P16, the default) or fp16 hi + lo
-    // (about 22 bits, when the tuning key asks for it).
-    const bool p16 = tuning(CRUCIBLE_TUNE_PREFILL_P16) != 0;
+    // Precision of P in the PV product: fp16 hi + lo (about 22 bits, the default: the
+    // reference validator's element gate holds unwidened) or one fp16 operand (P16, when the
+    // tuning key asks for it: one PV product per block instead of two).
+    const bool p16 = tuning(CRUCIBLE_TUNE_PREFILL_P16) == 1;
     // The register-direct form when the LDS form would leave CUs without a workgroup
     // (short prompts: config 1 is 96 workgroups); the LDS form, which reads each K/V tile
     // once per 64 rows instead of once per 16, when its grid fills the chip.

@@ -127,9 +127,13 @@ __device__ void attend_generic(GenericLds& lds, const GenericKeys& ks, int n, fl
         const int kend = min(64, n - key0);
         for (int pp = 0; pp * kPageTokens < kend; ++pp) {
             const int pk = key0 + pp * kPageTokens;  // first key of the page
-            const int64_t page = ks.table ? (int64_t)ks.table[pk >> kPageShift]
-                                          : (int64_t)(pk >> kPageShift);
-            const int64_t base = block_base(ks.addr, page);
+            // A page wholly at or past astart (hybrid) comes from cur_v alone: neither its
+            // table entry nor the pool is read, as in the reference (kernels.cu:2012-2016).
+            const bool from_pool = pk < ks.astart;  // uniform
+            int64_t base = 0;
+            if (from_pool)
+                base = block_base(ks.addr, ks.table ? (int64_t)ks.table[pk >> kPageShift]
+                                                    : (int64_t)(pk >> kPageShift));
             const float4_t* pw = reinterpret_cast<const float4_t*>(&lds.p[wave][pp * kPageTokens]);
             const float4_t p0 = pw[0], p1 = pw[1], p2 = pw[2], p3 = pw[3];
             const float pv[16] = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3],
@@ -138,9 +142,12 @@ __device__ void attend_generic(GenericLds& lds, const GenericKeys& ks, int n, fl
             for (int i = 0; i < kGenericMaxHeadDim / 64; ++i) {
                 const int d = lane + 64 * i;
                 if (d >= hd) break;
-                const half_t* vr = ks.v_pool + base + (int64_t)(head_off + d) * kPageTokens;
-                const half8_t v0 = *reinterpret_cast<const half8_t*>(vr);
-                const half8_t v1 = *reinterpret_cast<const half8_t*>(vr + 8);
+                half8_t v0 = {}, v1 = {};
+                if (from_pool) {
+                    const half_t* vr = ks.v_pool + base + (int64_t)(head_off + d) * kPageTokens;
+                    v0 = *reinterpret_cast<const half8_t*>(vr);
+                    v1 = *reinterpret_cast<const half8_t*>(vr + 8);
+                }
                 float acc = o[i];
 #pragma unroll
                 for (int s = 0; s < kPageTokens; ++s) {

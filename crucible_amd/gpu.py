@@ -110,19 +110,32 @@ class Gpu:
         self.lib = _lib.load()
         self.device = torch.device("cuda", device) if isinstance(device, int) else device
         self._workspaces: dict[tuple, torch.Tensor] = {}
+        self._bindings: dict[tuple, tuple] = {}  # workspace key -> pools it last served
 
     # ------------------------------------------------------------- plumbing
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
 
-    def workspace(self, batch: int, n_head: int, max_seq: int) -> torch.Tensor:
-        """Split-K scratch for decode, allocated once per shape (never inside a call)."""
+    def workspace(self, batch: int, n_head: int, max_seq: int, pools=None) -> torch.Tensor:
+        """Split-K scratch for decode, allocated once per shape (never inside a call).
+
+        ``pools`` is the call's ``(k_pool, v_pool)``. The workspace's unit plan holds page
+        ids read for one table and pair of pools, and the kernel takes an entry only for the
+        same three addresses; a pool freed and allocated again at the same address with
+        fewer pages would pass that check. So the cached workspace remembers the pools'
+        addresses and sizes and is zeroed (on the current stream, ordered before the call)
+        whenever they change."""
         key = (batch, n_head, max_seq)
         ws = self._workspaces.get(key)
         if ws is None:
             nbytes = self.lib.crucible_attention_decode_workspace_bytes(batch, n_head, max_seq)
             ws = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=self.device)
             self._workspaces[key] = ws
+        if pools is not None:
+            binding = tuple((t.data_ptr(), t.numel()) for t in pools)
+            if self._bindings.get(key, binding) != binding:
+                ws.zero_()
+            self._bindings[key] = binding
         return ws
 
     @staticmethod
@@ -183,7 +196,8 @@ class Gpu:
         _need(v_pool, "v_pool", dtype=torch.float16)
         _need(page_tables, "page_tables", dtype=torch.int32, numel=batch * table_stride)
         _need(seq_lens, "seq_lens", dtype=torch.int32, numel=batch)
-        ws = workspace if workspace is not None else self.workspace(batch, n_head, max_seq)
+        ws = workspace if workspace is not None else self.workspace(batch, n_head, max_seq,
+                                                                   (k_pool, v_pool))
         _need(ws, "workspace")
         _lib.check(self.lib.crucible_attention_decode_paged(
             _ptr(q), _dtype(q, "q"), _ptr(k_pool), _ptr(v_pool), _ptr(out), _dtype(out, "out"),
@@ -206,7 +220,8 @@ class Gpu:
         _need(page_tables, "page_tables", dtype=torch.int32, numel=batch * table_stride)
         _need(positions, "positions", dtype=torch.int32, numel=batch)
         _need(seq_lens, "seq_lens", dtype=torch.int32, numel=batch)
-        ws = workspace if workspace is not None else self.workspace(batch, n_head, max_seq)
+        ws = workspace if workspace is not None else self.workspace(batch, n_head, max_seq,
+                                                                   (k_pool, v_pool))
         _lib.check(self.lib.crucible_attention_decode_paged_append(
             _ptr(q), _dtype(q, "q"), _ptr(k_new), _ptr(v_new), _dtype(k_new, "k_new"),
             _ptr(k_pool), _ptr(v_pool), _ptr(out), _dtype(out, "out"), _ptr(page_tables),
@@ -234,7 +249,8 @@ class Gpu:
             _need(rope_cos, "rope_cos", dtype=torch.float32)
             _need(rope_sin, "rope_sin", dtype=torch.float32, numel=rope_cos.numel())
             max_pos = rope_cos.shape[0]
-        ws = workspace if workspace is not None else self.workspace(batch, n_head, max_seq)
+        ws = workspace if workspace is not None else self.workspace(batch, n_head, max_seq,
+                                                                   (k_pool, v_pool))
         _lib.check(self.lib.crucible_attention_decode_qkv_paged_append(
             _ptr(qkv), row_stride, _ptr(rope_cos), _ptr(rope_sin), max_pos, _ptr(k_pool),
             _ptr(v_pool), _ptr(out), _dtype(out, "out"), _ptr(page_tables), _ptr(positions),

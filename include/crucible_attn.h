@@ -87,7 +87,7 @@ enum crucible_tuning_key {
     CRUCIBLE_TUNE_PREFILL_BUFS = 6,        /* prefill LDS ring depth in key tiles: 4, 6 */
     CRUCIBLE_TUNE_LINEAR_TILE = 7,         /* projection tiles: 4 or 16 columns (decode), 32 (prompt rows) */
     CRUCIBLE_TUNE_DECODE_COMBINE_WIDTH = 8, /* decode splits merged per round trip: 8, 16 */
-    CRUCIBLE_TUNE_PREFILL_P16 = 9,         /* prefill P operand: 1 one fp16 (default), 0 fp16 hi + lo */
+    CRUCIBLE_TUNE_PREFILL_P16 = 9,         /* prefill P operand: 0 fp16 hi + lo (default), 1 one fp16 */
     CRUCIBLE_TUNE_PREFILL_M32 = 10,        /* prefill 32-row waves on 32x32 MFMAs: 1 (default), 0 */
     CRUCIBLE_TUNE_COUNT = 11
 };
@@ -158,10 +158,12 @@ int crucible_cache_store_packed_paged(const void* src, int src_dtype, void* pool
  * the round trip that loads the lengths instead of searching for it. Page ids
  * are still read from the table on every launch (beside the page loads, which
  * are reissued if an id changed), so a rewritten table is always honoured; the
- * plan only saves the search. An entry is used only for the same table address.
- * Its page ids are loaded from before they are checked, so a workspace whose plan
- * was made with one table and pool must be zeroed again (or another workspace
- * used) before that table serves a pool with fewer pages. Calls of any batch size may share one
+ * plan only saves the search. An entry is used only for the same table address and
+ * the same k_pool and v_pool addresses. Its page ids are loaded from before they are
+ * checked, so one case is left to the caller: a pool freed and allocated again, smaller,
+ * at the same address, served by a table at its old address. Zero the workspace again
+ * (or use another) when a pool is reallocated; pools allocated once, as the reference
+ * engine allocates them, never meet this. Calls of any batch size may share one
  * workspace, one launch at a time (launches that share it must be ordered, e.g.
  * on one stream). Two launches that run at once on one workspace (two streams
  * without an event between them) race on the counters and partials: a split can
@@ -224,13 +226,17 @@ int crucible_attention_decode_kernel_name(int64_t batch, int64_t n_head, int64_t
  * file-scope device array of this library (4 MiB per GPU, held until the process ends)
  * instead of a workspace argument. Same kernels, same results bit for bit. Limits:
  * batch * n_kv_head <= 8192, and batch * n_head * n_splits * 66 * 4 bytes of partials
- * <= 4 MiB - 32 KiB, where n_splits = ceil(ceil(max_seq / 16) / split pages) and a split
- * is 8, 16 or 32 pages (b16 x 12 heads fits up to max_seq 65536 tokens); larger calls
- * return CRUCIBLE_ERR_WORKSPACE before any launch. It calls no hipMalloc or hipFree;
- * the first call on a device looks up the array's address and clears its counters with
- * a small kernel on `stream`. Every call on one GPU shares that GPU's array: calls that
- * overlap on one GPU (several streams, or threads) race and must be ordered by the
- * caller. */
+ * <= 4 MiB - 32 KiB (4,161,536 bytes), where n_splits = ceil(ceil(max_seq / 16) /
+ * split pages) and a split is the 8, 16 or 32 pages the decode shape picks from
+ * batch * n_kv_head * ceil(max_seq / 16). Batch 16 x 12 query heads (3 or 12 kv heads)
+ * fits up to max_seq 20,992 tokens (82 splits of 16 pages); larger calls return
+ * CRUCIBLE_ERR_WORKSPACE before any launch. It calls no
+ * hipMalloc or hipFree; the first call on a device looks up the array's address and
+ * clears its counters with a small kernel on `stream` (under stream capture that clear
+ * is recorded into the graph, which is harmless: the counters are zero at load and every
+ * launch leaves them zero; a failed lookup is tried again on the next call). Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (several streams, or
+ * threads) race and must be ordered by the caller. */
 int crucible_attention_decode_paged_append_noalloc(
     const void* q, int q_dtype, const void* k_new, const void* v_new, int kv_dtype,
     void* k_pool, void* v_pool, void* out, int out_dtype, const int32_t* page_tables,
@@ -281,10 +287,12 @@ int crucible_attention_split(const void* q, int q_dtype, const void* k_cache,
  * Causal attention for query rows whose keys are already in the pool. q is
  * [rows][n_head * head_dim], out likewise. Row r sees keys [0, pos_r].
  * Arithmetic (head_dim 64): QK^T and PV on fp16 MFMAs with f32 accumulation, softmax in
- * f32. P enters the PV product as one fp16 operand rounded to nearest even, so an output
- * moves by at most 2^-11 sum_i w_i |v_i| from exact softmax weights (max-abs 4.4e-4 over
- * the reference's corpus); CRUCIBLE_TUNE_PREFILL_P16 = 0 carries P as fp16 hi + lo (about
- * 22 bits) for two PV products per block instead of one.
+ * f32. P enters the PV product as fp16 hi + lo (about 22 bits; within the reference
+ * validator's element gate, 2e-5 + 2e-5|ref|, unwidened). CRUCIBLE_TUNE_PREFILL_P16 = 1
+ * carries P as one fp16 operand rounded to nearest even instead: one PV product per block
+ * instead of two (about 1.3x faster tile loops on long prompts), and an output then moves
+ * by at most 2^-11 sum_i w_i |v_i| from exact softmax weights (max-abs 4.4e-4 over the
+ * reference's corpus).
  */
 
 /* Replaces Gpu::attention_prefill_paged (gpu.rs:1502-1549; kernels.cu:1927-1936):

@@ -40,10 +40,15 @@ def build() -> str:
 
 
 def lib():
+    """The built oracle library. It is never built here: a test process may already hold
+    the GPU, and starting ``make`` from it would fork a GPU-initialised process. Build it
+    beforehand (``oracle.build()``, ``__graft_entry__.build()``)."""
     global _lib
     if _lib is None:
         if not os.path.exists(_LIB_PATH):
-            build()
+            raise RuntimeError(f"oracle library missing: {_LIB_PATH}; build it first "
+                               "(python -c 'import oracle; oracle.build()', or "
+                               "__graft_entry__.build())")
         _lib = _bind(ctypes.CDLL(_LIB_PATH))
     return _lib
 

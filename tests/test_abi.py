@@ -157,6 +157,22 @@ def test_qkv_decode_entry_validates_before_launch():
     assert call(ws_bytes=16) == _lib.ERR_WORKSPACE        # split-K workspace too small
 
 
+def test_noalloc_limit_is_checked_before_launch():
+    """The allocation-free decode's documented limit for batch 16 x 12 query heads is
+    max_seq 20,992; one page more (83 splits of 16 pages) returns CRUCIBLE_ERR_WORKSPACE
+    before anything touches a device (the pointers here are never dereferenced)."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+    for n_kv in (3, 12):
+        rc = lib.crucible_attention_decode_paged_append_noalloc(
+            fake, _lib.F16, fake, fake, _lib.F32, fake, fake, fake, _lib.F32, fake, fake, fake,
+            16, 12, n_kv, 64, 1313, 1, 0, n_kv * 64, 20992 + 16, None)
+        assert rc == _lib.ERR_WORKSPACE, n_kv
+        assert "static scratch" in _lib.last_error()[1]
+        partials = 16 * 12 * 82 * 66 * 4   # the largest call that fits: 82 splits
+        assert partials <= (4 << 20) - 32 * 1024 < 16 * 12 * 83 * 66 * 4
+
+
 def test_tuning_overrides_are_validated_and_restorable():
     """Launch-shape overrides: every key has its environment name, accepts only its
     documented values, and reads back what was set (no GPU involved)."""

@@ -595,10 +595,11 @@ def test_unit_plan_with_the_qkv_rope_entry(gpu, dev):
 
 
 def test_unit_plan_is_not_taken_for_other_pools(gpu, dev):
-    """A plan entry records the table address it was made for: a call with equal lengths
-    and shape on other pools and another table rebuilds it (its entries then hold the new
-    address) and equals a call on a zeroed workspace, bit for bit. Both pools have the same
-    number of pages, so no page id of either table lies outside the other pool."""
+    """A plan entry records the table and pool addresses it was made for: a call with equal
+    lengths and shape on other pools and another table rebuilds it (its entries then hold
+    the new addresses) and equals a call on a zeroed workspace, bit for bit; so does a call
+    with the same table and other pools. Both pools have the same number of pages, so no
+    page id of either table lies outside the other pool."""
     rng = np.random.default_rng(2028)
     n_head, n_kv, n_layer, layer, stride = 12, 3, 1, 0, 128
     batch, max_seq, kv = 16, 2048, n_kv * 64
@@ -631,7 +632,40 @@ def test_unit_plan_is_not_taken_for_other_pools(gpu, dev):
     want = call(torch.zeros_like(warm), kb2, vb2, tb)
     assert torch.equal(got.view(torch.int32), want.view(torch.int32))
     assert torch.equal(kb.view(torch.int16), kb2.view(torch.int16))
-    # the entry's words 6 and 7: the table address it was made for
-    e = warm[PLAN_OFFSET:PLAN_OFFSET + 4 * PLAN_ENTRY_INTS].view(torch.int32).cpu().numpy()
-    w = [int(x) & 0xFFFFFFFF for x in e[6:8]]
-    assert w[0] | w[1] << 32 == tb.data_ptr()
+
+    def addresses():
+        # the entry's words 6..11: the table, k_pool and v_pool addresses it was made for
+        e = warm[PLAN_OFFSET:PLAN_OFFSET + 4 * PLAN_ENTRY_INTS].view(torch.int32).cpu().numpy()
+        w = [int(x) & 0xFFFFFFFF for x in e[6:12]]
+        return [w[0] | w[1] << 32, w[2] | w[3] << 32, w[4] | w[5] << 32]
+
+    assert addresses() == [tb.data_ptr(), kb.data_ptr(), vb.data_ptr()]
+    # the same table address with the other pools: the entry is rebuilt for those pools
+    call(warm, ka, va, ta)
+    assert addresses() == [ta.data_ptr(), ka.data_ptr(), va.data_ptr()]
+    kc, vc = kb.clone(), vb.clone()
+    got = call(warm, kb, vb, ta)
+    assert addresses() == [ta.data_ptr(), kb.data_ptr(), vb.data_ptr()]
+    want = call(torch.zeros_like(warm), kc, vc, ta)
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+    assert torch.equal(kb.view(torch.int16), kc.view(torch.int16))
+    assert torch.equal(vb.view(torch.int16), vc.view(torch.int16))
+
+
+def test_cached_workspace_is_zeroed_when_the_pools_change(gpu, dev):
+    """Gpu.workspace keeps one workspace per shape and zeroes it when a call brings other
+    pools (address or size), so a plan made for one pool never meets a pool reallocated
+    smaller at the same address."""
+    batch, n_head, max_seq = 4, 12, 512
+    k1 = torch.zeros(4096, dtype=torch.float16, device=dev)
+    v1 = torch.zeros(4096, dtype=torch.float16, device=dev)
+    ws = gpu.workspace(batch, n_head, max_seq, (k1, v1))
+    ws[PLAN_OFFSET:PLAN_OFFSET + 64].fill_(7)
+    assert gpu.workspace(batch, n_head, max_seq, (k1, v1)) is ws
+    assert int(ws[PLAN_OFFSET:PLAN_OFFSET + 64].sum()) == 7 * 64  # same pools: kept
+    assert gpu.workspace(batch, n_head, max_seq, (k1[:2048], v1[:2048])) is ws
+    assert int(ws.sum()) == 0  # same addresses, fewer elements: zeroed
+    ws[PLAN_OFFSET:PLAN_OFFSET + 64].fill_(7)
+    k2 = torch.zeros(4096, dtype=torch.float16, device=dev)
+    gpu.workspace(batch, n_head, max_seq, (k2, v1[:2048]))
+    assert int(ws.sum()) == 0  # another address: zeroed

@@ -8,9 +8,9 @@ compared with the f64 oracle on every element under the reference's element gate
 exact: future-page poison leaves outputs bit-identical (:597-632), descriptor composition,
 order and page reuse leave each request's bits unchanged (:639-682), and output rows outside
 the written range keep their sentinel (:23, :271-287). Both prefill kernels (LDS-tiled and
-register-direct) run every test in both precisions of P: the default single fp16 operand
-(P16, gated with the rounding term 2^-11 sum w|v| added to the element gate) and the fp16
-hi + lo pair (about 22 bits, the reference's gate as it stands); the LDS-tiled form runs
+register-direct) run every test in both precisions of P: the default fp16 hi + lo pair
+(about 22 bits, the reference's gate as it stands) and the opt-in single fp16 operand (P16,
+gated with the rounding term 2^-11 sum w|v| added to the element gate); the LDS-tiled form runs
 with 16 rows per wave and with 32 (the 32x32-MFMA kernel, and once over the corpus the
 16x16 kernel of that shape).
 """
@@ -25,19 +25,20 @@ from gates import element_gate
 pytestmark = pytest.mark.gpu
 
 
-_P16 = [True]  # precision of the running test's prefill_form
+_P16 = [False]  # precision of the running test's prefill_form
 
 
-@pytest.fixture(autouse=True, params=["lds", "lds32", "direct", "lds-hilo", "lds32-hilo",
-                                        "direct-hilo"])
+@pytest.fixture(autouse=True, params=["lds", "lds32", "direct", "lds-p16", "lds32-p16",
+                                        "direct-p16"])
 def prefill_form(request, tune):
     """Every test runs through every prefill kernel: the LDS-tiled form with 16 rows per wave
     and with 32 (the 32x32-MFMA kernel), and the register-direct form (the library picks one
-    by grid size; the overrides force it), each with P as one fp16 operand (the default) and
-    as fp16 hi + lo."""
+    by grid size; the overrides force it), each with P as fp16 hi + lo (the default, under
+    the reference's unwidened gate) and as one fp16 operand (P16)."""
     form = request.param
-    _P16[0] = not form.endswith("-hilo")
-    tune(prefill_direct=1 if form.startswith("direct") else 0, prefill_p16=int(_P16[0]),
+    _P16[0] = form.endswith("-p16")
+    tune(prefill_direct=1 if form.startswith("direct") else 0,
+         prefill_p16=1 if _P16[0] else None,
          prefill_qb=2 if form.startswith("lds32") else 1 if form.startswith("lds") else None)
     return form
 
@@ -242,6 +243,55 @@ def test_single_sequence_params_and_contiguous_forms(gpu, dev):
         got_c = d.result()[:rows]
         # same keys, same arithmetic: the contiguous form is bit-identical to the paged one
         assert np.array_equal(got_c.view(np.uint32), got.view(np.uint32))
+
+
+GPU_PAGED_LENS = [1, 7, 15, 16, 17, 31, 32, 33, 64, 127, 128, 129, 256, 511, 512, 1023]
+
+
+def _contiguous_caches(fx, n_hist, dev):
+    """A contiguous cache ([layer][cap][kv_dim], layer 1) holding request 0's first n_hist
+    rows, gathered from the fixture's pools: the same fp16 bits the paged forms read."""
+    cap = A.CONTEXT
+    k_c = np.zeros(A.LAYERS * cap * A.KD, np.uint16)
+    v_c = np.zeros_like(k_c)
+    kd = oracle.f32_to_f16_bits(oracle.gather(0, fx.k_pool, fx.tables[0], n_hist, A.KD,
+                                              A.LAYERS, A.LAYER))
+    vd = oracle.f32_to_f16_bits(oracle.gather(1, fx.v_pool, fx.tables[0], n_hist, A.KD,
+                                              A.LAYERS, A.LAYER))
+    for kind, cache, src in ((0, k_c, kd), (1, v_c, vd)):
+        oracle.cache_store(oracle.STORE_CONTIG, kind, cache, src, rows=n_hist, kv_dim=A.KD,
+                           layer_base=A.LAYER * cap * A.KD, pos_offset=0)
+    return _dev(k_c, dev), _dev(v_c, dev)
+
+
+def test_paged_equals_contiguous_over_the_gpu_paged_lengths(gpu, dev):
+    """The reference's gpu-paged check (main.rs:106-111, 1253-1257): for every length of its
+    list, a prompt of that many rows (positions 0..L-1) through the params form and the
+    segment form on the paged pool, and through the contiguous form on a cache holding the
+    same rows. Paged must equal contiguous bit for bit, in both paged forms; every output
+    is also checked against the f64 oracle."""
+    for L in GPU_PAGED_LENS:
+        case = A.Case(f"gpu-paged-{L}", [A.Slice(0, 0, L)], A.SEED + L, 0)
+        if case.name not in _ORACLE:
+            fx = A.fixture(case)
+            _ORACLE[case.name] = (fx, A.oracle_out(fx), A.oracle_abs_v(fx))
+        fx, want, vabs = _ORACLE[case.name]
+        d = Device(fx, dev)
+        params = _dev(np.zeros(6, np.int32), dev)
+        gpu.attention_prefill_paged(d.q[:L], d.k, d.v, d.out, d.tables[0], L, A.HEADS,
+                                    A.KV_HEADS, A.HD, A.LAYERS, A.LAYER, A.KD, A.CONTEXT, params)
+        got_p = d.result()[:L].copy()
+        d.reset()
+        run_segments(gpu, d)
+        got_s = d.result()[:L].copy()
+        k_c, v_c = _contiguous_caches(fx, L, dev)
+        d.reset()
+        gpu.attention_prefill(d.q[:L], k_c, v_c, d.out, L, A.HEADS, A.KV_HEADS, A.HD,
+                              A.CONTEXT, A.KD, A.LAYER * A.CONTEXT * A.KD, 0)
+        got_c = d.result()[:L].copy()
+        assert np.array_equal(got_p.view(np.uint32), got_c.view(np.uint32)), f"params, L={L}"
+        assert np.array_equal(got_s.view(np.uint32), got_c.view(np.uint32)), f"segments, L={L}"
+        gate(got_c, want[:L], f"gpu-paged L={L}", vabs=vabs[:L] if _P16[0] else None)
 
 
 def test_composition_order_and_page_reuse_invariance(gpu, dev):

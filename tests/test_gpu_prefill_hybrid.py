@@ -56,8 +56,8 @@ def test_hybrid_reads_the_chunk_from_current_kv(gpu, dev, tune, case):
     clean = Device(fx, dev)
     _run(gpu, clean, False)
     want = clean.result().copy()
-    # the default P16 precision: the element gate with its rounding term
-    element_gate(want, A.oracle_out(fx), f"{case.name} pool path", vabs=A.oracle_abs_v(fx))
+    # the default precision (P as fp16 hi + lo): the reference's element gate, unwidened
+    element_gate(want, A.oracle_out(fx), f"{case.name} pool path")
     # current K/V: the chunk's pool values widened to f32; then poison those pool slots
     cur_k = np.zeros((fx.rows, A.KD), np.float32)
     cur_v = np.zeros((fx.rows, A.KD), np.float32)
@@ -106,3 +106,32 @@ def test_hybrid_rounds_current_kv_like_the_append(gpu, dev, tune, case):
     _run(gpu, h, True, _dev(cur_k, dev), _dev(cur_v, dev))
     got = h.result()
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), case.name
+
+
+@pytest.mark.parametrize("case", HYBRID_CASES, ids=lambda c: c.name)
+def test_hybrid_ignores_table_entries_of_chunk_pages(gpu, dev, tune, case):
+    """The reference never reads the table or the pool for keys at or past absolute_start
+    (kernels.cu:2012-2016), so a table whose entries for pages wholly inside the chunk are
+    not yet the chunk's pages must give the same bits. Here those entries all name page 0
+    (a valid page, so every address stays inside the pool) and the output is unchanged."""
+    for direct in (1, None):  # the register-direct kernel, and the launcher's own choice
+        tune(prefill_direct=direct)
+        fx = A.fixture(case)
+        rng = np.random.default_rng(5)
+        cur_k = rng.standard_normal((fx.rows, A.KD)).astype(np.float32)
+        cur_v = rng.standard_normal((fx.rows, A.KD)).astype(np.float32)
+        d = Device(fx, dev)
+        _run(gpu, d, True, _dev(cur_k, dev), _dev(cur_v, dev))
+        want = d.result().copy()
+        tables = fx.tables.copy()
+        changed = 0
+        for packed, n, start, table in fx.segments:
+            for page in range(-(-int(start) // 16), -(-int(start + n) // 16)):
+                tables[table, page] = 0
+                changed += 1
+        assert changed > 0
+        d2 = Device(fx, dev)
+        d2.tables = _dev(tables, dev)
+        _run(gpu, d2, True, _dev(cur_k, dev), _dev(cur_v, dev))
+        got = d2.result()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), case.name

@@ -24,6 +24,25 @@ def test_reference_paging_kats_pass(tmp_path):
     assert "19 tests, 0 failed" in proc.stdout
 
 
+def test_paging_kats_pass_under_address_and_undefined_sanitizers(tmp_path):
+    """The same KATs with the allocator built under AddressSanitizer and UBSan (host code
+    only, g++ on the CPU): every out-of-range id, double free and rollback path of
+    paging.cpp runs with bounds, lifetime and overflow checks, and any report fails."""
+    here = os.path.dirname(os.path.abspath(__file__))
+    path = str(tmp_path / "paging_kat_san")
+    subprocess.run([os.environ.get("CXX", "g++"), "-O1", "-g", "-std=c++17", "-Wall",
+                    "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+                    "-fno-omit-frame-pointer", "-I", _build.CSRC,
+                    os.path.join(here, "paging_kat.cpp"), os.path.join(_build.CSRC, "paging.cpp"),
+                    "-o", path], check=True, capture_output=True, text=True)
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:halt_on_error=1",
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1")
+    proc = subprocess.run([path], capture_output=True, text=True, timeout=120, env=env)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    assert "19 tests, 0 failed" in proc.stdout
+    assert "runtime error" not in proc.stderr and "AddressSanitizer" not in proc.stderr
+
+
 def test_c_api_allocation_order_and_errors():
     pool = PagePool(4, 12, 192)
     assert [pool.alloc(), pool.alloc()] == [0, 1]

@@ -11,6 +11,7 @@ import torch
 import oracle
 from attn_cases import disjoint_tables, random_pools
 from crucible_amd import _lib
+from gates import element_gate
 
 pytestmark = pytest.mark.gpu
 
@@ -37,7 +38,7 @@ def _case(seed, lens, n_head, n_kv, n_layer, stride):
 
 
 def _call(lib, entry, dev, kp, vp, tables, q, k_new, v_new, lens, n_head, n_kv, n_layer, layer,
-          stride, workspace=None):
+          stride, workspace=None, max_seq=None):
     """One launch through the C ABI on copies of the pools; returns (k, v, out) on the host."""
     batch = len(lens)
     kv = n_kv * 64
@@ -51,7 +52,7 @@ def _call(lib, entry, dev, kp, vp, tables, q, k_new, v_new, lens, n_head, n_kv, 
     args = [d_q.data_ptr(), _lib.F16, d_kn.data_ptr(), d_vn.data_ptr(), _lib.F32,
             d_k.data_ptr(), d_v.data_ptr(), out.data_ptr(), _lib.F32, d_tab.data_ptr(),
             d_pos.data_ptr(), d_len.data_ptr(), batch, n_head, n_kv, 64, stride, n_layer, layer,
-            kv, stride * 16]
+            kv, max_seq or stride * 16]
     if workspace is not None:
         args += [workspace.data_ptr(), workspace.numel()]
     _lib.check(entry(*args, stream))
@@ -84,9 +85,50 @@ def test_noalloc_equals_workspace_form_on_two_calls(dev):
                                            np.asarray(lens, np.int32), n_head=n_head,
                                            n_kv_head=n_kv, head_dim=64, table_stride=stride,
                                            n_layer=n_layer, layer=layer)
-        err = float(np.abs(o2 - want).max())
+        err = element_gate(o2, want, f"no-alloc call {i}")
         print(f"no-alloc call {i}: max-abs {err:.3e} against the oracle", flush=True)
-        assert err <= 2e-5 + 2e-5 * float(np.abs(want).max())
+
+
+def test_noalloc_at_the_documented_limit(dev):
+    """The header's limit for batch 16 x 12 query heads: max_seq 20,992 tokens (82 splits of
+    16 pages) runs, bit-identical to the workspace form and within the element gate, with one
+    request at the full length; max_seq 21,008 (83 splits) is refused before any launch."""
+    lib = _lib.load()
+    n_head, n_kv, n_layer, layer = 12, 3, 1, 0
+    limit = 20992
+    stride = limit // 16
+    lens = [limit] + np.random.default_rng(7).integers(64, 1500, 15).astype(int).tolist()
+    print(f"no-alloc limit: batch 16, max_seq {limit}", flush=True)
+    kp, vp, tables, q, k_new, v_new = _case(77, lens, n_head, n_kv, n_layer, stride)
+    nbytes = lib.crucible_attention_decode_workspace_bytes(len(lens), n_head, limit)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    k1, v1, o1 = _call(lib, lib.crucible_attention_decode_paged_append, dev, kp, vp, tables, q,
+                       k_new, v_new, lens, n_head, n_kv, n_layer, layer, stride, ws)
+    k2, v2, o2 = _call(lib, lib.crucible_attention_decode_paged_append_noalloc, dev, kp, vp,
+                       tables, q, k_new, v_new, lens, n_head, n_kv, n_layer, layer, stride)
+    assert np.array_equal(k2, k1) and np.array_equal(v2, v1)
+    assert np.array_equal(o2.view(np.uint32), o1.view(np.uint32))
+    want = oracle.attention_paged_rows(q.astype(np.float32), k2, v2, tables,
+                                       np.asarray(lens, np.int32), n_head=n_head, n_kv_head=n_kv,
+                                       head_dim=64, table_stride=stride, n_layer=n_layer,
+                                       layer=layer)
+    err = element_gate(o2, want, "no-alloc at the limit")
+    print(f"no-alloc limit: max-abs {err:.3e}", flush=True)
+    # one page more: 83 splits, refused (the same real buffers; nothing is launched)
+    stride2 = stride + 1
+    tab2 = np.zeros((16, stride2), np.int32)
+    tab2[:, :stride] = tables
+    d = {name: _dev(a, dev) for name, a in (("q", q), ("kn", k_new), ("vn", v_new), ("k", kp),
+                                            ("v", vp), ("t", tab2))}
+    d_len = _dev(np.asarray(lens, np.int32), dev)
+    d_pos = _dev(np.asarray(lens, np.int32) - 1, dev)
+    out = torch.zeros((16, n_head * 64), device=dev)
+    rc = lib.crucible_attention_decode_paged_append_noalloc(
+        d["q"].data_ptr(), _lib.F16, d["kn"].data_ptr(), d["vn"].data_ptr(), _lib.F32,
+        d["k"].data_ptr(), d["v"].data_ptr(), out.data_ptr(), _lib.F32, d["t"].data_ptr(),
+        d_pos.data_ptr(), d_len.data_ptr(), 16, n_head, n_kv, 64, stride2, n_layer, layer,
+        n_kv * 64, limit + 16, None)
+    assert rc == _lib.ERR_WORKSPACE and "static scratch" in _lib.last_error()[1]
 
 
 def test_noalloc_rejects_calls_past_the_scratch(dev):

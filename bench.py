@@ -522,7 +522,7 @@ def copy_bandwidth(dev, mib: int = 256, reps: int = 10):
     return 2 * (mib << 20) / (ms * 1e-3) / 1e9
 
 
-PHASES = ("prologue", "loads", "compute", "merge", "publish", "counter", "combine")
+PHASES = ("unit", "issue", "loads", "compute", "merge", "publish", "counter", "combine")
 
 
 def decode_phases(gpu, dev, args, log):
@@ -530,8 +530,9 @@ def decode_phases(gpu, dev, args, log):
 
     Each replay of a step graph runs the 12 layer launches back to back; the stamps left
     afterwards are those of the last one. Per workgroup, from its slots (StampSlot in
-    attn_decode.hip): start skew (entry against the launch's first entry), prologue (entry
-    to the lengths and page ids in and the K/V loads issued), loads (to wave 0's pages
+    attn_decode.hip): start skew (entry against the launch's first entry), unit (entry to
+    the workgroup's unit known: the plan entry and the lengths in, or the search done),
+    issue (to the page ids in and the K/V loads issued), loads (to wave 0's pages
     resident), compute (wave 0's products issued), merge (to every wave past the LDS
     merge), publish (partial acknowledged, or the output stored for a one-split unit),
     counter (split counter returned) and, for the combining workgroup, combine (output
@@ -575,36 +576,37 @@ def decode_phases(gpu, dev, args, log):
 
 def summarize_stamps(launches, us_per_tick: float) -> dict:
     """Phase durations (median, p90, max over workgroups and launches) from stamp rows of
-    one launch each (uint64 [rows][9]: StampSlot order, slot 8 the meta word), and the
+    one launch each (uint64 [rows][10]: StampSlot order, slot 9 the meta word), and the
     phases of each launch's last-finishing workgroup."""
     import numpy as np
 
     per = {k: [] for k in ("skew",) + PHASES + ("chain",)}
     crit = []
     n_wg = 0
+    n_all = len(PHASES)  # 8 phases between 9 time slots
     for buf in launches:
-        meta = buf[:, 8]
+        meta = buf[:, n_all + 1]
         kind = (meta >> np.uint64(52)) & np.uint64(0xF)
         n_active = ((meta >> np.uint64(32)) & np.uint64(0xFFFF)).astype(np.int64)
         last = ((meta >> np.uint64(48)) & np.uint64(1)).astype(bool)
-        att = (buf[:, 0] != 0) & (kind == 0) & (buf[:, 5] != 0)
+        att = (buf[:, 0] != 0) & (kind == 0) & (buf[:, n_all - 2] != 0)
         n_wg = int(att.sum())
-        t = buf[att, :8].astype(np.int64)
+        t = buf[att, :n_all + 1].astype(np.int64)
         multi = n_active[att] > 1
         comb = multi & last[att]
         t0 = t[:, 0].min()
-        # a one-split unit stops at slot 5, a non-combining split at slot 6 (later slots
-        # may hold an earlier launch's values)
-        end = np.where(comb, t[:, 7], np.where(multi, t[:, 6], t[:, 5]))
-        d = np.diff(t, axis=1) * us_per_tick  # slots 0..7 -> the 7 phases
+        # a one-split unit stops at the publish slot, a non-combining split at the counter
+        # slot (later slots may hold an earlier launch's values)
+        end = np.where(comb, t[:, n_all], np.where(multi, t[:, n_all - 1], t[:, n_all - 2]))
+        d = np.diff(t, axis=1) * us_per_tick  # slots 0..8 -> the 8 phases
         per["skew"] += list((t[:, 0] - t0) * us_per_tick)
-        for i, name in enumerate(PHASES[:5]):
+        for i, name in enumerate(PHASES[:n_all - 2]):
             per[name] += list(d[:, i])
-        per["counter"] += list(d[multi, 5])
-        per["combine"] += list(d[comb, 6])
+        per["counter"] += list(d[multi, n_all - 2])
+        per["combine"] += list(d[comb, n_all - 1])
         per["chain"].append(float((end.max() - t0) * us_per_tick))
         w = int(np.argmax(end))
-        n_ph = 7 if comb[w] else 6 if multi[w] else 5
+        n_ph = n_all if comb[w] else n_all - 1 if multi[w] else n_all - 2
         crit.append({"skew": round(float((t[w, 0] - t0) * us_per_tick), 2),
                      **{PHASES[i]: round(float(d[w, i]), 2) for i in range(n_ph)}})
     summary = {}

@@ -51,22 +51,19 @@ namespace crucible {
 namespace {
 
 struct DecodeArgs {
-    // The first 64 bytes hold everything the prologue needs (one scalar fetch).
-    const int32_t* tables;       // nullptr: contiguous cache (page = pos >> 4)
-    const int32_t* lens;         // request b's length is lens[b * lens_stride + lens_off]
-    const int32_t* positions;    // fused append: row b goes to position positions[b]
-    const void* q;
+    // The first 64 bytes hold what the prologue's unit check and first page loads need
+    // besides the preloaded arguments (one scalar fetch).
+    half_t* k_pool;              // written only by the fused append
+    half_t* v_pool;
+    PoolAddr addr;
     int32_t table_stride;
-    int32_t q_row_stride;        // elements between query rows (n_head * 64)
-    int lens_stride;             // 1: per-request lengths; 0: one length in params
-    int lens_off;                // 0, or CRUCIBLE_PARAM_SEQ for a params buffer
     int max_pages;               // ceil(max_seq / 16) <= table_stride
     int split_shift;             // a split covers 1 << split_shift pages
     int max_seq;
+    int n_kv_head;
     int n_rep;
     // the rest
-    half_t* k_pool;              // written only by the fused append
-    half_t* v_pool;
+    const void* q;
     void* out;
     const void* k_new;           // fused append: [batch][kv_dim] rows (f32 or fp16)
     const void* v_new;
@@ -75,12 +72,9 @@ struct DecodeArgs {
     float* pl;                   // [batch][n_head][n_splits]
     uint32_t* counters;          // [batch * n_kv_head] x counter_stride; nullptr: combine in a second kernel
     int counter_stride;          // u32 between two units' counters (kCounterPad where they fit)
-    int32_t* plan;               // compact order's unit plan (kPlanUnits entries); nullptr: none
-    PoolAddr addr;
+    int32_t q_row_stride;        // elements between query rows (n_head * 64)
     uint32_t po_bytes;           // size of po (buffer-resource bound)
     int kv_new_f16;
-    int n_kv_head;
-    int batch;
     int n_head;
     int n_splits;
     int out_f16;
@@ -91,6 +85,15 @@ struct DecodeArgs {
     int rope_max_pos;
     int kv_new_stride;           // elements between k_new (and v_new) rows
     int out_row_stride;          // elements between output rows (n_head * 64)
+    // Passed to decode_kernel again as its leading (preloaded) arguments, which the kernel
+    // copies over these: kept last, so that no scalar fetch of the fields above carries them.
+    int lens_stride;             // 1: per-request lengths; 0: one length in params
+    int lens_off;                // 0, or CRUCIBLE_PARAM_SEQ for a params buffer
+    int batch;
+    const int32_t* tables;       // nullptr: contiguous cache (page = pos >> 4)
+    const int32_t* lens;         // request b's length is lens[b * lens_stride + lens_off]
+    const int32_t* positions;    // fused append: row b goes to position positions[b]
+    int32_t* plan;               // compact order's unit plan (kPlanUnits entries); nullptr: none
 };
 
 
@@ -106,7 +109,8 @@ struct DecodeArgs {
 constexpr int kStampRows = 8192;
 enum StampSlot {
     kStampStart,      // kernel entry
-    kStampPrologue,   // lengths and page ids in, the wave's K/V loads issued
+    kStampUnit,       // the workgroup's unit known (plan entry and lengths in, or searched)
+    kStampPrologue,   // page ids in, the wave's K/V loads issued
     kStampLoads,      // wave 0's K/V pages resident
     kStampCompute,    // wave 0's QK, softmax and PV products issued
     kStampMerged,     // every wave past the LDS merge barrier
@@ -132,7 +136,8 @@ __device__ __forceinline__ void stamp_now(int slot) {
 }
 
 __device__ __forceinline__ void stamp_after(int slot) {
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    // only thread 0's wave stores stamps; the other waves do not wait
+    if (threadIdx.x < 64) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     stamp_now(slot);
 }
 
@@ -736,6 +741,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(
         if constexpr (APPEND) asm volatile("" : "+s"(pos));
         len = lr < a.max_seq ? lr : a.max_seq;  // never index past the table
     }
+    CRUCIBLE_STAMP_NOW(kStampUnit);
     u_begin = s << a.split_shift;
     u_end = u_begin + (1 << a.split_shift);
     const int bg = b * a.n_kv_head + g;

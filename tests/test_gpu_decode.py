@@ -669,3 +669,4 @@ def test_cached_workspace_is_zeroed_when_the_pools_change(gpu, dev):
     k2 = torch.zeros(4096, dtype=torch.float16, device=dev)
     gpu.workspace(batch, n_head, max_seq, (k2, v1[:2048]))
     assert int(ws.sum()) == 0  # another address: zeroed
+

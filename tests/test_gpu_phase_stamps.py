@@ -39,9 +39,9 @@ def _twin_gpu():
 
 def _read(rd, rows=8192, clear=0):
     khz, slots = ctypes.c_int(0), ctypes.c_int(0)
-    buf = np.zeros((rows, 9), np.uint64)
+    buf = np.zeros((rows, 10), np.uint64)
     assert rd(buf.ctypes.data, rows, clear, ctypes.byref(khz), ctypes.byref(slots)) == 0
-    assert slots.value == 9 and khz.value > 0
+    assert slots.value == 10 and khz.value > 0
     return buf
 
 
@@ -87,22 +87,22 @@ def test_stamped_twin_matches_product_and_stamps_are_ordered(dev, gpu):
         assert torch.equal(a.view(bits), b.view(bits)), f"{what} differs from the product's"
 
     st = _read(rd)
-    meta = st[:, 8]
+    meta = st[:, 9]
     kind = (meta >> np.uint64(52)) & np.uint64(0xF)
-    att = (st[:, 0] != 0) & (kind == 0) & (st[:, 5] != 0)
+    att = (st[:, 0] != 0) & (kind == 0) & (st[:, 6] != 0)
     t = st[att].astype(np.int64)
-    n_active = (t[:, 8] >> 32) & 0xFFFF
-    last = ((t[:, 8] >> 48) & 1).astype(bool)
-    b_of = t[:, 8] & 0xFFFF
-    g_of = (t[:, 8] >> 16) & 0xFF
+    n_active = (t[:, 9] >> 32) & 0xFFFF
+    last = ((t[:, 9] >> 48) & 1).astype(bool)
+    b_of = t[:, 9] & 0xFFFF
+    g_of = (t[:, 9] >> 16) & 0xFF
     # one attending workgroup per (request, kv head, active split)
     pages = -(-lens.astype(np.int64) // 16)
     splits = -(-pages // 16)  # 16-page splits of the config-3 shape
     assert att.sum() == n_kv * int(splits.sum())
     assert np.all(b_of < batch) and np.all(g_of < n_kv)
-    assert np.all(np.diff(t[:, :6], axis=1) >= 0), "phases 0..5 out of order"
+    assert np.all(np.diff(t[:, :7], axis=1) >= 0), "phases 0..6 out of order"
     multi = n_active > 1
-    assert np.all(t[multi, 6] >= t[multi, 5])
+    assert np.all(t[multi, 7] >= t[multi, 6])
     comb = multi & last
     assert comb.sum() == n_kv * int((splits > 1).sum())  # one combining split per unit
-    assert np.all(t[comb, 7] >= t[comb, 6])
+    assert np.all(t[comb, 8] >= t[comb, 7])

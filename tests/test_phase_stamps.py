@@ -30,32 +30,34 @@ def test_stamped_twin_exports_the_header_and_the_reader():
 
 
 def _row(t0, phases, b, g, s, n_active, last):
-    """Stamp slots from an entry time and phase lengths (ticks); slot 8 the meta word."""
-    row = np.zeros(9, np.uint64)
+    """Stamp slots from an entry time and phase lengths (ticks); slot 9 the meta word."""
+    row = np.zeros(10, np.uint64)
     row[0] = t0
     t = t0
     for i, dt in enumerate(phases):
         t += dt
         row[i + 1] = t
-    row[8] = (b | g << 16 | s << 24 | n_active << 32 | last << 48)
+    row[9] = (b | g << 16 | s << 24 | n_active << 32 | last << 48)
     return row
 
 
 def test_summarize_stamps_recovers_known_phases():
     # unit (0, 0) in two splits, split 1 combines; unit (1, 0) in one split; one row of a
-    # workgroup with no unit (kind 2) and one zero row, both ignored
-    rows = np.zeros((16, 9), np.uint64)
-    rows[0] = _row(1000, [50, 100, 20, 30, 80, 40], 0, 0, 0, 2, 0)
-    rows[1] = _row(1010, [60, 90, 20, 40, 80, 50, 70], 0, 0, 1, 2, 1)
-    rows[2] = _row(1005, [40, 120, 10, 20, 60], 1, 0, 0, 1, 1)
-    rows[2, 6:8] = 999_999  # an earlier launch's slots beyond a one-split unit's last
+    # workgroup with no unit (kind 2) and one zero row, both ignored. Phases in order:
+    # unit, issue, loads, compute, merge, publish, counter, combine.
+    rows = np.zeros((16, 10), np.uint64)
+    rows[0] = _row(1000, [20, 30, 100, 20, 30, 80, 40], 0, 0, 0, 2, 0)
+    rows[1] = _row(1010, [25, 35, 90, 20, 40, 80, 50, 70], 0, 0, 1, 2, 1)
+    rows[2] = _row(1005, [15, 25, 120, 10, 20, 60], 1, 0, 0, 1, 1)
+    rows[2, 7:9] = 999_999  # an earlier launch's slots beyond a one-split unit's last
     rows[3, 0] = 1000
-    rows[3, 8] = 2 << 52
+    rows[3, 9] = 2 << 52
     out = bench.summarize_stamps([rows], us_per_tick=0.01)
     ph = out["phases"]
     assert out["workgroups_per_launch"] == 3
     assert ph["skew"]["max_us"] == pytest.approx(0.10)
-    assert ph["prologue"]["median_us"] == pytest.approx(0.50)
+    assert ph["unit"]["median_us"] == pytest.approx(0.20)
+    assert ph["issue"]["median_us"] == pytest.approx(0.30)
     assert ph["loads"]["max_us"] == pytest.approx(1.20)
     assert ph["counter"]["n"] == 2 and ph["counter"]["max_us"] == pytest.approx(0.50)
     assert ph["combine"]["n"] == 1 and ph["combine"]["median_us"] == pytest.approx(0.70)

@@ -115,9 +115,10 @@ def parse_args():
                         "default set)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run 5 more plain 256 MiB device copies (PMC traffic calibration)")
-    p.add_argument("--phases", nargs="?", const="decode", choices=("decode", "config4"),
-                   help="diagnostic: run config 3 (decode, the default) or config 4 (the "
-                        "16-row LDS prefill) on the stamped twin of the library "
+    p.add_argument("--phases", nargs="?", const="decode", choices=("decode", "config4", "config1"),
+                   help="diagnostic: run config 3 (decode, the default), config 4 (the "
+                        "16-row LDS prefill) or config 1 (the register-direct prefill) on the "
+                        "stamped twin of the library "
                         "(libcrucible_attn_stamps.so) and print where a launch's time goes, "
                         "per phase, instead of the bench line")
     p.add_argument("--phase-reps", type=int, default=28,
@@ -406,7 +407,7 @@ def bench_prefill(gpu, dev, cfg, launches: int = 50, q_dtype=None, cpu_inputs=No
 
 # ---------------------------------------------------------------- end to end (config 5)
 
-def bench_e2e(gpu, reps: int = 2):
+def bench_e2e(gpu, reps: int = 3):
     """random-init 120m preset, 16 prompts of U[64, 512] seeded token
     ids, 256 greedy tokens each, decode steps replayed from one HIP graph. tok/s counts the
     decode loop only (16 x 255 steps after the prefill's first token). The greedy tokens
@@ -422,12 +423,17 @@ def bench_e2e(gpu, reps: int = 2):
         timing = {}
         model.generate(prompts, 256, timing=timing)
         runs.append(timing)
-    t = runs[-1]  # the first run also pays for graph capture
+    # decode_ms times the graph replays of the decode loop (captured once per generate call;
+    # a server captures once per process), events on the replay stream; the median run
+    t = sorted(runs, key=lambda r: r["decode_ms"])[len(runs) // 2]
     tok_s = 16 * t["decode_steps"] / (t["decode_ms"] * 1e-3)
     return {"workload": "config5 greedy decode, random-init 120m (12 layers, 12/3 heads, "
                         "vocab 50257), b16, prompts U[64,512], 256 tokens",
             "tok_per_s": round(tok_s, 1), "ms_per_step": round(t["decode_ms"] / t["decode_steps"], 4),
             "prefill_ms": round(t["prefill_ms"], 3), "decode_steps": t["decode_steps"],
+            "runs": len(runs), "ms_per_step_runs": [round(r["decode_ms"] / r["decode_steps"], 4)
+                                                    for r in runs],
+            "capture_ms": round(t["capture_ms"], 2),
             "precision": "reference (f64-accumulated projections)",
             "reference_published_tok_per_s": 8366}
 
@@ -623,14 +629,16 @@ PREFILL_PHASES = ("rows", "first_pair", "loop", "merge", "write")
 
 
 def prefill_phases(gpu, dev, args, log):
-    """Per-workgroup phase stamps of config 4's prefill launch (the 16-row LDS kernel on the
-    stamped library). A graph of 12 back-to-back launches is replayed; the stamps left are
-    the last launch's. Per workgroup with rows (slots of PStampSlot in attn_prefill.hip):
-    start skew, rows (entry to the tile's rows resolved), first_pair (to the first pair of
-    key tiles in LDS: page ids, tile loads and query loads), loop (the rest of the tile
-    loop), merge (key halves merged), write (output stored), and `wait`, the part of
-    first_pair + loop its wave spent waiting for key tiles. Reported over all workgroups and
-    over the heaviest (most tile pairs), whose chain bounds the launch."""
+    """Per-workgroup phase stamps of a prefill launch on the stamped library: config 4 (the
+    16-row LDS kernel) or config 1 (the register-direct kernel). A graph of 12 back-to-back
+    launches is replayed; the stamps left are the last launch's. Per workgroup with rows
+    (slots of PStampSlot in attn_prefill.hip): start skew, rows (entry to the tile's rows
+    resolved; direct form: and the query loads issued), first_pair (LDS form: to the first
+    pair of key tiles in LDS, page ids, tile loads and query loads; direct form: to wave 0's
+    first key tile in registers), loop (the rest of the tile loop), merge (the states
+    merged), write (output stored), and `wait`, the part of first_pair + loop the LDS form's
+    wave spent waiting for key tiles (0 in the direct form). Reported over all workgroups
+    and over the heaviest (most tile pairs, resp. key tiles), whose chain bounds the launch."""
     import ctypes
 
     import numpy as np
@@ -647,7 +655,8 @@ def prefill_phases(gpu, dev, args, log):
     _lib.check(fn(None, 0, 1, ctypes.byref(khz), ctypes.byref(slots)))
     rows = 8192
     buf = np.zeros((rows, slots.value), np.uint64)
-    cfg = W.config4_packed()
+    direct = args.phases == "config1"
+    cfg = W.config1_prefill(n_kv_head=12) if direct else W.config4_packed()
     timing = bench_prefill(gpu, dev, cfg, launches=12)
     log(f"stamped build: {timing['us_per_launch']} us per launch (graph replay)")
     run = prefill_runner(gpu, dev, cfg)[0]
@@ -696,7 +705,10 @@ def prefill_phases(gpu, dev, args, log):
                       "max_us": round(float(a.max()), 3), "n": int(a.size)}
         return out
 
-    return {"kernel": "prefill_kernel<4, 1, false, 4, true>", "workload": cfg.name,
+    p16 = "true" if timing["p_operand"].startswith("one") else "false"
+    kernel = (f"prefill_direct_kernel<false, false, {p16}>" if direct
+              else f"prefill_kernel<4, 1, false, 4, {p16}>")
+    return {"kernel": kernel, "workload": cfg.name,
             "clock_khz": khz.value, "stamped_us_per_launch": timing["us_per_launch"],
             "launches_read": args.phase_reps, "workgroups_per_launch": n_wg,
             "max_pairs": int(pairs.max()), "phases": stats(per), "heaviest": stats(heavy)}

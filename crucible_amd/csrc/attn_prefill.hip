@@ -94,7 +94,19 @@ __device__ __forceinline__ uint64_t pstamp_clock() {
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); \
         pstamp_store(slot, pstamp_clock());                          \
     } while (0)
+// The register-direct kernel (prefill_direct_kernel) uses the same rows, with slots
+// kPRows = rows resolved and the query and first key tile's loads issued, kPFirst = wave
+// 0's first key tile resident, kPLoop = wave 0's key tiles done, kPMerged = the waves'
+// states merged (after the barrier), kPWritten = output stored; kPWait is 0 and the meta
+// word's top field the row tile's number of key tiles. Only wave 0 waits for its memory
+// operations at a stamp, so the other waves' loads stay in flight as in the product.
+#define CRUCIBLE_PSTAMP_AFTER_W0(slot)                                      \
+    do {                                                                    \
+        if (threadIdx.x < 64) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); \
+        pstamp_store(slot, pstamp_clock());                                 \
+    } while (0)
 #else
+#define CRUCIBLE_PSTAMP_AFTER_W0(slot) ((void)0)
 #define CRUCIBLE_PSTAMP_CLOCK() uint64_t(0)
 #define CRUCIBLE_PSTAMP(slot, v) ((void)0)
 #define CRUCIBLE_PSTAMP_AFTER(slot) ((void)0)
@@ -1193,6 +1205,7 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
     const int lane = tid & 63;
     const int col = lane & 15;
     const int grp = lane >> 4;
+    [[maybe_unused]] const uint64_t t_entry = CRUCIBLE_PSTAMP_CLOCK();
     const WgPos wp = wg_pos(a);
     const int h = wp.x;
     const int g = h / a.n_rep;
@@ -1266,6 +1279,10 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
         }
     }
 
+    CRUCIBLE_PSTAMP(kPStart, t_entry);
+    CRUCIBLE_PSTAMP(kPRows, CRUCIBLE_PSTAMP_CLOCK());
+    [[maybe_unused]] bool first_tile_stamp = true;
+    [[maybe_unused]] int stamp_tiles = 0;
     float m = -INFINITY, l = 0.0f;
     float4_t acc[4] = {};
     const int kv_dim = a.addr.kv_dim;
@@ -1301,6 +1318,9 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
                                      : nullptr;
         const int n_tiles = (hist_end + kKeyTile - 1) / kKeyTile;
         const int last_page = (hist_end - 1) >> kPageShift;
+#ifdef CRUCIBLE_STAMPS
+        stamp_tiles = max(stamp_tiles, n_tiles);
+#endif
 
         for (int t = wave; t < n_tiles; t += kDirectWaves) {
             const int kbase = t * kKeyTile;
@@ -1376,6 +1396,12 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
                             }
             }
 
+#ifdef CRUCIBLE_STAMPS
+            if (first_tile_stamp) {
+                CRUCIBLE_PSTAMP_AFTER_W0(kPFirst);
+                first_tile_stamp = false;
+            }
+#endif
             float4_t st[4];
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
@@ -1428,6 +1454,7 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
 
     // ---- merge the 8 waves' states (per column: m, l summed over the lane groups)
     l = group_sum4(l);
+    CRUCIBLE_PSTAMP_AFTER_W0(kPLoop);
     if (grp == 0) {
         s_m[wave][col] = m;
         s_l[wave][col] = l;
@@ -1435,6 +1462,13 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
 #pragma unroll
     for (int db = 0; db < 4; ++db) s_acc[wave][db][lane] = acc[db];
     __syncthreads();
+    CRUCIBLE_PSTAMP(kPMerged, CRUCIBLE_PSTAMP_CLOCK());
+#ifdef CRUCIBLE_STAMPS
+    CRUCIBLE_PSTAMP(kPWait, 0);
+    CRUCIBLE_PSTAMP(kPMeta, (uint64_t)(wp.tile & 0xffff) | (uint64_t)(wp.req & 0xffff) << 16 |
+                                (uint64_t)(wp.x & 0xffff) << 32 |
+                                (uint64_t)(stamp_tiles & 0xffff) << 48);
+#endif
     if (wave >= 4 || my_row < 0) return;
     const int db = wave;  // waves 0..3 each finish one 16-dim block
     float M = -INFINITY;
@@ -1459,6 +1493,7 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
     } else {
         *reinterpret_cast<float4_t*>(static_cast<float*>(a.out) + off) = o;
     }
+    CRUCIBLE_PSTAMP_AFTER_W0(kPWritten);
 }
 
 int heads_per_wg(int n_rep) { return (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1; }

@@ -32,6 +32,7 @@ tables do not change while the decode graph replays.
 from __future__ import annotations
 
 import math
+import time
 from dataclasses import dataclass
 
 import numpy as np
@@ -402,7 +403,7 @@ class GpuModel:
         seqs, tables = self._admit(prompts, n_new)
         try:
             d_tables = torch.from_numpy(tables).to(dev)
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
             ev[0].record()
             first, _ = self.prefill(prompts, d_tables)
             ev[1].record()
@@ -426,19 +427,25 @@ class GpuModel:
             if self.precision == "reference":  # the first step's input row
                 torch.index_select(self.tok_emb, 0, st["tokens"], out=st["x"])
             steps = n_new - 1
+            capture_s = 0.0
             if steps > 0 and graph:
-                g = self._capture(st)
+                t0 = time.perf_counter()
+                g = self._capture(st)  # once per call here; once per process in a server
+                capture_s = time.perf_counter() - t0
+                ev[2].record()  # the decode loop: the replays only
                 for _ in range(steps):
                     g.replay()
             else:
+                ev[2].record()
                 for _ in range(steps):
                     self._decode_step(st)
-            ev[2].record()
+            ev[3].record()
             torch.cuda.synchronize(dev)
             if timing is not None:
                 timing["prefill_ms"] = ev[0].elapsed_time(ev[1])
-                timing["decode_ms"] = ev[1].elapsed_time(ev[2])
+                timing["decode_ms"] = ev[2].elapsed_time(ev[3])
                 timing["decode_steps"] = steps
+                timing["capture_ms"] = capture_s * 1e3
             out = np.empty((batch, n_new), np.int32)
             out[:, 0] = first.cpu().numpy()
             if steps > 0:

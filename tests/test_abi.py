@@ -1,6 +1,7 @@
 """The C-ABI library loads, exports every symbol include/crucible_attn.h declares, and
 rejects invalid arguments before launching anything (no GPU needed for these calls)."""
 import ctypes
+import os
 import re
 
 import pytest
@@ -196,3 +197,19 @@ def test_tuning_overrides_are_validated_and_restorable():
         set_tuning(prefill_bufs=5)
     with pytest.raises(_lib.CrucibleError):
         set_tuning(no_such_key=1)
+
+
+def test_native_caller_compiles_and_links(tmp_path):
+    """tests/native_step.cpp, the native caller of the ABI, builds against the header, the
+    library and the oracle (host compile only; tests/test_gpu_native_caller.py runs it)."""
+    import subprocess
+
+    import native_build
+
+    out = str(tmp_path / "native_step")
+    native_build.build(out)
+    assert os.path.exists(out)
+    nm = subprocess.run(["nm", "-D", "--undefined-only", out], capture_output=True, text=True)
+    for sym in ("crucible_attention_decode_paged_append", "crucible_attention_prefill_tiled",
+                "crucible_cache_store_packed_paged", "orc_attention_paged_rows"):
+        assert sym in nm.stdout, sym

@@ -311,7 +311,7 @@ def gather_rows(pool, table_row, n, n_layer, layer, kv_dim, v_kind):
 
 def prefill_runner(gpu, dev, cfg, q_dtype=None):
     """Device inputs of a prefill config and a closure that launches its segment-form
-    prefill once; returns (run, q, k_pool, v_pool, tables)."""
+    prefill once (its output tensor is run.out); returns (run, q, k_pool, v_pool, tables)."""
     import numpy as np
     import torch
 
@@ -335,6 +335,7 @@ def prefill_runner(gpu, dev, cfg, q_dtype=None):
                                     len(cfg.seq_lens), max_chunk, stride, cfg.n_head,
                                     cfg.n_kv_head, 64, 1, 0, kv_dim)
 
+    run.out = out  # the output rows the launch writes
     return run, q, k_pool, v_pool, d_tab
 
 

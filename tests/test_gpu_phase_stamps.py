@@ -106,3 +106,49 @@ def test_stamped_twin_matches_product_and_stamps_are_ordered(dev, gpu):
     comb = multi & last
     assert comb.sum() == n_kv * int((splits > 1).sum())  # one combining split per unit
     assert np.all(t[comb, 8] >= t[comb, 7])
+
+
+def _read_prefill(twin_lib, rows=8192, clear=0):
+    rd = twin_lib.crucible_debug_prefill_stamps
+    rd.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                   ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]
+    rd.restype = ctypes.c_int
+    khz, slots = ctypes.c_int(0), ctypes.c_int(0)
+    buf = np.zeros((rows, 8), np.uint64)
+    if clear:
+        assert rd(None, 0, 1, ctypes.byref(khz), ctypes.byref(slots)) == 0
+    else:
+        assert rd(buf.ctypes.data, rows, 0, ctypes.byref(khz), ctypes.byref(slots)) == 0
+        assert slots.value == 8 and khz.value > 0
+    return buf
+
+
+@pytest.mark.parametrize("direct", [1, 0], ids=["direct", "lds"])
+def test_stamped_twin_prefill_matches_product(dev, gpu, tune, direct):
+    """The register-direct (config-1 shape) and LDS-tiled (config-4 shape) prefill kernels of
+    the stamped twin give the product's bits, and their stamps run forward: entry <= rows <=
+    first key tile <= loop end <= merge (and the write for the direct form)."""
+    if not os.path.exists(_build.STAMPS_LIB_PATH):
+        pytest.skip("stamped library not built")
+    from crucible_amd import workloads as W
+    import bench
+
+    tune(prefill_direct=direct)
+    twin, _ = _twin_gpu()
+    cfg = W.config1_prefill(n_kv_head=12) if direct else W.config4_packed()
+    outs = []
+    for g_run in (gpu, twin):
+        run = bench.prefill_runner(g_run, dev, cfg)[0]
+        if g_run is twin:
+            _read_prefill(twin.lib, clear=1)
+        run()
+        torch.cuda.synchronize()
+        outs.append(run.out.cpu().clone())
+    assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32))
+    st = _read_prefill(twin.lib)
+    live = (st[:, 0] != 0) & (st[:, 5] != 0)
+    assert live.sum() > 0
+    t = st[live].astype(np.int64)
+    assert np.all(np.diff(t[:, :5], axis=1) >= 0), "entry, rows, first tile, loop, merge out of order"
+    if direct:
+        assert np.all(t[:, 5] >= t[:, 4])

@@ -61,6 +61,7 @@ constexpr TuneKey kTuneKeys[CRUCIBLE_TUNE_COUNT] = {
     {"CRUCIBLE_DECODE_COMBINE_WIDTH", 8, 16}, // splits merged per round trip: 8 or 16
     {"CRUCIBLE_PREFILL_P16", 0, 1},           // prefill P operand: fp16 hi + lo / one fp16
     {"CRUCIBLE_PREFILL_M32", 0, 1},           // prefill 32-row waves on 32x32 MFMAs off / on
+    {"CRUCIBLE_PREFILL_PERSIST", 0, 65536},   // prefill persistent LDS form off / on / n workgroups
 };
 
 bool tune_value_ok(int key, int v) {

@@ -40,6 +40,7 @@
 #include "generic_attend.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <type_traits>
@@ -60,9 +61,11 @@ constexpr int kThreads = 512;  // 8 waves: 4 row/head slots x 2 tile parities
 #ifdef CRUCIBLE_STAMPS
 // Phase stamps of the 16-row LDS kernel (prefill_kernel), compiled only into the
 // diagnostic libcrucible_attn_stamps.so. Thread 0 of each workgroup (wave 0: key half 0 of
-// the first slot) records s_memrealtime at the end of each phase in row `workgroup id`,
-// and the time its wave spent in the tile loop's waits for key tiles (the wait for its own
-// tile loads plus the barrier that makes every wave's loads visible).
+// the first slot) records s_memrealtime at the end of each phase in row `workgroup id`
+// (in the persistent form, the tile's list position; a tile's kPStart is then the time its
+// workgroup began it: the kernel's entry for its first tile), and the time its wave spent
+// in the tile loop's waits for key tiles (the wait for its own tile loads plus the barrier
+// that makes every wave's loads visible).
 constexpr int kPStampRows = 8192;
 enum PStampSlot {
     kPStart,      // kernel entry
@@ -80,19 +83,19 @@ __device__ uint64_t g_prefill_stamps[kPStampRows][kPSlots];
 __device__ __forceinline__ unsigned pstamp_row() {
     return blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
 }
-__device__ __forceinline__ void pstamp_store(int slot, uint64_t v) {
-    if (threadIdx.x == 0 && pstamp_row() < kPStampRows) g_prefill_stamps[pstamp_row()][slot] = v;
+__device__ __forceinline__ void pstamp_store(unsigned row, int slot, uint64_t v) {
+    if (threadIdx.x == 0 && row < kPStampRows) g_prefill_stamps[row][slot] = v;
 }
 __device__ __forceinline__ uint64_t pstamp_clock() {
     asm volatile("" ::: "memory");
     return __builtin_amdgcn_s_memrealtime();
 }
 #define CRUCIBLE_PSTAMP_CLOCK() pstamp_clock()
-#define CRUCIBLE_PSTAMP(slot, v) pstamp_store(slot, v)
+#define CRUCIBLE_PSTAMP(slot, v) pstamp_store(pstamp_id, slot, v)
 #define CRUCIBLE_PSTAMP_AFTER(slot)                                  \
     do {                                                             \
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); \
-        pstamp_store(slot, pstamp_clock());                          \
+        pstamp_store(pstamp_id, slot, pstamp_clock());               \
     } while (0)
 // The register-direct kernel (prefill_direct_kernel) uses the same rows, with slots
 // kPRows = rows resolved and the query and first key tile's loads issued, kPFirst = wave
@@ -103,9 +106,10 @@ __device__ __forceinline__ uint64_t pstamp_clock() {
 #define CRUCIBLE_PSTAMP_AFTER_W0(slot)                                      \
     do {                                                                    \
         if (threadIdx.x < 64) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); \
-        pstamp_store(slot, pstamp_clock());                                 \
+        pstamp_store(pstamp_id, slot, pstamp_clock());                      \
     } while (0)
 #else
+__device__ __forceinline__ unsigned pstamp_row() { return 0; }
 #define CRUCIBLE_PSTAMP_AFTER_W0(slot) ((void)0)
 #define CRUCIBLE_PSTAMP_CLOCK() uint64_t(0)
 #define CRUCIBLE_PSTAMP(slot, v) ((void)0)
@@ -302,15 +306,20 @@ struct WgPos {
     int64_t req;
 };
 
-__device__ __forceinline__ WgPos wg_pos(const PrefillArgs& a) {
-    if (!a.heavy_first) return {(int)blockIdx.x, (int64_t)blockIdx.y, (int64_t)blockIdx.z};
-    // 32-bit arithmetic: the launcher keeps the grid below 2^31 workgroups
+// Longest-first id -> (x, row tile, request).
+__device__ __forceinline__ WgPos wg_pos(const PrefillArgs& a, uint32_t id) {
+    // 32-bit arithmetic: the launcher keeps the ids below 2^31
     const uint32_t per_level = (uint32_t)a.grid_x * (uint32_t)a.grid_reqs;
-    const uint32_t level = blockIdx.x / per_level;
+    const uint32_t level = id / per_level;
     const uint32_t rem =
-        (uint32_t)(((uint64_t)(blockIdx.x - level * per_level) + (uint64_t)level * a.grid_x) % per_level);
+        (uint32_t)(((uint64_t)(id - level * per_level) + (uint64_t)level * a.grid_x) % per_level);
     return {(int)(rem % (uint32_t)a.grid_x), (int64_t)a.grid_tiles - 1 - level,
             (int64_t)(rem / (uint32_t)a.grid_x)};
+}
+
+__device__ __forceinline__ WgPos wg_pos(const PrefillArgs& a) {
+    if (!a.heavy_first) return {(int)blockIdx.x, (int64_t)blockIdx.y, (int64_t)blockIdx.z};
+    return wg_pos(a, blockIdx.x);
 }
 
 // Row `local` of the grid tile: its packed row (-1 = none), owner (table) and absolute
@@ -341,18 +350,101 @@ __device__ __forceinline__ void tile_row(const PrefillArgs& a, int64_t req, int6
     if (pos < 0 || pos >= a.max_seq) row = -1;  // outside the table: never read
 }
 
+// The persistent form's list of row tiles with rows, longest-first: level v (row tile
+// grid_tiles - 1 - v) of every request that has that tile, in request order, x fastest
+// within a request. Request r has n_r = min(ceil(len_r / R), grid_tiles) tiles, the
+// non-persistent grid's coverage, so it holds levels grid_tiles - n_r .. grid_tiles - 1,
+// and every level from the first one held (start) on holds at least one request. The
+// launcher keeps grid_tiles <= 64, so one lane per level holds the list position where
+// that level begins.
+struct CompactList {
+    int4 seg;          // lane r < grid_reqs: segment r
+    int first_level;   // lane r: grid_tiles - n_r
+    int start;         // first level any request holds
+    int span;          // levels held: grid_tiles - start
+    uint32_t begin;    // lane i < span: list position of level start + i's first tile
+    uint32_t n_list;   // tiles in the list
+};
+
+// Wave 0 alone loads the segments (every wave of every workgroup reading the same few
+// lines would queue on one L2 channel) and hands them to the other waves through s_seg.
+// The sums and the minimum over the requests are scalar loops over readlane (no LDS
+// round trips).
+template <int R>
+__device__ __forceinline__ CompactList compact_list(const PrefillArgs& a, int wave, int lane,
+                                                    int4* s_seg) {
+    CompactList c;
+    typedef const __attribute__((address_space(1))) int32_t* global_i32_ptr;
+    global_i32_ptr segs = (global_i32_ptr)a.segments;
+    int n_req = a.grid_reqs;
+    asm volatile("" : "+s"(segs), "+s"(n_req));  // both kernel arguments load together
+    if (wave == 0 && lane < n_req) {
+        const global_i32_ptr sp = segs + 4 * lane;
+        s_seg[lane] = int4{sp[0], sp[1], sp[2], sp[3]};
+    }
+    __syncthreads();
+    c.seg = lane < n_req ? s_seg[lane] : int4{0, 0, 0, 0};
+    const int len = c.seg.y;
+    const int n = len > 0 ? min((len + R - 1) / R, a.grid_tiles) : 0;
+    c.first_level = a.grid_tiles - n;
+    int lo = a.grid_tiles;
+    uint32_t total = 0;
+    for (int r = 0; r < n_req; ++r) {
+        const int f = __builtin_amdgcn_readlane(c.first_level, r);
+        lo = min(lo, f);
+        total += (uint32_t)(a.grid_tiles - f);
+    }
+    c.start = lo;
+    c.span = a.grid_tiles - lo;
+    c.n_list = total * (uint32_t)a.grid_x;
+    // tiles at levels below start + lane: request r holds max(0, start + lane - first_r)
+    // of them (grid_x each)
+    uint32_t below = 0;
+    for (int r = 0; r < n_req; ++r)
+        below += (uint32_t)max(0, lo + lane - __builtin_amdgcn_readlane(c.first_level, r));
+    c.begin = below * (uint32_t)a.grid_x;
+    return c;
+}
+
+// (x, row tile, request) at list position k < n_list: the level is the last one that
+// begins at or before k (begin grows strictly with the level), then the (j / grid_x)-th
+// request holding that level.
+__device__ __forceinline__ WgPos compact_pos(const PrefillArgs& a, const CompactList& c,
+                                             uint32_t k, int lane) {
+    const uint32_t gx = (uint32_t)a.grid_x;
+    const uint64_t started = __ballot(lane < c.span && c.begin <= k);
+    const int li = __builtin_popcountll(started) - 1;  // level start + li (begin[0] = 0)
+    const int v = c.start + li;
+    const uint32_t j = k - (uint32_t)__builtin_amdgcn_readlane((int)c.begin, li);
+    const uint64_t held = __ballot(lane < a.grid_reqs && c.first_level <= v);
+    const uint32_t nth = j / gx;
+    const uint32_t before = __builtin_amdgcn_mbcnt_hi(
+        (uint32_t)(held >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)held, 0u));
+    const uint64_t pick = __ballot(((held >> lane) & 1) && before == nth);
+    // (k < n_list always finds one; a position past it would get row tile -1: no rows)
+    if (pick == 0 || li < 0 || v >= a.grid_tiles) return {0, -1, 0};
+    return {(int)(j - nth * gx), (int64_t)a.grid_tiles - 1 - v, (int64_t)__builtin_ctzll(pick)};
+}
+
 // `tables` is passed on its own, read-only and unaliased, so the page-id loads of the
 // tile loop compile to scalar loads (lgkmcnt) that never wait on the in-flight tiles.
 // KB: LDS ring depth in key tiles (4 or 6): KB / 2 - 1 pairs of tiles load ahead.
 // P16: P as one fp16 operand (tile_p), one PV MFMA per dim block and key half.
-template <int HPW, int QB, bool QF32, int KB, bool P16>
+// PERSIST (segment rows, at most 64 requests and 64 row tiles a request): the grid is the
+// resident workgroups, not the tiles. Each workgroup loads all the segments once and from
+// their lengths lists the row tiles that hold rows, in the longest-first order
+// (compact_list, compact_pos); workgroup w of G then serves list positions w, 2G - 1 - w,
+// 2G + w, 4G - 1 - w, ... (each round in the other direction, so the workgroups with the
+// heaviest tiles of one round get the lightest of the next, or none). Tiles without rows
+// cost nothing, no workgroup waits for a free slot, and nothing is shared between
+// workgroups. Every tile's arithmetic is the non-persistent kernel's, so the outputs are
+// the same bits.
+template <int HPW, int QB, bool QF32, int KB, bool P16, bool PERSIST>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
                                                       const int32_t* __restrict__ tables) {
     constexpr int RS = 4 / HPW;          // row slices per workgroup
     constexpr int WROWS = 16 * QB;       // rows per wave
     constexpr int R = RS * WROWS;        // rows per workgroup
-    [[maybe_unused]] const uint64_t t_entry = CRUCIBLE_PSTAMP_CLOCK();
-    [[maybe_unused]] uint64_t t_wait = 0;
 
     // ring of key tiles, 128-byte rows whose 16-byte chunks are XOR-swizzled by row
     __shared__ half_t s_k[KB][kKeyTile][64];   // [buf][key][dim]
@@ -361,6 +453,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
     __shared__ int s_pos[R];
     __shared__ int s_row[R];
     __shared__ uint64_t s_mask[2];
+    __shared__ int4 s_seg[PERSIST ? 64 : 1];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -375,389 +468,442 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a,
     const int rs = slot / HPW;
     const int hi = slot % HPW;
 
-    const WgPos wp = wg_pos(a);
-    const int groups_per_kv = a.n_rep / HPW;
-    const int g = wp.x / groups_per_kv;
-    const int h = g * a.n_rep + (wp.x % groups_per_kv) * HPW + hi;
+    [[maybe_unused]] const uint64_t t_kernel = CRUCIBLE_PSTAMP_CLOCK();
+    // PERSIST: lane r holds segment r and its number of row tiles; n_list tiles in all
+    [[maybe_unused]] CompactList cl{};
+    if constexpr (PERSIST) cl = compact_list<R>(a, wave, lane, s_seg);
 
-    // ---- rows of this tile: (packed row, owner, absolute position); -1 = none
-    int row = -1, owner = 0, pos = 0;
-    if (tid < R) {
-        tile_row(a, wp.req, wp.tile * R + tid, row, owner, pos);
-        s_row[tid] = row;
-        s_owner[tid] = owner;
-        s_pos[tid] = pos;
-    }
-    // valid-row masks of rows 0..63 and 64..127 (R <= 128, so waves 0 and 1 cover them)
-    const uint64_t vmask = __ballot(tid < R && row >= 0);
-    if (wave < 2 && lane == 0) s_mask[wave] = vmask;
-    __syncthreads();
-    const uint64_t mask0 = s_mask[0];
-    const uint64_t mask1 = R > 64 ? s_mask[1] : 0;
-    if (mask0 == 0 && mask1 == 0) return;  // uniform: no row of this tile is valid
-    CRUCIBLE_PSTAMP(kPStart, t_entry);
-    CRUCIBLE_PSTAMP(kPRows, CRUCIBLE_PSTAMP_CLOCK());
+    for (int round = 0;; ++round) {
+        [[maybe_unused]] uint32_t k = 0;  // PERSIST: this tile's list position
+        if constexpr (PERSIST) {
+            const uint32_t G = gridDim.x, w = blockIdx.x;
+            k = (round & 1) ? (uint32_t)(round + 1) * G - 1 - w : (uint32_t)round * G + w;
+            if (k >= cl.n_list) break;  // uniform; every later round's position is larger
+        }
+        // a tile's start: the kernel's entry for the first, else the end of the previous tile
+        [[maybe_unused]] const uint64_t t_entry = round == 0 ? t_kernel : CRUCIBLE_PSTAMP_CLOCK();
+        [[maybe_unused]] uint64_t t_wait = 0;
+        [[maybe_unused]] const unsigned pstamp_id = PERSIST ? k : pstamp_row();
 
-    // ---- per-lane query state for each 16-row block (the query rows load after the first
-    // run's leading tiles are issued, below, so the two round trips overlap)
-    const int64_t ld_q = (int64_t)a.n_head * kHeadDim;
-    half8_t qh[QB][2], ql[QB][2];
-    float m[QB], l[QB];
-    float4_t acc[QB][4];
-    int my_row[QB], my_pos[QB];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-        const int ri = rs * WROWS + qb * 16 + col;
-        my_row[qb] = s_row[ri];
-        my_pos[qb] = s_pos[ri];
-        m[qb] = -INFINITY;
-        l[qb] = 0.0f;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) acc[qb][db] = float4_t{0.f, 0.f, 0.f, 0.f};
-        qh[qb][0] = qh[qb][1] = ql[qb][0] = ql[qb][1] = half8_t{};
-    }
-    auto load_queries = [&]() {
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-            if (my_row[qb] < 0) continue;
-            const int64_t off = (int64_t)my_row[qb] * ld_q + (int64_t)h * kHeadDim + 8 * grp;
-            if constexpr (QF32) {
-                const float* qp = static_cast<const float*>(a.q) + off;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float x0 = qp[j], x1 = qp[32 + j];
-                    qh[qb][0][j] = (half_t)x0;
-                    qh[qb][1][j] = (half_t)x1;
-                    ql[qb][0][j] = (half_t)(x0 - (float)qh[qb][0][j]);
-                    ql[qb][1][j] = (half_t)(x1 - (float)qh[qb][1][j]);
+        const WgPos wp = PERSIST ? compact_pos(a, cl, k, lane) : wg_pos(a);
+        const int groups_per_kv = a.n_rep / HPW;
+        const int g = wp.x / groups_per_kv;
+        const int h = g * a.n_rep + (wp.x % groups_per_kv) * HPW + hi;
+
+        // ---- rows of this tile: (packed row, owner, absolute position); -1 = none
+        int row = -1, owner = 0, pos = 0;
+        if constexpr (PERSIST) {
+            // the request's segment from the lane that holds it (wp.req is wave-uniform)
+            const int r = (int)wp.req;
+            const int s0 = __builtin_amdgcn_readlane(cl.seg.x, r);
+            const int s1 = __builtin_amdgcn_readlane(cl.seg.y, r);
+            const int s2 = __builtin_amdgcn_readlane(cl.seg.z, r);
+            const int s3 = __builtin_amdgcn_readlane(cl.seg.w, r);
+            if (tid < R) {
+                const int64_t local = wp.tile * R + tid;
+                if (local >= 0 && local < s1) {
+                    row = (int)(s0 + local);
+                    pos = (int)(s2 + local);
+                    owner = s3;
                 }
+                if (pos < 0 || pos >= a.max_seq) row = -1;
+                s_row[tid] = row;
+                s_owner[tid] = owner;
+                s_pos[tid] = pos;
+            }
+        } else if (tid < R) {
+            tile_row(a, wp.req, wp.tile * R + tid, row, owner, pos);
+            s_row[tid] = row;
+            s_owner[tid] = owner;
+            s_pos[tid] = pos;
+        }
+        // valid-row masks of rows 0..63 and 64..127 (R <= 128, so waves 0 and 1 cover them)
+        const uint64_t vmask = __ballot(tid < R && row >= 0);
+        if (wave < 2 && lane == 0) s_mask[wave] = vmask;
+        __syncthreads();
+        const uint64_t mask0 = s_mask[0];
+        const uint64_t mask1 = R > 64 ? s_mask[1] : 0;
+        if (mask0 == 0 && mask1 == 0) {  // uniform: no row of this tile is valid
+            if constexpr (!PERSIST) {
+                return;
             } else {
-                const half_t* qp = static_cast<const half_t*>(a.q) + off;
-                qh[qb][0] = *reinterpret_cast<const half8_t*>(qp);
-                qh[qb][1] = *reinterpret_cast<const half8_t*>(qp + 32);
+                __syncthreads();  // every wave has read the masks before the next tile's rows
+                continue;
             }
         }
-    };
+        CRUCIBLE_PSTAMP(kPStart, t_entry);
+        CRUCIBLE_PSTAMP(kPRows, CRUCIBLE_PSTAMP_CLOCK());
 
-    const int kv_dim = a.addr.kv_dim;
-    typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
-
-    // ---- runs of one owner (the values come from LDS: readfirstlane makes the compiler
-    // treat them as the wave-uniform values they are, so page ids load as scalars)
-    // Segment, params and contiguous tiles hold one run of consecutive positions: its
-    // rows are the span of valid rows, read off the masks. Owner tiles may hold several
-    // runs (one per request) and are scanned row by row.
-    const int first_valid = mask0 ? __builtin_ctzll(mask0) : 64 + __builtin_ctzll(mask1);
-    const int last_valid = mask1 ? 127 - __builtin_clzll(mask1) : 63 - __builtin_clzll(mask0);
-    const int wlo = rs * WROWS, whi = rs * WROWS + WROWS;
-    // Wave w stages page w >> 1 of every tile: K rows 8 (w & 1) .. +7 and V^T dims
-    // 32 (w & 1) .. +31 of that page (below), so each wave needs one page id per tile.
-    const int my_page = wave >> 1;
-    bool first_run = true;
-#ifdef CRUCIBLE_STAMPS
-    bool first_pair_stamp = true;
-    int stamp_pairs = 0;
-#endif
-    int r0 = a.mode == kOwners ? 0 : first_valid;
-    while (r0 < R) {
-        int r1, owner, hist_end, wave_last;
-        if (a.mode != kOwners) {
-            r1 = last_valid + 1;
-            owner = s_owner[r0];
-            hist_end = s_pos[last_valid] + 1;
-            const int lo = max(r0, wlo), hi = min(r1, whi);
-            wave_last = lo < hi ? s_pos[hi - 1] : -1;
-        } else {
-            // next run start: first valid row at or after r0
-            while (r0 < R && s_row[r0] < 0) ++r0;
-            if (r0 >= R) break;
-            owner = s_owner[r0];
-            r1 = r0 + 1;
-            while (r1 < R && s_row[r1] >= 0 && s_owner[r1] == owner) ++r1;
-            hist_end = 0;
-            for (int r = r0; r < r1; ++r) hist_end = max(hist_end, s_pos[r] + 1);
-            // this wave's last visible key within the run
-            wave_last = -1;
-            for (int r = max(r0, wlo); r < min(r1, whi); ++r) wave_last = max(wave_last, s_pos[r]);
-        }
-        r0 = __builtin_amdgcn_readfirstlane(r0);
-        r1 = __builtin_amdgcn_readfirstlane(r1);
-        owner = __builtin_amdgcn_readfirstlane(owner);
-        hist_end = __builtin_amdgcn_readfirstlane(hist_end);
-        wave_last = __builtin_amdgcn_readfirstlane(wave_last);
-
-        // Page ids go through the scalar cache (constant address space): the tables are
-        // never written during a launch, and scalar loads (lgkmcnt) never wait on the
-        // in-flight tile loads the way vector loads (vmcnt) would. Without a table
-        // (contiguous cache) the page index is the id; the load then reads a harmless word
-        // of the pool, so it needs no branch.
-        const bool paged = tables != nullptr;
-        const const_i32_ptr table = paged ? (const_i32_ptr)(tables + (int64_t)owner * a.table_stride)
-                                          : (const_i32_ptr)a.k_pool;
-        const int n_tiles = (hist_end + kKeyTile - 1) / kKeyTile;
-        const int last_page = (hist_end - 1) >> kPageShift;
-        // This wave's page of tile t; pages past the run's last one are clamped to it (in
-        // bounds; their keys are zeroed or masked later).
-        auto page_of = [&](int t) -> int64_t {
-            const int idx = min(4 * t + my_page, last_page);
-            const int id = table[paged ? idx : 0];
-            return paged ? (int64_t)id : (int64_t)idx;
-        };
-
-        // Issue tile t into ring buffer t % KB: 2 direct-to-LDS loads per thread.
-        auto issue = [&](int t, int64_t page) {
-            const int buf = t % KB;
-            const int64_t base = block_base(a.addr, page);
-            // K: wave w covers keys 8w .. 8w+7 of the tile; lane L puts chunk
-            // (L & 7) ^ (row & 7) of its row at chunk position L & 7.
-            {
-                const int row = 8 * wave + (lane >> 3);
-                const int c = (lane & 7) ^ (row & 7);
-                const half_t* src = a.k_pool + base + (int64_t)(row & kPageMask) * kv_dim +
-                                    g * kHeadDim + 8 * c;
-                lds_dma16(src, lds_offset(&s_k[buf][8 * wave][0]));
-            }
-            // V^T, page-major: buffer `buf` holds the tile's 4 pages, each [64 dims][16 keys]
-            // (32-byte rows, the two 8-key halves of a row swapped when bit 3 of the dim is
-            // set, which keeps the operand reads free of bank conflicts). Lane L of wave w
-            // moves dim 32 (w & 1) + (L >> 1), row position L & 1, of page w >> 1: the
-            // wave's 64 lanes fill 1 KiB of that page in order.
-            {
-                const int d = 32 * (wave & 1) + (lane >> 1);
-                const int half = (lane & 1) ^ ((d >> 3) & 1);
-                const half_t* src = a.v_pool + base +
-                                    (int64_t)(g * kHeadDim + d) * kPageTokens + 8 * half;
-                lds_dma16(src, lds_offset(&s_v[buf][0][0] + my_page * 1024 + (wave & 1) * 512));
-            }
-        };
-
-        bool in_run[QB];
+        // ---- per-lane query state for each 16-row block (the query rows load after the first
+        // run's leading tiles are issued, below, so the two round trips overlap)
+        const int64_t ld_q = (int64_t)a.n_head * kHeadDim;
+        half8_t qh[QB][2], ql[QB][2];
+        float m[QB], l[QB];
+        float4_t acc[QB][4];
+        int my_row[QB], my_pos[QB];
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
             const int ri = rs * WROWS + qb * 16 + col;
-            in_run[qb] = my_row[qb] >= 0 && ri >= r0 && ri < r1;
+            my_row[qb] = s_row[ri];
+            my_pos[qb] = s_pos[ri];
+            m[qb] = -INFINITY;
+            l[qb] = 0.0f;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[qb][db] = float4_t{0.f, 0.f, 0.f, 0.f};
+            qh[qb][0] = qh[qb][1] = ql[qb][0] = ql[qb][1] = half8_t{};
         }
+        auto load_queries = [&]() {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                if (my_row[qb] < 0) continue;
+                const int64_t off = (int64_t)my_row[qb] * ld_q + (int64_t)h * kHeadDim + 8 * grp;
+                if constexpr (QF32) {
+                    const float* qp = static_cast<const float*>(a.q) + off;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float x0 = qp[j], x1 = qp[32 + j];
+                        qh[qb][0][j] = (half_t)x0;
+                        qh[qb][1][j] = (half_t)x1;
+                        ql[qb][0][j] = (half_t)(x0 - (float)qh[qb][0][j]);
+                        ql[qb][1][j] = (half_t)(x1 - (float)qh[qb][1][j]);
+                    }
+                } else {
+                    const half_t* qp = static_cast<const half_t*>(a.q) + off;
+                    qh[qb][0] = *reinterpret_cast<const half8_t*>(qp);
+                    qh[qb][1] = *reinterpret_cast<const half8_t*>(qp + 32);
+                }
+            }
+        };
 
-        // Tiles go in pairs: wave w computes tile 2i + (w >> 2) of pair i, so each wave of
-        // a slot runs half of the tiles and the two halves' softmax chains overlap.
-        constexpr int PS = KB / 2;  // pair slots in the ring
-        const int n_pairs = (n_tiles + 1) / 2;
+        const int kv_dim = a.addr.kv_dim;
+        typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+
+        // ---- runs of one owner (the values come from LDS: readfirstlane makes the compiler
+        // treat them as the wave-uniform values they are, so page ids load as scalars)
+        // Segment, params and contiguous tiles hold one run of consecutive positions: its
+        // rows are the span of valid rows, read off the masks. Owner tiles may hold several
+        // runs (one per request) and are scanned row by row.
+        const int first_valid = mask0 ? __builtin_ctzll(mask0) : 64 + __builtin_ctzll(mask1);
+        const int last_valid = mask1 ? 127 - __builtin_clzll(mask1) : 63 - __builtin_clzll(mask0);
+        const int wlo = rs * WROWS, whi = rs * WROWS + WROWS;
+        // Wave w stages page w >> 1 of every tile: K rows 8 (w & 1) .. +7 and V^T dims
+        // 32 (w & 1) .. +31 of that page (below), so each wave needs one page id per tile.
+        const int my_page = wave >> 1;
+        bool first_run = true;
 #ifdef CRUCIBLE_STAMPS
-        stamp_pairs += n_pairs;
+        bool first_pair_stamp = true;
+        int stamp_pairs = 0;
 #endif
-        // the pair holding the run's last tile when that tile is partial, else none
-        const int tail_pair = (hist_end % kKeyTile) ? (n_tiles - 1) / 2 : -1;
-#pragma unroll
-        for (int p = 0; p < PS - 1; ++p)
-            if (p < n_pairs) {
-                const int64_t pa = page_of(2 * p), pb = page_of(2 * p + 1);
-                issue(2 * p, pa);
-                issue(2 * p + 1, pb);  // past n_tiles: a clamped, in-bounds load nobody reads
+        int r0 = a.mode == kOwners ? 0 : first_valid;
+        while (r0 < R) {
+            int r1, owner, hist_end, wave_last;
+            if (a.mode != kOwners) {
+                r1 = last_valid + 1;
+                owner = s_owner[r0];
+                hist_end = s_pos[last_valid] + 1;
+                const int lo = max(r0, wlo), hi = min(r1, whi);
+                wave_last = lo < hi ? s_pos[hi - 1] : -1;
+            } else {
+                // next run start: first valid row at or after r0
+                while (r0 < R && s_row[r0] < 0) ++r0;
+                if (r0 >= R) break;
+                owner = s_owner[r0];
+                r1 = r0 + 1;
+                while (r1 < R && s_row[r1] >= 0 && s_owner[r1] == owner) ++r1;
+                hist_end = 0;
+                for (int r = r0; r < r1; ++r) hist_end = max(hist_end, s_pos[r] + 1);
+                // this wave's last visible key within the run
+                wave_last = -1;
+                for (int r = max(r0, wlo); r < min(r1, whi); ++r)
+                    wave_last = max(wave_last, s_pos[r]);
             }
-        if (first_run) {
-            // The query operands are complete before the loop, so no wait for them can land
-            // inside it (where it would also wait for the tiles in flight).
-            load_queries();
-            __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
-            first_run = false;
-        }
-        for (int ip = 0; ip < n_pairs; ++ip) {
-            // Wait for this thread's loads of pair ip (later pairs may stay in flight, 4
-            // loads each) and its LDS reads of pair ip - 1; the barrier then makes every
-            // wave's loads visible and frees pair ip - 1's buffers for pair ip + PS - 1.
-            const int ahead = min(PS - 2, n_pairs - 1 - ip);
-            [[maybe_unused]] const uint64_t t_w0 = CRUCIBLE_PSTAMP_CLOCK();
-            if (ahead >= 2) __builtin_amdgcn_s_waitcnt(kWaitVm8Lgkm0);
-            else if (ahead == 1) __builtin_amdgcn_s_waitcnt(kWaitVm4Lgkm0);
-            else __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
-            // Keys past the run's end may hold anything, NaN included, and P = 0 there
-            // would still give 0 * NaN: in the run's last tile, each thread zeroes them in
-            // the V^T chunk it loaded (its own load has landed), before the barrier.
-            if (ip == tail_pair) {
-                const int t = n_tiles - 1;
-                const int d = 32 * (wave & 1) + (lane >> 1);
-                const int half = (lane & 1) ^ ((d >> 3) & 1);  // keys 16 j + 8 half .. +7
-                const int nv = hist_end - (t * kKeyTile + 16 * my_page + 8 * half);
-                if (nv < 8) {
-                    half8_t* chunk = reinterpret_cast<half8_t*>(
-                        &s_v[t % KB][0][0] + my_page * 1024 + (wave & 1) * 512) + lane;
-                    half8_t v = *chunk;
-#pragma unroll
-                    for (int r = 0; r < 8; ++r)
-                        if (r >= nv) v[r] = (half_t)0.0f;
-                    *chunk = v;
-                }
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            }
-            __builtin_amdgcn_s_barrier();
-#ifdef CRUCIBLE_STAMPS
-            {
-                const uint64_t t_w1 = CRUCIBLE_PSTAMP_CLOCK();
-                t_wait += t_w1 - t_w0;
-                if (first_pair_stamp) {
-                    CRUCIBLE_PSTAMP(kPFirst, t_w1);
-                    first_pair_stamp = false;
-                }
-            }
-#endif
-            if (ip + PS - 1 < n_pairs) {
-                const int tn = 2 * (ip + PS - 1);
-                const int64_t pa = page_of(tn), pb = page_of(tn + 1);
-                issue(tn, pa);
-                issue(tn + 1, pb);
-            }
-            const int t = 2 * ip + kh;
-            const int kbase = t * kKeyTile;
-            if (t < n_tiles && wave_last >= kbase) {
+            r0 = __builtin_amdgcn_readfirstlane(r0);
+            r1 = __builtin_amdgcn_readfirstlane(r1);
+            owner = __builtin_amdgcn_readfirstlane(owner);
+            hist_end = __builtin_amdgcn_readfirstlane(hist_end);
+            wave_last = __builtin_amdgcn_readfirstlane(wave_last);
+
+            // Page ids go through the scalar cache (constant address space): the tables are
+            // never written during a launch, and scalar loads (lgkmcnt) never wait on the
+            // in-flight tile loads the way vector loads (vmcnt) would. Without a table
+            // (contiguous cache) the page index is the id; the load then reads a harmless word
+            // of the pool, so it needs no branch.
+            const bool paged = tables != nullptr;
+            const const_i32_ptr table =
+                paged ? (const_i32_ptr)(tables + (int64_t)owner * a.table_stride)
+                      : (const_i32_ptr)a.k_pool;
+            const int n_tiles = (hist_end + kKeyTile - 1) / kKeyTile;
+            const int last_page = (hist_end - 1) >> kPageShift;
+            // This wave's page of tile t; pages past the run's last one are clamped to it (in
+            // bounds; their keys are zeroed or masked later).
+            auto page_of = [&](int t) -> int64_t {
+                const int idx = min(4 * t + my_page, last_page);
+                const int id = table[paged ? idx : 0];
+                return paged ? (int64_t)id : (int64_t)idx;
+            };
+
+            // Issue tile t into ring buffer t % KB: 2 direct-to-LDS loads per thread.
+            auto issue = [&](int t, int64_t page) {
                 const int buf = t % KB;
-                // S^T blocks: st[qb][kb] = S^T[kbase + key(kb, 4 grp + r)][q = col]
-                float4_t st[QB][4];
+                const int64_t base = block_base(a.addr, page);
+                // K: wave w covers keys 8w .. 8w+7 of the tile; lane L puts chunk
+                // (L & 7) ^ (row & 7) of its row at chunk position L & 7.
+                {
+                    const int row = 8 * wave + (lane >> 3);
+                    const int c = (lane & 7) ^ (row & 7);
+                    const half_t* src = a.k_pool + base + (int64_t)(row & kPageMask) * kv_dim +
+                                        g * kHeadDim + 8 * c;
+                    lds_dma16(src, lds_offset(&s_k[buf][8 * wave][0]));
+                }
+                // V^T, page-major: buffer `buf` holds the tile's 4 pages, each [64 dims][16 keys]
+                // (32-byte rows, the two 8-key halves of a row swapped when bit 3 of the dim is
+                // set, which keeps the operand reads free of bank conflicts). Lane L of wave w
+                // moves dim 32 (w & 1) + (L >> 1), row position L & 1, of page w >> 1: the
+                // wave's 64 lanes fill 1 KiB of that page in order.
+                {
+                    const int d = 32 * (wave & 1) + (lane >> 1);
+                    const int half = (lane & 1) ^ ((d >> 3) & 1);
+                    const half_t* src = a.v_pool + base +
+                                        (int64_t)(g * kHeadDim + d) * kPageTokens + 8 * half;
+                    lds_dma16(src, lds_offset(&s_v[buf][0][0] + my_page * 1024 + (wave & 1) * 512));
+                }
+            };
+
+            bool in_run[QB];
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb) {
-                    const int row = tile_key(kb, col);
-                    const half8_t a0 = *reinterpret_cast<const half8_t*>(
-                        &s_k[buf][row][8 * (grp ^ (row & 7))]);
-                    const half8_t a1 = *reinterpret_cast<const half8_t*>(
-                        &s_k[buf][row][8 * ((4 + grp) ^ (row & 7))]);
+            for (int qb = 0; qb < QB; ++qb) {
+                const int ri = rs * WROWS + qb * 16 + col;
+                in_run[qb] = my_row[qb] >= 0 && ri >= r0 && ri < r1;
+            }
+
+            // Tiles go in pairs: wave w computes tile 2i + (w >> 2) of pair i, so each wave of
+            // a slot runs half of the tiles and the two halves' softmax chains overlap.
+            constexpr int PS = KB / 2;  // pair slots in the ring
+            const int n_pairs = (n_tiles + 1) / 2;
+#ifdef CRUCIBLE_STAMPS
+            stamp_pairs += n_pairs;
+#endif
+            // the pair holding the run's last tile when that tile is partial, else none
+            const int tail_pair = (hist_end % kKeyTile) ? (n_tiles - 1) / 2 : -1;
 #pragma unroll
-                    for (int qb = 0; qb < QB; ++qb) {
-                        float4_t c = {0.f, 0.f, 0.f, 0.f};
-                        c = mfma_16x16x32(a0, qh[qb][0], c);
-                        c = mfma_16x16x32(a1, qh[qb][1], c);
-                        if constexpr (QF32) {
-                            c = mfma_16x16x32(a0, ql[qb][0], c);
-                            c = mfma_16x16x32(a1, ql[qb][1], c);
-                        }
-                        st[qb][kb] = c;
+            for (int p = 0; p < PS - 1; ++p)
+                if (p < n_pairs) {
+                    const int64_t pa = page_of(2 * p), pb = page_of(2 * p + 1);
+                    issue(2 * p, pa);
+                    issue(2 * p + 1, pb);  // past n_tiles: a clamped, in-bounds load nobody reads
+                }
+            if (first_run) {
+                // The query operands are complete before the loop, so no wait for them can land
+                // inside it (where it would also wait for the tiles in flight).
+                load_queries();
+                __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+                first_run = false;
+            }
+            for (int ip = 0; ip < n_pairs; ++ip) {
+                // Wait for this thread's loads of pair ip (later pairs may stay in flight, 4
+                // loads each) and its LDS reads of pair ip - 1; the barrier then makes every
+                // wave's loads visible and frees pair ip - 1's buffers for pair ip + PS - 1.
+                const int ahead = min(PS - 2, n_pairs - 1 - ip);
+                [[maybe_unused]] const uint64_t t_w0 = CRUCIBLE_PSTAMP_CLOCK();
+                if (ahead >= 2) __builtin_amdgcn_s_waitcnt(kWaitVm8Lgkm0);
+                else if (ahead == 1) __builtin_amdgcn_s_waitcnt(kWaitVm4Lgkm0);
+                else __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+                // Keys past the run's end may hold anything, NaN included, and P = 0 there
+                // would still give 0 * NaN: in the run's last tile, each thread zeroes them in
+                // the V^T chunk it loaded (its own load has landed), before the barrier.
+                if (ip == tail_pair) {
+                    const int t = n_tiles - 1;
+                    const int d = 32 * (wave & 1) + (lane >> 1);
+                    const int half = (lane & 1) ^ ((d >> 3) & 1);  // keys 16 j + 8 half .. +7
+                    const int nv = hist_end - (t * kKeyTile + 16 * my_page + 8 * half);
+                    if (nv < 8) {
+                        half8_t* chunk = reinterpret_cast<half8_t*>(
+                            &s_v[t % KB][0][0] + my_page * 1024 + (wave & 1) * 512) + lane;
+                        half8_t v = *chunk;
+#pragma unroll
+                        for (int r = 0; r < 8; ++r)
+                            if (r >= nv) v[r] = (half_t)0.0f;
+                        *chunk = v;
+                    }
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                }
+                __builtin_amdgcn_s_barrier();
+#ifdef CRUCIBLE_STAMPS
+                {
+                    const uint64_t t_w1 = CRUCIBLE_PSTAMP_CLOCK();
+                    t_wait += t_w1 - t_w0;
+                    if (first_pair_stamp) {
+                        CRUCIBLE_PSTAMP(kPFirst, t_w1);
+                        first_pair_stamp = false;
                     }
                 }
-                // Mask; a tile that every row of the wave sees whole (below the diagonal,
-                // all rows in the run) needs none.
-                bool lane_full = true;
-#pragma unroll
-                for (int qb = 0; qb < QB; ++qb)
-                    lane_full = lane_full && in_run[qb] && my_pos[qb] >= kbase + kKeyTile - 1;
-                if (!__all(lane_full)) {
-#pragma unroll
-                    for (int qb = 0; qb < QB; ++qb)
-                        mask_tile(st[qb], in_run[qb] ? my_pos[qb] - kbase - 8 * grp : -1);
+#endif
+                if (ip + PS - 1 < n_pairs) {
+                    const int tn = 2 * (ip + PS - 1);
+                    const int64_t pa = page_of(tn), pb = page_of(tn + 1);
+                    issue(tn, pa);
+                    issue(tn + 1, pb);
                 }
-                half8_t pb[QB][2];
-                half8_t pl[QB][2];  // P = hi + lo: the product keeps ~22 bits of P (not P16)
+                const int t = 2 * ip + kh;
+                const int kbase = t * kKeyTile;
+                if (t < n_tiles && wave_last >= kbase) {
+                    const int buf = t % KB;
+                    // S^T blocks: st[qb][kb] = S^T[kbase + key(kb, 4 grp + r)][q = col]
+                    float4_t st[QB][4];
 #pragma unroll
-                for (int qb = 0; qb < QB; ++qb) {
-                    const float tm = tile_max(st[qb]) * a.scale_log2;  // base-2 units
-                    // Lazy rescale: the running max moves only when the tile's max exceeds
-                    // it by more than kLazyLog2, so P stays <= 2^kLazyLog2 and most tiles
-                    // skip rescaling the accumulators. out = acc / l is unchanged.
-                    const bool grow = tm > m[qb] + kLazyLog2;
-                    if (__any(grow)) {
-                        // alpha = 1 where the max is kept (also -inf, where m - m is NaN);
-                        // 0 where it grows from -inf
-                        const float alpha = grow ? fast_exp2(m[qb] - tm) : 1.0f;
-                        const float mn = grow ? tm : m[qb];
-                        l[qb] *= alpha;
-#pragma unroll
-                        for (int db = 0; db < 4; ++db) acc[qb][db] = acc[qb][db] * alpha;
-                        m[qb] = mn;
-                    }
-                    const float mu = (m[qb] == -INFINITY) ? 0.0f : m[qb];
-                    l[qb] += tile_p<P16>(st[qb], a.scale_log2, mu, pb[qb], pl[qb]);
-                }
-                // O^T[dim][q] += V^T[dim][32 keys] . P^T[32 keys][q], key halves ks = 0, 1
-                // (keys past the run's end were zeroed in LDS above). Keys 32 ks + 8 grp .. +7
-                // of dim d are half grp & 1 of page 2 ks + (grp >> 1), at row position
-                // (grp & 1) ^ (bit 3 of d), one 16-byte read.
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    const int d = 16 * db + col;
-#pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) {
-                        const half8_t va = *reinterpret_cast<const half8_t*>(
-                            &s_v[buf][0][0] + (2 * ks + (grp >> 1)) * 1024 + d * 16 +
-                            8 * ((grp & 1) ^ ((d >> 3) & 1)));
+                    for (int kb = 0; kb < 4; ++kb) {
+                        const int row = tile_key(kb, col);
+                        const half8_t a0 = *reinterpret_cast<const half8_t*>(
+                            &s_k[buf][row][8 * (grp ^ (row & 7))]);
+                        const half8_t a1 = *reinterpret_cast<const half8_t*>(
+                            &s_k[buf][row][8 * ((4 + grp) ^ (row & 7))]);
 #pragma unroll
                         for (int qb = 0; qb < QB; ++qb) {
-                            acc[qb][db] = mfma_16x16x32(va, pb[qb][ks], acc[qb][db]);
-                            if constexpr (!P16)
-                                acc[qb][db] = mfma_16x16x32(va, pl[qb][ks], acc[qb][db]);
+                            float4_t c = {0.f, 0.f, 0.f, 0.f};
+                            c = mfma_16x16x32(a0, qh[qb][0], c);
+                            c = mfma_16x16x32(a1, qh[qb][1], c);
+                            if constexpr (QF32) {
+                                c = mfma_16x16x32(a0, ql[qb][0], c);
+                                c = mfma_16x16x32(a1, ql[qb][1], c);
+                            }
+                            st[qb][kb] = c;
+                        }
+                    }
+                    // Mask; a tile that every row of the wave sees whole (below the diagonal,
+                    // all rows in the run) needs none.
+                    bool lane_full = true;
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb)
+                        lane_full = lane_full && in_run[qb] && my_pos[qb] >= kbase + kKeyTile - 1;
+                    if (!__all(lane_full)) {
+#pragma unroll
+                        for (int qb = 0; qb < QB; ++qb)
+                            mask_tile(st[qb], in_run[qb] ? my_pos[qb] - kbase - 8 * grp : -1);
+                    }
+                    half8_t pb[QB][2];
+                    half8_t pl[QB][2];  // P = hi + lo: the product keeps ~22 bits of P (not P16)
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb) {
+                        const float tm = tile_max(st[qb]) * a.scale_log2;  // base-2 units
+                        // Lazy rescale: the running max moves only when the tile's max exceeds
+                        // it by more than kLazyLog2, so P stays <= 2^kLazyLog2 and most tiles
+                        // skip rescaling the accumulators. out = acc / l is unchanged.
+                        const bool grow = tm > m[qb] + kLazyLog2;
+                        if (__any(grow)) {
+                            // alpha = 1 where the max is kept (also -inf, where m - m is NaN);
+                            // 0 where it grows from -inf
+                            const float alpha = grow ? fast_exp2(m[qb] - tm) : 1.0f;
+                            const float mn = grow ? tm : m[qb];
+                            l[qb] *= alpha;
+#pragma unroll
+                            for (int db = 0; db < 4; ++db) acc[qb][db] = acc[qb][db] * alpha;
+                            m[qb] = mn;
+                        }
+                        const float mu = (m[qb] == -INFINITY) ? 0.0f : m[qb];
+                        l[qb] += tile_p<P16>(st[qb], a.scale_log2, mu, pb[qb], pl[qb]);
+                    }
+                    // O^T[dim][q] += V^T[dim][32 keys] . P^T[32 keys][q], key halves ks = 0, 1
+                    // (keys past the run's end were zeroed in LDS above). Keys 32 ks + 8 grp .. +7
+                    // of dim d are half grp & 1 of page 2 ks + (grp >> 1), at row position
+                    // (grp & 1) ^ (bit 3 of d), one 16-byte read.
+#pragma unroll
+                    for (int db = 0; db < 4; ++db) {
+                        const int d = 16 * db + col;
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks) {
+                            const half8_t va = *reinterpret_cast<const half8_t*>(
+                                &s_v[buf][0][0] + (2 * ks + (grp >> 1)) * 1024 + d * 16 +
+                                8 * ((grp & 1) ^ ((d >> 3) & 1)));
+#pragma unroll
+                            for (int qb = 0; qb < QB; ++qb) {
+                                acc[qb][db] = mfma_16x16x32(va, pb[qb][ks], acc[qb][db]);
+                                if constexpr (!P16)
+                                    acc[qb][db] = mfma_16x16x32(va, pl[qb][ks], acc[qb][db]);
+                            }
                         }
                     }
                 }
             }
+            // every wave's reads of the last buffers are done before the next run reuses them
+            __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+            __builtin_amdgcn_s_barrier();
+            if (a.mode != kOwners) break;  // a single run
+            r0 = r1;
         }
-        // every wave's reads of the last buffers are done before the next run reuses them
-        __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
-        __builtin_amdgcn_s_barrier();
-        if (a.mode != kOwners) break;  // a single run
-        r0 = r1;
-    }
 
-    CRUCIBLE_PSTAMP(kPLoop, CRUCIBLE_PSTAMP_CLOCK());
-    // ---- merge the key halves: waves 4..7 hand (m, l, acc) to their partner through
-    // the (now idle) ring; per lane, both hold the same query column and dims. Lane-major
-    // layout keeps the exchange free of bank conflicts: acc (4 x QB x 16 x 64 floats,
-    // 32 KiB at QB = 2) in the K ring, m and l in the V ring.
-    static_assert(4 * QB * 16 * 64 * sizeof(float) <= sizeof(s_k), "merge buffer");
-    float* s_macc = reinterpret_cast<float*>(&s_k[0][0][0]);
-    float* s_ml = reinterpret_cast<float*>(&s_v[0][0][0]);
-    if (kh == 1) {
+        CRUCIBLE_PSTAMP(kPLoop, CRUCIBLE_PSTAMP_CLOCK());
+        // ---- merge the key halves: waves 4..7 hand (m, l, acc) to their partner through
+        // the (now idle) ring; per lane, both hold the same query column and dims. Lane-major
+        // layout keeps the exchange free of bank conflicts: acc (4 x QB x 16 x 64 floats,
+        // 32 KiB at QB = 2) in the K ring, m and l in the V ring.
+        static_assert(4 * QB * 16 * 64 * sizeof(float) <= sizeof(s_k), "merge buffer");
+        float* s_macc = reinterpret_cast<float*>(&s_k[0][0][0]);
+        float* s_ml = reinterpret_cast<float*>(&s_v[0][0][0]);
+        if (kh == 1) {
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-            float* p = s_macc + (slot * QB + qb) * 16 * 64 + lane;
+            for (int qb = 0; qb < QB; ++qb) {
+                float* p = s_macc + (slot * QB + qb) * 16 * 64 + lane;
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
+                for (int db = 0; db < 4; ++db)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) p[(4 * db + r) * 64] = acc[qb][db][r];
-            float* q = s_ml + (slot * QB + qb) * 2 * 64 + lane;
-            q[0] = m[qb];
-            q[64] = l[qb];
-        }
-    }
-    __syncthreads();
-    if (kh == 1) return;
-    CRUCIBLE_PSTAMP(kPMerged, CRUCIBLE_PSTAMP_CLOCK());
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-        const float* p = s_macc + (slot * QB + qb) * 16 * 64 + lane;
-        const float* q = s_ml + (slot * QB + qb) * 2 * 64 + lane;
-        const float m1 = q[0], l1 = q[64];
-        const float mx = fmaxf(m[qb], m1);
-        const float mu = mx == -INFINITY ? 0.0f : mx;
-        const float w0 = fast_exp2(m[qb] - mu), w1 = fast_exp2(m1 - mu);
-        l[qb] = l[qb] * w0 + l1 * w1;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                acc[qb][db][r] = acc[qb][db][r] * w0 + p[(4 * db + r) * 64] * w1;
-    }
-
-    // ---- normalise and write: lane (q = col, grp) holds dims 16*db + 4*grp .. +3
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-        const float lt = group_sum4(l[qb]);
-        if (my_row[qb] < 0) continue;
-        const float inv = 1.0f / lt;
-        const int64_t off = (int64_t)my_row[qb] * ld_q + (int64_t)h * kHeadDim + 4 * grp;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const float4_t o = acc[qb][db] * inv;
-            if (a.out_f16) {
-                const half4_t hv = {(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
-                *reinterpret_cast<half4_t*>(static_cast<half_t*>(a.out) + off + 16 * db) = hv;
-            } else {
-                *reinterpret_cast<float4_t*>(static_cast<float*>(a.out) + off + 16 * db) = o;
+                    for (int r = 0; r < 4; ++r) p[(4 * db + r) * 64] = acc[qb][db][r];
+                float* q = s_ml + (slot * QB + qb) * 2 * 64 + lane;
+                q[0] = m[qb];
+                q[64] = l[qb];
             }
         }
-    }
+        __syncthreads();
+        if (kh == 0) {
+            CRUCIBLE_PSTAMP(kPMerged, CRUCIBLE_PSTAMP_CLOCK());
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                const float* p = s_macc + (slot * QB + qb) * 16 * 64 + lane;
+                const float* q = s_ml + (slot * QB + qb) * 2 * 64 + lane;
+                const float m1 = q[0], l1 = q[64];
+                const float mx = fmaxf(m[qb], m1);
+                const float mu = mx == -INFINITY ? 0.0f : mx;
+                const float w0 = fast_exp2(m[qb] - mu), w1 = fast_exp2(m1 - mu);
+                l[qb] = l[qb] * w0 + l1 * w1;
+#pragma unroll
+                for (int db = 0; db < 4; ++db)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[qb][db][r] = acc[qb][db][r] * w0 + p[(4 * db + r) * 64] * w1;
+            }
+
+            // ---- normalise and write: lane (q = col, grp) holds dims 16*db + 4*grp .. +3
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                const float lt = group_sum4(l[qb]);
+                if (my_row[qb] < 0) continue;
+                const float inv = 1.0f / lt;
+                const int64_t off = (int64_t)my_row[qb] * ld_q + (int64_t)h * kHeadDim + 4 * grp;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const float4_t o = acc[qb][db] * inv;
+                    if (a.out_f16) {
+                        const half4_t hv = {(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
+                        *reinterpret_cast<half4_t*>(static_cast<half_t*>(a.out) + off +
+                                                    16 * db) = hv;
+                    } else {
+                        *reinterpret_cast<float4_t*>(static_cast<float*>(a.out) + off +
+                                                     16 * db) = o;
+                    }
+                }
+            }
 #ifdef CRUCIBLE_STAMPS
-    CRUCIBLE_PSTAMP_AFTER(kPWritten);
-    CRUCIBLE_PSTAMP(kPWait, t_wait);
-    CRUCIBLE_PSTAMP(kPMeta, (uint64_t)(wp.tile & 0xffff) | (uint64_t)(wp.req & 0xffff) << 16 |
-                                (uint64_t)(wp.x & 0xffff) << 32 |
-                                (uint64_t)(stamp_pairs & 0xffff) << 48);
+            CRUCIBLE_PSTAMP_AFTER(kPWritten);
+            CRUCIBLE_PSTAMP(kPWait, t_wait);
+            CRUCIBLE_PSTAMP(kPMeta, (uint64_t)(wp.tile & 0xffff) |
+                                        (uint64_t)(wp.req & 0xffff) << 16 |
+                                        (uint64_t)(wp.x & 0xffff) << 32 |
+                                        (uint64_t)(stamp_pairs & 0xffff) << 48);
 #endif
+        }  // kh == 0
+        if constexpr (!PERSIST) return;
+        // The key-half-1 waves go on to the next tile's rows at once; its first barrier holds
+        // them until the key-half-0 waves have read the merge buffers (in the ring) above.
+    }  // rounds
 }
 
 // ---------------------------------------------------------------- 32-row waves on 32x32 MFMAs
@@ -1206,6 +1352,7 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
     const int col = lane & 15;
     const int grp = lane >> 4;
     [[maybe_unused]] const uint64_t t_entry = CRUCIBLE_PSTAMP_CLOCK();
+    [[maybe_unused]] const unsigned pstamp_id = pstamp_row();
     const WgPos wp = wg_pos(a);
     const int h = wp.x;
     const int g = h / a.n_rep;
@@ -1498,14 +1645,48 @@ __global__ __launch_bounds__(kDirectWaves * 64, 4) void prefill_direct_kernel(
 
 int heads_per_wg(int n_rep) { return (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1; }
 
+// Workgroups of `kernel` resident at once on this device (0 if unknown).
+int resident_workgroups(const void* kernel, int threads) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return per_cu * device_cu_count();
+}
+
 template <int HPW, int QB, bool QF32, bool P16>
 void launch_kb(const PrefillArgs& a, int kb, dim3 grid, hipStream_t stream) {
-    if (kb == 6)
-        hipLaunchKernelGGL((prefill_kernel<HPW, QB, QF32, 6, P16>), grid, dim3(kThreads), 0,
+    if (kb == 6) {
+        hipLaunchKernelGGL((prefill_kernel<HPW, QB, QF32, 6, P16, false>), grid, dim3(kThreads), 0,
                            stream, a, a.tables);
-    else
-        hipLaunchKernelGGL((prefill_kernel<HPW, QB, QF32, 4, P16>), grid, dim3(kThreads), 0,
-                           stream, a, a.tables);
+        return;
+    }
+    // On request (the tuning key), a longest-first segment grid larger than the resident
+    // workgroups runs persistent: the dispatcher hands every id, those of tiles without rows
+    // included, to a freed slot on the XCD the id maps to, and each pays a workgroup's
+    // launch and its own segment round trip. That pays off when most ids hold no rows (one
+    // long prompt packed with many short ones); with few such ids (config 4) the dispatcher's
+    // dynamic order is as good and the list costs the first tile about a microsecond, so
+    // the default stays the one-workgroup-per-id grid.
+    auto persistent = prefill_kernel<HPW, QB, QF32, 4, P16, true>;
+    static std::atomic<int> resident{-1};  // per instantiation; the same device type throughout
+    const int mode = tuning(CRUCIBLE_TUNE_PREFILL_PERSIST);  // 1: resident; n >= 2: n
+    if (a.heavy_first && a.mode == kSegments && a.grid_reqs <= 64 && a.grid_tiles <= 64 &&
+        mode > 0) {
+        int r = mode >= 2 ? mode : resident.load(std::memory_order_relaxed);
+        if (r < 0) {
+            r = resident_workgroups(reinterpret_cast<const void*>(persistent), kThreads);
+            resident.store(r, std::memory_order_relaxed);
+        }
+        if (r > 0 && grid.x > (unsigned)r) {
+            hipLaunchKernelGGL(persistent, dim3((unsigned)r), dim3(kThreads), 0, stream, a,
+                               a.tables);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((prefill_kernel<HPW, QB, QF32, 4, P16, false>), grid, dim3(kThreads), 0,
+                       stream, a, a.tables);
 }
 
 // ---------------------------------------------------------------- head_dim other than 64

@@ -59,7 +59,8 @@ def set_tuning(**overrides) -> None:
     """Force launch shapes for every later launch in the process (crucible_attn_set_tuning):
     decode_pages, decode_waves, decode_order ("split" | "request" | "compact"),
     prefill_direct, prefill_heavy_first, prefill_qb, prefill_bufs, linear_tile,
-    decode_combine_width, prefill_p16, prefill_m32. None returns a key to the launcher's own choice."""
+    decode_combine_width, prefill_p16, prefill_m32, prefill_persist. None returns a key to the
+    launcher's own choice."""
     lib = _lib.load()
     for name, value in overrides.items():
         if name not in _lib.TUNE_KEYS:

@@ -89,7 +89,11 @@ enum crucible_tuning_key {
     CRUCIBLE_TUNE_DECODE_COMBINE_WIDTH = 8, /* decode splits merged per round trip: 8, 16 */
     CRUCIBLE_TUNE_PREFILL_P16 = 9,         /* prefill P operand: 0 fp16 hi + lo (default), 1 one fp16 */
     CRUCIBLE_TUNE_PREFILL_M32 = 10,        /* prefill 32-row waves on 32x32 MFMAs: 1 (default), 0 */
-    CRUCIBLE_TUNE_COUNT = 11
+    CRUCIBLE_TUNE_PREFILL_PERSIST = 11,    /* prefill persistent 16-row LDS form for segment rows
+                                              (a static longest-first list of the row tiles that
+                                              hold rows): 0 off (default), 1 one workgroup per
+                                              resident slot, n >= 2 a grid of n workgroups */
+    CRUCIBLE_TUNE_COUNT = 12
 };
 int crucible_attn_set_tuning(int key, int value);
 /* Current value of a key (-1: automatic, or an unknown key). */

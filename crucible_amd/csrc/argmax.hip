@@ -147,7 +147,8 @@ extern "C" int crucible_greedy_advance(const float* logits, int64_t rows, int64_
                                        uint32_t* done, crucible_stream_t stream) {
     const char* what = "greedy_advance";
     CRUCIBLE_CHECK(rows >= 0 && rows <= 65535 && cols > 0 && cols < 0x7fffffffLL &&
-                       n_embd > 0 && ldx >= n_embd && max_steps >= 0,
+                       n_embd > 0 && ldx >= n_embd && ldx <= INT32_MAX && max_steps >= 0 &&
+                       max_steps <= INT32_MAX,
                    CRUCIBLE_ERR_INVALID, "%s: rows=%lld cols=%lld n_embd=%lld ldx=%lld", what,
                    (long long)rows, (long long)cols, (long long)n_embd, (long long)ldx);
     if (rows == 0) return CRUCIBLE_OK;

@@ -1271,6 +1271,8 @@ int check_geometry(const char* what, int64_t n_head, int64_t n_kv_head, int64_t 
     CRUCIBLE_CHECK(n_head > 0 && n_kv_head > 0 && n_head % n_kv_head == 0, CRUCIBLE_ERR_INVALID,
                    "%s: n_head %lld must be a positive multiple of n_kv_head %lld", what,
                    (long long)n_head, (long long)n_kv_head);
+    // before any product of the head counts: n_kv_head <= n_head <= 2^20 from here on
+    CRUCIBLE_CHECK(n_head <= (1 << 20), CRUCIBLE_ERR_INVALID, "%s: n_head too large", what);
     CRUCIBLE_CHECK(head_dim == kHeadDim || generic_head_dim_ok(head_dim),
                    CRUCIBLE_ERR_UNSUPPORTED,
                    "%s: head_dim %lld unsupported (a multiple of 8 up to %d)", what,
@@ -1279,7 +1281,6 @@ int check_geometry(const char* what, int64_t n_head, int64_t n_kv_head, int64_t 
                    "%s: more than 16 query heads per kv head", what);
     CRUCIBLE_CHECK(kv_dim == n_kv_head * head_dim, CRUCIBLE_ERR_INVALID,
                    "%s: kv_dim %lld != n_kv_head * head_dim", what, (long long)kv_dim);
-    CRUCIBLE_CHECK(n_head <= (1 << 20), CRUCIBLE_ERR_INVALID, "%s: n_head too large", what);
     return CRUCIBLE_OK;
 }
 
@@ -1300,12 +1301,24 @@ int counter_stride(int64_t units, int64_t capacity) {
     return units * kCounterPad <= capacity ? kCounterPad : 1;
 }
 
+// Saturating: a size past SIZE_MAX reads as SIZE_MAX, which no workspace or scratch meets,
+// so an absurd shape fails the size check instead of wrapping to a small need.
 size_t partial_floats(int64_t batch, int64_t n_head, int64_t n_splits) {
-    return (size_t)batch * n_head * n_splits * (kHeadDim + 2);
+    if (batch < 0 || n_head < 0 || n_splits < 0) return SIZE_MAX;
+    size_t r;
+    if (__builtin_mul_overflow((size_t)batch, (size_t)n_head, &r) ||
+        __builtin_mul_overflow(r, (size_t)n_splits, &r) ||
+        __builtin_mul_overflow(r, (size_t)(kHeadDim + 2), &r))
+        return SIZE_MAX;
+    return r;
 }
 
 size_t workspace_need(int64_t batch, int64_t n_head, int64_t n_splits) {
-    return kCounterBytes + kPlanBytes + partial_floats(batch, n_head, n_splits) * sizeof(float);
+    size_t r;
+    if (__builtin_mul_overflow(partial_floats(batch, n_head, n_splits), sizeof(float), &r) ||
+        __builtin_add_overflow(r, kCounterBytes + kPlanBytes, &r))
+        return SIZE_MAX;
+    return r;
 }
 
 void bind_workspace(DecodeArgs& a, void* ws) {
@@ -1472,6 +1485,8 @@ using namespace crucible;
 extern "C" size_t crucible_attention_decode_workspace_bytes(int64_t batch, int64_t n_head,
                                                             int64_t max_seq) {
     if (batch <= 0 || n_head <= 0 || max_seq <= 0) return 0;
+    // past the entry points' limits (max_seq and batch <= INT32_MAX) the need saturates
+    if (max_seq > INT32_MAX || batch > INT32_MAX) return SIZE_MAX;
     const int64_t max_pages = (max_seq + kPageMask) >> kPageShift;
     const int64_t n_splits = (max_pages + 3) / 4;  // the smallest split: 1 page x 4 waves
     return workspace_need(batch, n_head, n_splits);
@@ -1505,8 +1520,9 @@ extern "C" int crucible_attention_decode_paged(
     a.lens = seq_lens;
     a.lens_stride = 1;
     a.addr.kv_dim = (int32_t)kv_dim;
-    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
-    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    CRUCIBLE_CHECK(paged_addr(n_layer, layer, kv_dim, a.addr), CRUCIBLE_ERR_INVALID,
+                   "%s: page geometry of %lld layers x %lld channels overflows", what,
+                   (long long)n_layer, (long long)kv_dim);
     a.table_stride = (int32_t)table_stride;
     if (head_dim != kHeadDim)
         return launch_decode_generic(a, (int)head_dim, q_dtype == CRUCIBLE_F32, stream, what);
@@ -1548,8 +1564,9 @@ extern "C" int crucible_attention_decode_paged_append(
     a.kv_new_f16 = kv_dtype == CRUCIBLE_F16;
     a.kv_new_stride = (int32_t)kv_dim;
     a.addr.kv_dim = (int32_t)kv_dim;
-    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
-    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    CRUCIBLE_CHECK(paged_addr(n_layer, layer, kv_dim, a.addr), CRUCIBLE_ERR_INVALID,
+                   "%s: page geometry of %lld layers x %lld channels overflows", what,
+                   (long long)n_layer, (long long)kv_dim);
     a.table_stride = (int32_t)table_stride;
     if (head_dim != kHeadDim) {
         if (const int rc = append_rows_generic(a, kv_dtype, n_layer, layer, stream)) return rc;
@@ -1593,8 +1610,9 @@ extern "C" int crucible_attention_decode_paged_append_noalloc(
     a.kv_new_f16 = kv_dtype == CRUCIBLE_F16;
     a.kv_new_stride = (int32_t)kv_dim;
     a.addr.kv_dim = (int32_t)kv_dim;
-    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
-    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    CRUCIBLE_CHECK(paged_addr(n_layer, layer, kv_dim, a.addr), CRUCIBLE_ERR_INVALID,
+                   "%s: page geometry of %lld layers x %lld channels overflows", what,
+                   (long long)n_layer, (long long)kv_dim);
     a.table_stride = (int32_t)table_stride;
     if (head_dim != kHeadDim) {  // the generic kernels use no scratch
         if (const int rc = append_rows_generic(a, kv_dtype, n_layer, layer, stream)) return rc;
@@ -1610,7 +1628,9 @@ extern "C" int crucible_attention_decode_paged_append_noalloc(
     a.n_splits = (a.max_pages + split_pages - 1) / split_pages;
     if (a.n_splits > 1) {
         // the limits of the static scratch: counters and partials
-        const size_t partial_bytes = partial_floats(a.batch, a.n_head, a.n_splits) * sizeof(float);
+        const size_t floats = partial_floats(a.batch, a.n_head, a.n_splits);
+        const size_t partial_bytes =
+            floats > SIZE_MAX / sizeof(float) ? SIZE_MAX : floats * sizeof(float);
         CRUCIBLE_CHECK((int64_t)a.batch * a.n_kv_head <= kScratchCounters &&
                            partial_bytes <= kScratchBytes - kScratchCounterBytes,
                        CRUCIBLE_ERR_WORKSPACE,
@@ -1682,8 +1702,9 @@ extern "C" int crucible_attention_decode_qkv_paged_append(
     a.rope_sin = rope_sin;
     a.rope_max_pos = (int)rope_max_pos;
     a.addr.kv_dim = (int32_t)kv_dim;
-    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
-    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    CRUCIBLE_CHECK(paged_addr(n_layer, layer, kv_dim, a.addr), CRUCIBLE_ERR_INVALID,
+                   "%s: page geometry of %lld layers x %lld channels overflows", what,
+                   (long long)n_layer, (long long)kv_dim);
     a.table_stride = (int32_t)table_stride;
     if (head_dim != kHeadDim) {
         const int64_t threads = batch * n_kv_head * (head_dim / 2);
@@ -1704,7 +1725,10 @@ extern "C" int crucible_attention_decode_kernel_name(int64_t batch, int64_t n_he
                                                      int64_t n_kv_head, int64_t max_seq,
                                                      int q_dtype, int entry, char* buf,
                                                      size_t n) {
-    if (!buf || n == 0 || batch <= 0 || n_head <= 0 || n_kv_head <= 0 || max_seq <= 0 ||
+    // the entry points' own limits (batch and max_seq up to INT32_MAX, n_head up to 2^20, a
+    // positive multiple of n_kv_head)
+    if (!buf || n == 0 || batch <= 0 || batch > INT32_MAX || n_head <= 0 || n_head > (1 << 20) ||
+        n_kv_head <= 0 || n_head % n_kv_head != 0 || max_seq <= 0 || max_seq > INT32_MAX ||
         entry < 0 || entry > 2) {
         set_error(CRUCIBLE_ERR_INVALID, "decode_kernel_name: bad arguments");
         return CRUCIBLE_ERR_INVALID;
@@ -1743,8 +1767,12 @@ extern "C" int crucible_attention_decode(const void* q, int q_dtype, const void*
     if (int rc = check_geometry(what, n_head, n_kv_head, head_dim, cache_stride)) return rc;
     CRUCIBLE_CHECK(q && k_cache && v_cache && out && params, CRUCIBLE_ERR_INVALID,
                    "%s: null buffer", what);
-    CRUCIBLE_CHECK(max_seq > 0 && max_seq <= INT32_MAX && layer_base >= 0, CRUCIBLE_ERR_INVALID,
+    CRUCIBLE_CHECK(max_seq > 0 && max_seq <= INT32_MAX, CRUCIBLE_ERR_INVALID,
                    "%s: max_seq %lld", what, (long long)max_seq);
+    // the last position's element index, layer_base + max_seq * cache_stride, fits int64
+    // (max_seq * cache_stride < 2^59 after the checks above)
+    CRUCIBLE_CHECK(layer_base >= 0 && layer_base <= INT64_MAX - max_seq * cache_stride,
+                   CRUCIBLE_ERR_INVALID, "%s: layer_base %lld", what, (long long)layer_base);
     DecodeArgs a = common_args(q, k_cache, v_cache, out, out_dtype, 1, n_head, n_kv_head,
                                max_seq, head_dim);
     a.lens = params;
@@ -1772,8 +1800,10 @@ extern "C" int crucible_attention_split(const void* q, int q_dtype, const void* 
     CRUCIBLE_CHECK(q && k_cache && v_cache && out && params && partial_o && partial_m &&
                        partial_l,
                    CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
-    CRUCIBLE_CHECK(capacity > 0 && capacity <= INT32_MAX && layer_base >= 0,
-                   CRUCIBLE_ERR_INVALID, "%s: capacity %lld", what, (long long)capacity);
+    CRUCIBLE_CHECK(capacity > 0 && capacity <= INT32_MAX, CRUCIBLE_ERR_INVALID,
+                   "%s: capacity %lld", what, (long long)capacity);
+    CRUCIBLE_CHECK(layer_base >= 0 && layer_base <= INT64_MAX - capacity * cache_stride,
+                   CRUCIBLE_ERR_INVALID, "%s: layer_base %lld", what, (long long)layer_base);
     DecodeArgs a = common_args(q, k_cache, v_cache, out, out_dtype, 1, n_head, n_kv_head,
                                capacity, head_dim);
     a.lens = params;

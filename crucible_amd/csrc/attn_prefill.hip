@@ -1887,13 +1887,14 @@ int check_prefill(const char* what, int q_dtype, int out_dtype, int64_t n_head,
     CRUCIBLE_CHECK(n_head > 0 && n_kv_head > 0 && n_head % n_kv_head == 0, CRUCIBLE_ERR_INVALID,
                    "%s: n_head %lld must be a positive multiple of n_kv_head %lld", what,
                    (long long)n_head, (long long)n_kv_head);
+    // before any product of the head counts: n_kv_head <= n_head <= 2^20 from here on
+    CRUCIBLE_CHECK(n_head <= (1 << 20), CRUCIBLE_ERR_INVALID, "%s: n_head too large", what);
     CRUCIBLE_CHECK(head_dim == kHeadDim || generic_head_dim_ok(head_dim),
                    CRUCIBLE_ERR_UNSUPPORTED,
                    "%s: head_dim %lld unsupported (a multiple of 8 up to %d)", what,
                    (long long)head_dim, kGenericMaxHeadDim);
     CRUCIBLE_CHECK(kv_dim == n_kv_head * head_dim, CRUCIBLE_ERR_INVALID,
                    "%s: kv_dim %lld != n_kv_head * head_dim", what, (long long)kv_dim);
-    CRUCIBLE_CHECK(n_head <= (1 << 20), CRUCIBLE_ERR_INVALID, "%s: n_head too large", what);
     return CRUCIBLE_OK;
 }
 
@@ -1944,8 +1945,9 @@ extern "C" int crucible_attention_prefill_paged(const void* q, int q_dtype, cons
     a.tables = page_table;
     a.params = params;
     a.rows = rows;
-    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
-    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    CRUCIBLE_CHECK(paged_addr(n_layer, layer, kv_dim, a.addr), CRUCIBLE_ERR_INVALID,
+                   "%s: page geometry of %lld layers x %lld channels overflows", what,
+                   (long long)n_layer, (long long)kv_dim);
     if (head_dim != kHeadDim)
         return launch_prefill_generic(a, (int)head_dim, rows, 1, q_dtype == CRUCIBLE_F32, stream,
                                       what);
@@ -1967,8 +1969,8 @@ extern "C" int crucible_attention_prefill_packed(
     CRUCIBLE_CHECK(n_layer > 0 && layer >= 0 && layer < n_layer, CRUCIBLE_ERR_INVALID,
                    "%s: layer %lld outside n_layer %lld", what, (long long)layer,
                    (long long)n_layer);
-    CRUCIBLE_CHECK(table_stride > 0 && max_seq > 0 && max_seq <= table_stride * kPageTokens &&
-                       max_seq <= INT32_MAX,
+    CRUCIBLE_CHECK(table_stride > 0 && table_stride <= INT32_MAX && max_seq > 0 &&
+                       max_seq <= table_stride * kPageTokens && max_seq <= INT32_MAX,
                    CRUCIBLE_ERR_INVALID, "%s: max_seq %lld must be in 1..table_stride*16", what,
                    (long long)max_seq);
     PrefillArgs a = base_args(q, k_pool, v_pool, out, out_dtype, n_head, n_kv_head, kv_dim, max_seq);
@@ -1978,8 +1980,9 @@ extern "C" int crucible_attention_prefill_packed(
     a.positions = positions;
     a.rows = rows;
     a.table_stride = table_stride;
-    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
-    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    CRUCIBLE_CHECK(paged_addr(n_layer, layer, kv_dim, a.addr), CRUCIBLE_ERR_INVALID,
+                   "%s: page geometry of %lld layers x %lld channels overflows", what,
+                   (long long)n_layer, (long long)kv_dim);
     if (head_dim != kHeadDim)
         return launch_prefill_generic(a, (int)head_dim, rows, 1, q_dtype == CRUCIBLE_F32, stream,
                                       what);
@@ -1998,8 +2001,9 @@ extern "C" int crucible_attention_prefill_tiled(
     CRUCIBLE_CHECK(!hybrid || (current_k && current_v), CRUCIBLE_ERR_INVALID,
                    "%s: hybrid needs the chunk's current K/V rows", what);
     // Launch checks of gpu.rs:1680-1719.
-    CRUCIBLE_CHECK(requests > 0 && max_chunk > 0 && table_stride > 0 && n_layer > 0 &&
-                       layer >= 0 && layer < n_layer && requests <= 65535,
+    CRUCIBLE_CHECK(requests > 0 && max_chunk > 0 && max_chunk <= INT32_MAX && table_stride > 0 &&
+                       table_stride <= INT32_MAX / kPageTokens && n_layer > 0 && layer >= 0 &&
+                       layer < n_layer && requests <= 65535,
                    CRUCIBLE_ERR_INVALID, "%s: invalid launch dimensions", what);
     CRUCIBLE_CHECK(q && k_pool && v_pool && out && tables && segments, CRUCIBLE_ERR_INVALID,
                    "%s: null buffer", what);
@@ -2012,8 +2016,9 @@ extern "C" int crucible_attention_prefill_tiled(
     a.tables = tables;
     a.segments = segments;
     a.table_stride = table_stride;
-    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
-    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    CRUCIBLE_CHECK(paged_addr(n_layer, layer, kv_dim, a.addr), CRUCIBLE_ERR_INVALID,
+                   "%s: page geometry of %lld layers x %lld channels overflows", what,
+                   (long long)n_layer, (long long)kv_dim);
     a.hybrid = hybrid != 0;
     a.cur_k = static_cast<const float*>(current_k);
     a.cur_v = static_cast<const float*>(current_v);
@@ -2036,9 +2041,13 @@ extern "C" int crucible_attention_prefill(const void* q, int q_dtype, const void
     CRUCIBLE_CHECK(rows >= 0 && rows <= INT32_MAX, CRUCIBLE_ERR_INVALID, "%s: rows", what);
     if (rows == 0) return CRUCIBLE_OK;
     CRUCIBLE_CHECK(q && k_cache && v_cache && out, CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
-    CRUCIBLE_CHECK(max_seq > 0 && max_seq <= INT32_MAX && layer_base >= 0 && pos_offset >= 0 &&
-                       pos_offset + rows <= max_seq,
+    CRUCIBLE_CHECK(max_seq > 0 && max_seq <= INT32_MAX && pos_offset >= 0 &&
+                       pos_offset <= max_seq && rows <= max_seq - pos_offset,
                    CRUCIBLE_ERR_INVALID, "%s: rows past max_seq", what);
+    // the last position's element index, layer_base + max_seq * cache_stride, fits int64
+    // (max_seq * cache_stride < 2^59 after the checks above)
+    CRUCIBLE_CHECK(layer_base >= 0 && layer_base <= INT64_MAX - max_seq * cache_stride,
+                   CRUCIBLE_ERR_INVALID, "%s: layer_base %lld", what, (long long)layer_base);
     PrefillArgs a = base_args(q, k_cache, v_cache, out, out_dtype, n_head, n_kv_head,
                               cache_stride, max_seq);
     a.mode = kContig;

@@ -164,6 +164,26 @@ int tuning(int key);
 // CUs of the current device (256 on MI355X), queried once per device: the launch-shape
 // choices compare grids against it.
 int device_cu_count();
+// a * b * c for non-negative factors, or -1 when a factor is negative or the product does
+// not fit int64 (argument validation computes sizes with it before anything uses them)
+inline int64_t checked_mul(int64_t a, int64_t b, int64_t c = 1) {
+    int64_t r;
+    if (a < 0 || b < 0 || c < 0 || __builtin_mul_overflow(a, b, &r) ||
+        __builtin_mul_overflow(r, c, &r))
+        return -1;
+    return r;
+}
+// The element offsets of a paged pool: layer `layer`'s block of page p starts at
+// p * page_stride + layer_off. False when the layer is outside n_layer or a page id up to
+// INT32_MAX (any int32 table entry) would not give an int64 offset.
+inline bool paged_addr(int64_t n_layer, int64_t layer, int64_t kv_dim, PoolAddr& out) {
+    const int64_t stride = checked_mul(n_layer, kPageTokens, kv_dim);
+    if (stride <= 0 || checked_mul(stride, INT32_MAX) < 0 || layer < 0 || layer >= n_layer)
+        return false;
+    out.page_stride = stride;
+    out.layer_off = layer * kPageTokens * kv_dim;  // below stride
+    return true;
+}
 inline bool dtype_ok(int d) { return d == CRUCIBLE_F32 || d == CRUCIBLE_F16; }
 inline bool kind_ok(int k) { return k == CRUCIBLE_POOL_K || k == CRUCIBLE_POOL_V; }
 

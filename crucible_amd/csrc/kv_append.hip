@@ -114,8 +114,9 @@ int check_common(const char* what, const void* src, int src_dtype, const void* p
     CRUCIBLE_CHECK(dtype_ok(src_dtype), CRUCIBLE_ERR_INVALID, "%s: bad src dtype %d", what,
                    src_dtype);
     CRUCIBLE_CHECK(kind_ok(kind), CRUCIBLE_ERR_INVALID, "%s: bad pool kind %d", what, kind);
-    CRUCIBLE_CHECK(rows >= 0 && kv_dim > 0 && kv_dim <= INT32_MAX, CRUCIBLE_ERR_INVALID,
-                   "%s: rows=%lld kv_dim=%lld", what, (long long)rows, (long long)kv_dim);
+    CRUCIBLE_CHECK(rows >= 0 && rows <= INT32_MAX && kv_dim > 0 && kv_dim <= INT32_MAX,
+                   CRUCIBLE_ERR_INVALID, "%s: rows=%lld kv_dim=%lld", what, (long long)rows,
+                   (long long)kv_dim);
     CRUCIBLE_CHECK(rows == 0 || (src && pool), CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
     return CRUCIBLE_OK;
 }
@@ -137,8 +138,9 @@ int check_paged(const char* what, int64_t n_layer, int64_t layer, int64_t table_
     CRUCIBLE_CHECK(n_layer > 0 && layer >= 0 && layer < n_layer, CRUCIBLE_ERR_INVALID,
                    "%s: layer %lld outside n_layer %lld", what, (long long)layer,
                    (long long)n_layer);
-    CRUCIBLE_CHECK(!need_stride || table_stride > 0, CRUCIBLE_ERR_INVALID,
-                   "%s: table_stride must be positive", what);
+    CRUCIBLE_CHECK(!need_stride || (table_stride > 0 && table_stride <= INT32_MAX),
+                   CRUCIBLE_ERR_INVALID, "%s: table_stride %lld outside 1..INT32_MAX", what,
+                   (long long)table_stride);
     return CRUCIBLE_OK;
 }
 
@@ -152,8 +154,13 @@ extern "C" int crucible_cache_store(const void* src, int src_dtype, void* cache,
                                     int64_t pos_offset, crucible_stream_t stream) {
     const char* what = "cache_store";
     if (int rc = check_common(what, src, src_dtype, cache, kind, rows, kv_dim)) return rc;
-    CRUCIBLE_CHECK(layer_base >= 0 && pos_offset >= 0, CRUCIBLE_ERR_INVALID,
-                   "%s: negative layer_base/pos_offset", what);
+    CRUCIBLE_CHECK(layer_base >= 0 && pos_offset >= 0 && pos_offset <= INT32_MAX,
+                   CRUCIBLE_ERR_INVALID, "%s: layer_base %lld, pos_offset %lld", what,
+                   (long long)layer_base, (long long)pos_offset);
+    // the last row's element index, layer_base + (pos_offset + rows) * kv_dim, fits int64
+    const int64_t span = checked_mul(pos_offset + rows, kv_dim);
+    CRUCIBLE_CHECK(span >= 0 && layer_base <= INT64_MAX - span, CRUCIBLE_ERR_INVALID,
+                   "%s: cache offsets overflow", what);
     AppendArgs a = base_args(src, src_dtype, cache, kind, rows, kv_dim);
     a.mode = kContig;
     a.pos_offset = pos_offset;
@@ -175,8 +182,9 @@ extern "C" int crucible_cache_store_paged(const void* src, int src_dtype, void* 
     a.mode = kParams;
     a.tables = page_table;
     a.params = params;
-    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
-    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    CRUCIBLE_CHECK(paged_addr(n_layer, layer, kv_dim, a.addr), CRUCIBLE_ERR_INVALID,
+                   "%s: page geometry of %lld layers x %lld channels overflows", what,
+                   (long long)n_layer, (long long)kv_dim);
     return launch_append(a, stream, what);
 }
 
@@ -196,8 +204,9 @@ extern "C" int crucible_cache_store_rows_paged(const void* src, int src_dtype, v
     a.tables = page_tables;
     a.positions = positions;
     a.table_stride = table_stride;
-    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
-    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    CRUCIBLE_CHECK(paged_addr(n_layer, layer, kv_dim, a.addr), CRUCIBLE_ERR_INVALID,
+                   "%s: page geometry of %lld layers x %lld channels overflows", what,
+                   (long long)n_layer, (long long)kv_dim);
     return launch_append(a, stream, what);
 }
 
@@ -219,7 +228,8 @@ extern "C" int crucible_cache_store_packed_paged(const void* src, int src_dtype,
     a.owners = owners;
     a.positions = positions;
     a.table_stride = table_stride;
-    a.addr.page_stride = n_layer * kPageTokens * kv_dim;
-    a.addr.layer_off = layer * kPageTokens * kv_dim;
+    CRUCIBLE_CHECK(paged_addr(n_layer, layer, kv_dim, a.addr), CRUCIBLE_ERR_INVALID,
+                   "%s: page geometry of %lld layers x %lld channels overflows", what,
+                   (long long)n_layer, (long long)kv_dim);
     return launch_append(a, stream, what);
 }

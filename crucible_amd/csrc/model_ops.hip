@@ -954,9 +954,10 @@ int check_linear(const char* what, const float* x, int64_t ldx, const float* nor
                    what, (long long)n_out);
     CRUCIBLE_CHECK(k_in > 0 && k_in % 32 == 0 && k_in <= (1 << 20), CRUCIBLE_ERR_UNSUPPORTED,
                    "%s: k_in %lld must be a positive multiple of 32", what, (long long)k_in);
-    CRUCIBLE_CHECK(ldx >= k_in && ldx % 4 == 0 && ldo >= n_out, CRUCIBLE_ERR_INVALID,
-                   "%s: leading dimensions (ldx %lld, ldo %lld)", what, (long long)ldx,
-                   (long long)ldo);
+    CRUCIBLE_CHECK(ldx >= k_in && ldx % 4 == 0 && ldo >= n_out && ldx <= INT32_MAX &&
+                       ldo <= INT32_MAX,
+                   CRUCIBLE_ERR_INVALID, "%s: leading dimensions (ldx %lld, ldo %lld)", what,
+                   (long long)ldx, (long long)ldo);
     CRUCIBLE_CHECK(aligned16(x) && aligned16(w) && (!norm_w || aligned16(norm_w)),
                    CRUCIBLE_ERR_INVALID, "%s: x, w and norm_w must be 16-byte aligned", what);
     return CRUCIBLE_OK;
@@ -1075,7 +1076,7 @@ extern "C" int crucible_rmsnorm_rows(const float* x, int64_t ldx, const float* w
     const char* what = "crucible_rmsnorm_rows";
     CRUCIBLE_CHECK(x && w && out, CRUCIBLE_ERR_INVALID, "%s: null buffer", what);
     CRUCIBLE_CHECK(rows >= 0 && rows <= INT32_MAX && n > 0 && n <= INT32_MAX && ldx >= n &&
-                       ldo >= n,
+                       ldo >= n && ldx <= INT32_MAX && ldo <= INT32_MAX,
                    CRUCIBLE_ERR_INVALID, "%s: bad shape", what);
     if (rows == 0) return CRUCIBLE_OK;
     hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0,
@@ -1096,7 +1097,8 @@ extern "C" int crucible_rope_split_qkv(const float* qkv, int64_t ld, float* q, f
                    "%s: head_dim %lld unsupported (an even number up to 4096)", what,
                    (long long)head_dim);
     CRUCIBLE_CHECK(n_head > 0 && n_kv_head > 0 && n_head <= 4096 && n_kv_head <= 4096 &&
-                       ld >= (n_head + 2 * n_kv_head) * head_dim && max_pos > 0 &&
+                       ld >= (n_head + 2 * n_kv_head) * head_dim && ld <= INT32_MAX &&
+                       max_pos > 0 &&
                        max_pos <= INT32_MAX && rows >= 0 && rows <= (1 << 24),
                    CRUCIBLE_ERR_INVALID, "%s: bad shape", what);
     if (rows == 0) return CRUCIBLE_OK;

@@ -1,15 +1,38 @@
 // Paged KV bookkeeping (see paging.hpp) and its C API from crucible_attn.h.
 #include "paging.hpp"
 
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 
 namespace crucible {
 
-PagePool::PagePool(int64_t n_pages, int64_t n_layer, int64_t kv_dim)
-    : n_pages_(n_pages), page_elems_(n_layer * kPagingTokens * kv_dim), in_use_(n_pages, false) {
-    if (n_pages < 0 || n_pages > (int64_t)UINT32_MAX)
+namespace {
+// The pool's shape, checked before anything is allocated: page ids reach the device in
+// int32 tables, so a pool holds at most 2^31 pages, and the byte count of both pools
+// (2 x pages x elements x 2 bytes) must fit int64.
+int64_t checked_pages(int64_t n_pages) {
+    if (n_pages < 0 || n_pages > (int64_t)INT32_MAX + 1)
         throw PagingError("page count out of range");
+    return n_pages;
+}
+
+int64_t checked_page_elems(int64_t n_pages, int64_t n_layer, int64_t kv_dim) {
+    if (n_layer <= 0 || kv_dim <= 0) throw PagingError("n_layer and kv_dim must be positive");
+    int64_t elems, bytes;
+    if (__builtin_mul_overflow(n_layer, kPagingTokens, &elems) ||
+        __builtin_mul_overflow(elems, kv_dim, &elems) ||
+        __builtin_mul_overflow(elems, (int64_t)4, &bytes) ||
+        __builtin_mul_overflow(bytes, n_pages, &bytes))
+        throw PagingError("pool size overflows");
+    return elems;
+}
+}  // namespace
+
+PagePool::PagePool(int64_t n_pages, int64_t n_layer, int64_t kv_dim)
+    : n_pages_(checked_pages(n_pages)),
+      page_elems_(checked_page_elems(n_pages, n_layer, kv_dim)),
+      in_use_((size_t)n_pages, false) {
     free_.reserve(n_pages);
     // Reverse order so the first allocation is page 0 (paged.rs:76-78).
     for (int64_t i = n_pages; i-- > 0;) free_.push_back((uint32_t)i);
@@ -43,6 +66,7 @@ std::pair<uint32_t, int64_t> SequencePages::translate(int64_t pos) const {
 
 void SequencePages::grow(PagePool& pool, int64_t extra) {
     if (extra < 0) throw PagingError("negative growth");
+    if (extra > INT64_MAX - kPagingTokens - len_) throw PagingError("growth overflows");
     const int64_t target = len_ + extra;
     const int64_t needed = (target + kPagingTokens - 1) / kPagingTokens;
     std::vector<uint32_t> taken;
@@ -75,7 +99,10 @@ std::vector<int32_t> SequencePages::table_padded(int64_t stride) const {
 int64_t request_page_reservation(int64_t prompt, int64_t generated, int64_t context) {
     if (prompt <= 0 || generated <= 0)
         throw PagingError("prompt length and output token budget must be positive");
-    const int64_t positions = prompt + (generated - 1);
+    int64_t positions;
+    if (__builtin_add_overflow(prompt, generated - 1, &positions) ||
+        positions > INT64_MAX - kPagingTokens)
+        throw PagingError("request length overflows");
     if (positions > context)
         throw PagingError("request needs " + std::to_string(positions) +
                           " cache positions, capacity is " + std::to_string(context));

@@ -149,13 +149,14 @@ int crucible_cache_store_packed_paged(const void* src, int src_dtype, void* pool
  * (RoPE rows: one append launch) before it, and attention_split leaves its partial
  * buffers untouched. The same holds for the prefill entries below.
  * The split-K partials live in a caller-provided workspace of at least
- * crucible_attention_decode_workspace_bytes(...) bytes (no allocation here),
- * 16-byte aligned. It starts with a fixed region of 65536 u32 counters, one per
- * (request, kv head) (so batch * n_kv_head <= 65536; one per 64-byte line while
- * batch * n_kv_head <= 4096, so that the splits' atomics on different counters do
- * not queue on one line), that order the in-kernel combine of the splits: zero the
- * workspace once when it is allocated; every launch leaves the counters zeroed again. A unit plan follows, also at a fixed
- * place (1.5 MiB): launches of batch <= 64 in the compact grid order record there
+ * crucible_attention_decode_workspace_bytes(...) bytes (no allocation here; 0 for an
+ * empty batch, SIZE_MAX for a shape past the entry points' limits), 16-byte aligned.
+ * It starts with a fixed region of 65536 u32 counters, one per (request, kv head) (so
+ * batch * n_kv_head <= 65536; one per 64-byte line while batch * n_kv_head <= 4096,
+ * so that the splits' atomics on different counters do not queue on one line), that
+ * order the in-kernel combine of the splits: zero the workspace once when it is
+ * allocated; every launch leaves the counters zeroed again. A unit plan follows, also
+ * at a fixed place (1.5 MiB): launches of batch <= 64 in the compact grid order record there
  * which (request, kv head, split) each workgroup served and its page ids, with
  * the lengths, positions and launch shape they came from; a later launch on the
  * same workspace whose lengths, positions and shape are equal loads its unit in

@@ -22,7 +22,11 @@
  *   - Return value: CRUCIBLE_OK (0) or an error code. Argument validation
  *     happens before any launch; on error nothing is enqueued. The message of
  *     the last error on the calling thread is available from
- *     crucible_attn_last_error().
+ *     crucible_attn_last_error(). Sizes are bounded so that no offset a kernel
+ *     computes can overflow int64: counts of rows, requests, positions, strides and
+ *     leading dimensions at most INT32_MAX, n_head at most 2^20, and a paged pool's
+ *     page stride (n_layer * 16 * kv_dim elements) such that any int32 page id gives
+ *     an int64 offset.
  *   - Page geometry is the reference's: 16-token pages, page = table[pos >> 4],
  *     slot = pos & 15, and a page holds every layer. Element offsets of the
  *     (page, layer) block are ((page * n_layer + layer) * 16) * kv_dim.

@@ -21,7 +21,7 @@ PAGE_TOKENS = 16
 TUNE_KEYS = {"decode_pages": 0, "decode_waves": 1, "decode_order": 2, "prefill_direct": 3,
              "prefill_heavy_first": 4, "prefill_qb": 5, "prefill_bufs": 6, "linear_tile": 7,
              "decode_combine_width": 8, "prefill_p16": 9,
-             "prefill_m32": 10, "prefill_persist": 11}
+             "prefill_m32": 10, "prefill_persist": 11, "linear_prefetch": 12}
 DECODE_ORDERS = {"split": 0, "request": 1, "compact": 2}
 
 _P = ctypes.c_void_p
@@ -59,6 +59,10 @@ SIGNATURES = {
                                 _P], _I),
     "crucible_linear_swiglu_f64acc": ([_P, _I64, _P, ctypes.c_float, _P, _P, _I64, _I64, _P,
                                        _I64, _I64, _P], _I),
+    "crucible_linear_f64acc_prefetch": ([_P, _I64, _P, ctypes.c_float, _P, _I64, _I64, _P, _P,
+                                         _I64, _I64, _P, _I64, _P], _I),
+    "crucible_linear_swiglu_f64acc_prefetch": ([_P, _I64, _P, ctypes.c_float, _P, _P, _I64,
+                                                _I64, _P, _I64, _I64, _P, _I64, _P], _I),
     "crucible_rmsnorm_rows": ([_P, _I64, _P, ctypes.c_float, _P, _I64, _I64, _I64, _P], _I),
     "crucible_rope_split_qkv": ([_P, _I64, _P, _P, _P, _P, _P, _P] + [_I64] * 5 + [_P], _I),
     "crucible_segments_from_cu_seqlens": ([_P, _I64, _P, _P], _I64),

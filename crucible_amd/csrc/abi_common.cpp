@@ -62,6 +62,7 @@ constexpr TuneKey kTuneKeys[CRUCIBLE_TUNE_COUNT] = {
     {"CRUCIBLE_PREFILL_P16", 0, 1},           // prefill P operand: fp16 hi + lo / one fp16
     {"CRUCIBLE_PREFILL_M32", 0, 1},           // prefill 32-row waves on 32x32 MFMAs off / on
     {"CRUCIBLE_PREFILL_PERSIST", 0, 65536},   // prefill persistent LDS form off / on / n workgroups
+    {"CRUCIBLE_LINEAR_PREFETCH", 0, 1},       // projections' next-kernel prefetch off / on
 };
 
 bool tune_value_ok(int key, int v) {
@@ -86,7 +87,8 @@ int parse_env(int key, const char* s) {
     const long v = std::strtol(s, &end, 10);
     if (end == s || *end != '\0') return -1;
     if (key == CRUCIBLE_TUNE_PREFILL_DIRECT || key == CRUCIBLE_TUNE_PREFILL_HEAVY_FIRST ||
-        key == CRUCIBLE_TUNE_PREFILL_P16 || key == CRUCIBLE_TUNE_PREFILL_M32)
+        key == CRUCIBLE_TUNE_PREFILL_P16 || key == CRUCIBLE_TUNE_PREFILL_M32 ||
+        key == CRUCIBLE_TUNE_LINEAR_PREFETCH)
         return v != 0;
     return tune_value_ok(key, (int)v) ? (int)v : -1;
 }

@@ -60,12 +60,55 @@ struct LinArgs {
     int rows;
     int n_out;
     int k_in;
+    const unsigned char* pf;  // read-only bytes the next kernel will read (or nullptr)
+    int64_t pf_bytes;         // their length; whole 64-byte lines are fetched
+    int pf_per;               // 64-byte lines a workgroup fetches (set by the launcher)
 };
+
+// ---------------------------------------------------------------- next-kernel prefetch
+//
+// A decode step's projections are short kernels, each waiting once for a cold HBM round
+// trip of its weights (the step streams more bytes than the last-level cache holds, so
+// they are evicted between steps). Given the next kernel's read-only operands (pf: the
+// next projection's weights), each workgroup loads one 4-byte word of every 64-byte line
+// of its share of them, right after it has issued its own loads, so that those lines are
+// in the last-level cache when the next kernel asks. A wave's loads complete in issue
+// order, so no wait for the wave's own operands (issued earlier) waits for these; the words
+// are consumed by an empty asm statement at the kernel's end, which is the only wait for
+// them. The loads are buffer loads whose range check drops the lines outside the
+// workgroup's share (and all of them when there is no prefetch): no branch around them,
+// so the compiler's count of the loads in flight stays exact.
+constexpr int kPfPerThread = 4;  // at most 4 x 512 lines (128 KB) a workgroup
+
+struct Prefetch {
+    uint32_t v[kPfPerThread];
+};
+
+template <int THREADS>
+__device__ __forceinline__ Prefetch prefetch_issue(const LinArgs& a) {
+    const int64_t lines = a.pf_bytes >> 6;
+    const int64_t l0 = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * a.pf_per;
+    int64_t n = lines - l0 < a.pf_per ? lines - l0 : a.pf_per;  // this workgroup's lines
+    n = n < 0 ? 0 : n;
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(a.pf + (n > 0 ? l0 * 64 : 0), (uint32_t)(n * 64));
+    Prefetch p;
+#pragma unroll
+    for (int i = 0; i < kPfPerThread; ++i)
+        p.v[i] = __builtin_amdgcn_raw_buffer_load_b32(
+            r, (uint32_t)(threadIdx.x + i * THREADS) * 64u, 0, 0);
+    return p;
+}
+
+__device__ __forceinline__ void prefetch_retire(const Prefetch& p) {
+#pragma unroll
+    for (int i = 0; i < kPfPerThread; ++i) asm volatile("" ::"v"(p.v[i]));
+}
 
 template <int NB>
 struct Chunk {
     float4_t x0, x1;
     half8_t w[NB];
+    float4_t n0, n1;  // fused-norm weights of the chunk's 8 k (loaded under NORM only)
 };
 
 // out tile = 16 rows x (16 * NB) columns. kSwiGLU (NB = 1): 8 output columns, whose gate
@@ -167,21 +210,25 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
         c.x1 = *reinterpret_cast<const float4_t*>(xp + k0 + 4);
 #pragma unroll
         for (int j = 0; j < NB; ++j) c.w[j] = *reinterpret_cast<const half8_t*>(wp[j] + k0);
+        if constexpr (NORM) {
+            c.n0 = *reinterpret_cast<const float4_t*>(nwp + k0);
+            c.n1 = *reinterpret_cast<const float4_t*>(nwp + k0 + 4);
+        }
         return c;
     };
 
     double4_t acc[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[j] = double4_t{0.0, 0.0, 0.0, 0.0};
+    Prefetch pf{};
 
     // One chunk into the accumulators: the activations (normalised first under NORM)
     // and the weights go to f64, 8 MFMA steps per column block.
     auto feed = [&](const Chunk<NB>& ch, int k0, double scale) {
         float xs[8] = {ch.x0[0], ch.x0[1], ch.x0[2], ch.x0[3], ch.x1[0], ch.x1[1], ch.x1[2], ch.x1[3]};
         if constexpr (NORM) {
-            const float4_t w0 = *reinterpret_cast<const float4_t*>(nwp + k0);
-            const float4_t w1 = *reinterpret_cast<const float4_t*>(nwp + k0 + 4);
-            const float nw[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+            const float nw[8] = {ch.n0[0], ch.n0[1], ch.n0[2], ch.n0[3],
+                                 ch.n1[0], ch.n1[1], ch.n1[2], ch.n1[3]};
 #pragma unroll
             for (int i = 0; i < 8; ++i) xs[i] = (float)((double)xs[i] * scale) * nw[i];
         }
@@ -205,6 +252,8 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
 #pragma unroll
         for (int c = 0; c < RC; ++c)
             if (c < nch) ch[c] = load(c * kLinK);
+        pf = prefetch_issue<kLinThreads>(a);
+        __builtin_amdgcn_sched_barrier(0);  // issued now, not after the waits below
         double ss = 0.0;
 #pragma unroll
         for (int c = 0; c < RC; ++c) {
@@ -239,6 +288,7 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
 #pragma unroll
             for (int c = 0; c < BATCH; ++c)
                 if (b0 + c * kLinK < kw) ch[c] = load(b0 + c * kLinK);
+            if (b0 == 0) pf = prefetch_issue<kLinThreads>(a);
 #pragma unroll
             for (int c = 0; c < BATCH; ++c) {
                 if (b0 + c * kLinK >= kw) break;
@@ -270,6 +320,7 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
                 a.out[(int64_t)orow * a.ldo + n0 + c] = gf / (1.0f + expf(-gf)) * (float)u;
             }
         }
+        prefetch_retire(pf);
         return;
     }
 #pragma unroll
@@ -291,6 +342,7 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinArgs a) {
             *dst = (float)y;
         }
     }
+    prefetch_retire(pf);
 }
 
 // ---------------------------------------------------------------- 4-column tiles
@@ -382,19 +434,23 @@ __global__ __launch_bounds__(kLinThreads, 4) void linear4_kernel(LinArgs a) {
         c.x1 = *reinterpret_cast<const float4_t*>(xp + k0 + 4);
 #pragma unroll
         for (int j = 0; j < G; ++j) c.w[j] = *reinterpret_cast<const half8_t*>(wp[j] + k0);
+        if constexpr (NORM) {
+            c.n0 = *reinterpret_cast<const float4_t*>(nwp + k0);
+            c.n1 = *reinterpret_cast<const float4_t*>(nwp + k0 + 4);
+        }
         return c;
     };
 
     double acc[G][2];
 #pragma unroll
     for (int j = 0; j < G; ++j) acc[j][0] = acc[j][1] = 0.0;
+    Prefetch pf{};
 
     auto feed = [&](const Chunk<G>& ch, int k0, double scale) {
         float xs[8] = {ch.x0[0], ch.x0[1], ch.x0[2], ch.x0[3], ch.x1[0], ch.x1[1], ch.x1[2], ch.x1[3]};
         if constexpr (NORM) {
-            const float4_t w0 = *reinterpret_cast<const float4_t*>(nwp + k0);
-            const float4_t w1 = *reinterpret_cast<const float4_t*>(nwp + k0 + 4);
-            const float nw[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+            const float nw[8] = {ch.n0[0], ch.n0[1], ch.n0[2], ch.n0[3],
+                                 ch.n1[0], ch.n1[1], ch.n1[2], ch.n1[3]};
 #pragma unroll
             for (int i = 0; i < 8; ++i) xs[i] = (float)((double)xs[i] * scale) * nw[i];
         }
@@ -415,6 +471,8 @@ __global__ __launch_bounds__(kLinThreads, 4) void linear4_kernel(LinArgs a) {
 #pragma unroll
         for (int c = 0; c < RC; ++c)
             if (c < nch) ch[c] = load(c * kLinK);
+        pf = prefetch_issue<kLinThreads>(a);
+        __builtin_amdgcn_sched_barrier(0);  // issued now, not after the waits below
         double ss = 0.0;
 #pragma unroll
         for (int c = 0; c < RC; ++c) {
@@ -449,6 +507,7 @@ __global__ __launch_bounds__(kLinThreads, 4) void linear4_kernel(LinArgs a) {
 #pragma unroll
             for (int c = 0; c < BATCH; ++c)
                 if (b0 + c * kLinK < kw) ch[c] = load(b0 + c * kLinK);
+            if (b0 == 0) pf = prefetch_issue<kLinThreads>(a);
 #pragma unroll
             for (int c = 0; c < BATCH; ++c) {
                 if (b0 + c * kLinK >= kw) break;
@@ -460,24 +519,26 @@ __global__ __launch_bounds__(kLinThreads, 4) void linear4_kernel(LinArgs a) {
 #pragma unroll
     for (int j = 0; j < G; ++j) s_red[wave][j][lane] = acc[j][0] + acc[j][1];
     __syncthreads();
-    if (!out_ok) return;
-    // fixed summation order over the waves
-    double y[G];
+    if (out_ok) {
+        // fixed summation order over the waves
+        double y[G];
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-        y[j] = 0.0;
+        for (int j = 0; j < G; ++j) {
+            y[j] = 0.0;
 #pragma unroll
-        for (int w = 0; w < kLinWaves; ++w) y[j] += s_red[w][j][lane];
+            for (int w = 0; w < kLinWaves; ++w) y[j] += s_red[w][j][lane];
+        }
+        float* dst = a.out + (int64_t)orow * a.ldo + ocol;
+        if constexpr (MODE == kSwiGLU) {
+            const float gf = (float)y[0];
+            *dst = gf / (1.0f + expf(-gf)) * (float)y[G - 1];
+        } else if constexpr (MODE == kResidual) {
+            *dst = rv + (float)y[0];
+        } else {
+            *dst = (float)y[0];
+        }
     }
-    float* dst = a.out + (int64_t)orow * a.ldo + ocol;
-    if constexpr (MODE == kSwiGLU) {
-        const float gf = (float)y[0];
-        *dst = gf / (1.0f + expf(-gf)) * (float)y[G - 1];
-    } else if constexpr (MODE == kResidual) {
-        *dst = rv + (float)y[0];
-    } else {
-        *dst = (float)y[0];
-    }
+    prefetch_retire(pf);
 }
 
 // ---------------------------------------------------------------- wide projections
@@ -897,17 +958,28 @@ __global__ void rope_split_kernel(const float* __restrict__ qkv, int64_t ld, flo
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// The prefetch's lines a workgroup: the region spread evenly over the grid, at most
+// kPfPerThread lines a thread.
+LinArgs with_prefetch_share(LinArgs a, const dim3& grid) {
+    const int64_t n_wg = (int64_t)grid.x * grid.y;
+    const int64_t lines = a.pf_bytes >> 6;
+    a.pf_per = (int)std::min<int64_t>((lines + n_wg - 1) / n_wg, kPfPerThread * kLinThreads);
+    return a;
+}
+
 template <bool NORM, int MODE, int NB>
 void launch_linear(const LinArgs& a, hipStream_t stream) {
     const int cols = MODE == kSwiGLU ? 8 : 16 * NB;
     const dim3 grid((unsigned)((a.n_out + cols - 1) / cols), (unsigned)((a.rows + 15) / 16));
-    hipLaunchKernelGGL((linear_kernel<NORM, MODE, NB>), grid, dim3(kLinThreads), 0, stream, a);
+    hipLaunchKernelGGL((linear_kernel<NORM, MODE, NB>), grid, dim3(kLinThreads), 0, stream,
+                       with_prefetch_share(a, grid));
 }
 
 template <bool NORM, int MODE>
 void launch_linear4(const LinArgs& a, hipStream_t stream) {
     const dim3 grid((unsigned)((a.n_out + 3) / 4), (unsigned)((a.rows + 15) / 16));
-    hipLaunchKernelGGL((linear4_kernel<NORM, MODE>), grid, dim3(kLinThreads), 0, stream, a);
+    hipLaunchKernelGGL((linear4_kernel<NORM, MODE>), grid, dim3(kLinThreads), 0, stream,
+                       with_prefetch_share(a, grid));
 }
 
 template <bool NORM, int MODE, int RB, int CB>
@@ -963,17 +1035,28 @@ int check_linear(const char* what, const float* x, int64_t ldx, const float* nor
     return CRUCIBLE_OK;
 }
 
-}  // namespace
-}  // namespace crucible
+int check_prefetch(const char* what, const void* pf, int64_t pf_bytes) {
+    CRUCIBLE_CHECK(pf_bytes >= 0 && pf_bytes % 64 == 0 && (pf_bytes == 0 || pf) &&
+                       ((uintptr_t)pf & 3) == 0,
+                   CRUCIBLE_ERR_INVALID,
+                   "%s: prefetch (%p, %lld bytes) must be 4-byte aligned, a multiple of 64 bytes",
+                   what, pf, (long long)pf_bytes);
+    return CRUCIBLE_OK;
+}
 
-using namespace crucible;
+// The prefetch region as the kernels take it: none when the tuning key turns it off.
+void set_prefetch(LinArgs& a, const void* pf, int64_t pf_bytes) {
+    if (tuning(CRUCIBLE_TUNE_LINEAR_PREFETCH) == 0) pf_bytes = 0;
+    a.pf = pf_bytes > 0 ? static_cast<const unsigned char*>(pf) : nullptr;
+    a.pf_bytes = pf_bytes;
+}
 
-extern "C" int crucible_linear_f64acc(const float* x, int64_t ldx, const float* norm_w, float eps,
-                                      const void* w, int64_t n_out, int64_t k_in,
-                                      const float* resid, float* out, int64_t ldo, int64_t rows,
-                                      crucible_stream_t stream) {
-    const char* what = "crucible_linear_f64acc";
-    const int rc = check_linear(what, x, ldx, norm_w, w, n_out, k_in, out, ldo, rows);
+int linear_f64acc(const char* what, const float* x, int64_t ldx, const float* norm_w, float eps,
+                  const void* w, int64_t n_out, int64_t k_in, const float* resid, float* out,
+                  int64_t ldo, int64_t rows, const void* pf, int64_t pf_bytes,
+                  crucible_stream_t stream) {
+    int rc = check_linear(what, x, ldx, norm_w, w, n_out, k_in, out, ldo, rows);
+    if (rc == CRUCIBLE_OK) rc = check_prefetch(what, pf, pf_bytes);
     if (rc != CRUCIBLE_OK) return rc;
     if (rows == 0) return CRUCIBLE_OK;
     LinArgs a{x, ldx, norm_w, (double)eps, static_cast<const half_t*>(w), nullptr, resid, out,
@@ -984,6 +1067,7 @@ extern "C" int crucible_linear_f64acc(const float* x, int64_t ldx, const float* 
         else launch_gemm_mode<kPlain>(a, s);
         return fail_launch(what);
     }
+    set_prefetch(a, pf, pf_bytes);
     // Wide outputs (the vocabulary projection): the persistent tile walk when the K range
     // fits its registers, else 4 column blocks per workgroup so each activation fragment
     // feeds 4 MFMAs; narrow ones keep a workgroup per 16 columns.
@@ -994,6 +1078,8 @@ extern "C" int crucible_linear_f64acc(const float* x, int64_t ldx, const float* 
                            ((rows - 1) * ldx + k_in) * 4 < (1LL << 31) &&
                            ((rows - 1) * ldo + n_out) * 4 < (1LL << 31);
     if (wide && !resid && wide_rc <= 4 && wide_fits) {
+        a.pf = nullptr;  // the persistent walk streams its own tiles to the end
+        a.pf_bytes = 0;
         const int64_t row_blocks = (rows + 15) / 16;
         const int64_t tiles = (n_out + 15) / 16;
         // one workgroup per CU (and row block), or more when a CU would need more than
@@ -1040,13 +1126,12 @@ extern "C" int crucible_linear_f64acc(const float* x, int64_t ldx, const float* 
     return fail_launch(what);
 }
 
-extern "C" int crucible_linear_swiglu_f64acc(const float* x, int64_t ldx, const float* norm_w,
-                                             float eps, const void* w_gate, const void* w_up,
-                                             int64_t hidden, int64_t k_in, float* out,
-                                             int64_t ldo, int64_t rows,
-                                             crucible_stream_t stream) {
-    const char* what = "crucible_linear_swiglu_f64acc";
+int linear_swiglu_f64acc(const char* what, const float* x, int64_t ldx, const float* norm_w,
+                         float eps, const void* w_gate, const void* w_up, int64_t hidden,
+                         int64_t k_in, float* out, int64_t ldo, int64_t rows, const void* pf,
+                         int64_t pf_bytes, crucible_stream_t stream) {
     int rc = check_linear(what, x, ldx, norm_w, w_gate, hidden, k_in, out, ldo, rows);
+    if (rc == CRUCIBLE_OK) rc = check_prefetch(what, pf, pf_bytes);
     if (rc != CRUCIBLE_OK) return rc;
     CRUCIBLE_CHECK(w_up && aligned16(w_up), CRUCIBLE_ERR_INVALID,
                    "%s: w_up must be a 16-byte aligned buffer", what);
@@ -1059,6 +1144,7 @@ extern "C" int crucible_linear_swiglu_f64acc(const float* x, int64_t ldx, const 
         launch_gemm_mode<kSwiGLU>(a, s);
         return fail_launch(what);
     }
+    set_prefetch(a, pf, pf_bytes);
     if (use_tile4(hidden, rows, 8, norm_w != nullptr)) {
         if (norm_w) launch_linear4<true, kSwiGLU>(a, s);
         else launch_linear4<false, kSwiGLU>(a, s);
@@ -1068,6 +1154,50 @@ extern "C" int crucible_linear_swiglu_f64acc(const float* x, int64_t ldx, const 
         launch_linear<false, kSwiGLU, 1>(a, s);
     }
     return fail_launch(what);
+}
+
+}  // namespace
+}  // namespace crucible
+
+using namespace crucible;
+
+extern "C" int crucible_linear_f64acc(const float* x, int64_t ldx, const float* norm_w, float eps,
+                                      const void* w, int64_t n_out, int64_t k_in,
+                                      const float* resid, float* out, int64_t ldo, int64_t rows,
+                                      crucible_stream_t stream) {
+    return linear_f64acc("crucible_linear_f64acc", x, ldx, norm_w, eps, w, n_out, k_in, resid,
+                         out, ldo, rows, nullptr, 0, stream);
+}
+
+extern "C" int crucible_linear_f64acc_prefetch(const float* x, int64_t ldx, const float* norm_w,
+                                               float eps, const void* w, int64_t n_out,
+                                               int64_t k_in, const float* resid, float* out,
+                                               int64_t ldo, int64_t rows, const void* prefetch,
+                                               int64_t prefetch_bytes, crucible_stream_t stream) {
+    return linear_f64acc("crucible_linear_f64acc_prefetch", x, ldx, norm_w, eps, w, n_out, k_in,
+                         resid, out, ldo, rows, prefetch, prefetch_bytes, stream);
+}
+
+extern "C" int crucible_linear_swiglu_f64acc(const float* x, int64_t ldx, const float* norm_w,
+                                             float eps, const void* w_gate, const void* w_up,
+                                             int64_t hidden, int64_t k_in, float* out,
+                                             int64_t ldo, int64_t rows,
+                                             crucible_stream_t stream) {
+    return linear_swiglu_f64acc("crucible_linear_swiglu_f64acc", x, ldx, norm_w, eps, w_gate,
+                                w_up, hidden, k_in, out, ldo, rows, nullptr, 0, stream);
+}
+
+extern "C" int crucible_linear_swiglu_f64acc_prefetch(const float* x, int64_t ldx,
+                                                      const float* norm_w, float eps,
+                                                      const void* w_gate, const void* w_up,
+                                                      int64_t hidden, int64_t k_in, float* out,
+                                                      int64_t ldo, int64_t rows,
+                                                      const void* prefetch,
+                                                      int64_t prefetch_bytes,
+                                                      crucible_stream_t stream) {
+    return linear_swiglu_f64acc("crucible_linear_swiglu_f64acc_prefetch", x, ldx, norm_w, eps,
+                                w_gate, w_up, hidden, k_in, out, ldo, rows, prefetch,
+                                prefetch_bytes, stream);
 }
 
 extern "C" int crucible_rmsnorm_rows(const float* x, int64_t ldx, const float* w, float eps,

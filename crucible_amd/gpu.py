@@ -55,12 +55,19 @@ def _need(t, what, *, dtype=None, numel=None):
     return t
 
 
+def _prefetch_region(t):
+    """(pointer, bytes) of a prefetch tensor: contiguous on the device, whole 64-byte lines
+    (a trailing partial line is left out)."""
+    _need(t, "prefetch")
+    return _ptr(t), (t.numel() * t.element_size()) // 64 * 64
+
+
 def set_tuning(**overrides) -> None:
     """Force launch shapes for every later launch in the process (crucible_attn_set_tuning):
     decode_pages, decode_waves, decode_order ("split" | "request" | "compact"),
     prefill_direct, prefill_heavy_first, prefill_qb, prefill_bufs, linear_tile,
-    decode_combine_width, prefill_p16, prefill_m32, prefill_persist. None returns a key to the
-    launcher's own choice."""
+    decode_combine_width, prefill_p16, prefill_m32, prefill_persist, linear_prefetch. None
+    returns a key to the launcher's own choice."""
     lib = _lib.load()
     for name, value in overrides.items():
         if name not in _lib.TUNE_KEYS:
@@ -340,10 +347,12 @@ class Gpu:
             self._stream()))
 
     # ------------------------------------------------------------- decode-step glue
-    def linear_f64acc(self, x, w, out, *, norm_w=None, eps=1e-6, resid=None):
+    def linear_f64acc(self, x, w, out, *, norm_w=None, eps=1e-6, resid=None, prefetch=None):
         """out = [resid +] f32(f64-accumulated h . w^T), h = x or rmsnorm(x, norm_w)
         (ops.rs:17-32 matvec, :39-52 rmsnorm). x [rows][k_in] f32, w [n_out][k_in] fp16,
-        out (and resid) [rows][n_out] f32; resid may be out itself."""
+        out (and resid) [rows][n_out] f32; resid may be out itself. prefetch: a contiguous
+        device tensor the next kernel reads (its next projection's weights), fetched into
+        the last-level cache during this product (crucible_linear_f64acc_prefetch)."""
         rows, k_in = x.shape
         n_out = w.shape[0]
         _need(x, "x", dtype=torch.float32)
@@ -353,14 +362,20 @@ class Gpu:
             _need(norm_w, "norm_w", dtype=torch.float32, numel=k_in)
         if resid is not None:
             _need(resid, "resid", dtype=torch.float32, numel=rows * n_out)
-        _lib.check(self.lib.crucible_linear_f64acc(
-            _ptr(x), k_in, _ptr(norm_w) if norm_w is not None else None, float(eps), _ptr(w),
-            n_out, k_in, _ptr(resid) if resid is not None else None, _ptr(out), n_out, rows,
-            self._stream()))
+        args = (_ptr(x), k_in, _ptr(norm_w) if norm_w is not None else None, float(eps),
+                _ptr(w), n_out, k_in, _ptr(resid) if resid is not None else None, _ptr(out),
+                n_out, rows)
+        if prefetch is None:
+            _lib.check(self.lib.crucible_linear_f64acc(*args, self._stream()))
+        else:
+            _lib.check(self.lib.crucible_linear_f64acc_prefetch(
+                *args, *_prefetch_region(prefetch), self._stream()))
 
-    def linear_swiglu_f64acc(self, x, w_gate, w_up, out, *, norm_w=None, eps=1e-6):
+    def linear_swiglu_f64acc(self, x, w_gate, w_up, out, *, norm_w=None, eps=1e-6,
+                             prefetch=None):
         """out = silu(g) * u with g, u the f64-accumulated projections of
-        rmsnorm(x, norm_w) (or x) by w_gate and w_up (model.rs:252-262)."""
+        rmsnorm(x, norm_w) (or x) by w_gate and w_up (model.rs:252-262). prefetch: as for
+        linear_f64acc."""
         rows, k_in = x.shape
         hidden = w_gate.shape[0]
         _need(x, "x", dtype=torch.float32)
@@ -369,9 +384,13 @@ class Gpu:
         _need(out, "out", dtype=torch.float32, numel=rows * hidden)
         if norm_w is not None:
             _need(norm_w, "norm_w", dtype=torch.float32, numel=k_in)
-        _lib.check(self.lib.crucible_linear_swiglu_f64acc(
-            _ptr(x), k_in, _ptr(norm_w) if norm_w is not None else None, float(eps),
-            _ptr(w_gate), _ptr(w_up), hidden, k_in, _ptr(out), hidden, rows, self._stream()))
+        args = (_ptr(x), k_in, _ptr(norm_w) if norm_w is not None else None, float(eps),
+                _ptr(w_gate), _ptr(w_up), hidden, k_in, _ptr(out), hidden, rows)
+        if prefetch is None:
+            _lib.check(self.lib.crucible_linear_swiglu_f64acc(*args, self._stream()))
+        else:
+            _lib.check(self.lib.crucible_linear_swiglu_f64acc_prefetch(
+                *args, *_prefetch_region(prefetch), self._stream()))
 
     def rmsnorm_rows(self, x, w, out, eps=1e-6):
         """ops.rs:39-52 on every row of x [rows][n]."""

@@ -147,6 +147,10 @@ class GpuModel:
         self.layers = []
         for i in range(cfg.n_layer):
             p = f"blocks.{i}"
+            # gate and up rows in one buffer, so the o projection can prefetch both as one
+            # region
+            wgu = torch.cat([h16(f"{p}.mlp.gate_proj.weight"),
+                             h16(f"{p}.mlp.up_proj.weight")]).contiguous()
             self.layers.append({
                 "attn_norm": f32(f"{p}.attn_norm.weight"),
                 "wqkv": torch.cat([h16(f"{p}.attn.q_proj.weight"),
@@ -154,8 +158,9 @@ class GpuModel:
                                    h16(f"{p}.attn.v_proj.weight")]).contiguous(),
                 "wo": h16(f"{p}.attn.o_proj.weight"),
                 "mlp_norm": f32(f"{p}.mlp_norm.weight"),
-                "wg": h16(f"{p}.mlp.gate_proj.weight"),
-                "wu": h16(f"{p}.mlp.up_proj.weight"),
+                "wgu": wgu,
+                "wg": wgu[:cfg.hidden],
+                "wu": wgu[cfg.hidden:],
                 "wd": h16(f"{p}.mlp.down_proj.weight"),
             })
         self.final_norm = f32("final_norm.weight")
@@ -342,8 +347,12 @@ class GpuModel:
         b = st["batch"]
         eps = float(np.float32(cfg.norm_eps))
         x = st["x"]
+        # Each projection fetches the next one's weights into the last-level cache while it
+        # runs (the step streams more than that cache holds, so they would arrive cold).
         for layer_i, layer in enumerate(self.layers):
-            gpu.linear_f64acc(x, layer["wqkv"], st["qkv"], norm_w=layer["attn_norm"], eps=eps)
+            nxt = self.layers[layer_i + 1]["wqkv"] if layer_i + 1 < cfg.n_layer else None
+            gpu.linear_f64acc(x, layer["wqkv"], st["qkv"], norm_w=layer["attn_norm"], eps=eps,
+                              prefetch=layer["wo"])
             # RoPE of q and k, both appends and attention: one launch on the fused rows
             gpu.attention_decode_qkv_paged_append(st["qkv"], self.rope_cos, self.rope_sin,
                                                   self.k_pool, self.v_pool, st["attn"],
@@ -352,10 +361,10 @@ class GpuModel:
                                                   self.table_stride, cfg.n_layer, layer_i,
                                                   cfg.kv_dim, self.capacity,
                                                   workspace=self.workspace)
-            gpu.linear_f64acc(st["attn"], layer["wo"], x, resid=x)
+            gpu.linear_f64acc(st["attn"], layer["wo"], x, resid=x, prefetch=layer["wgu"])
             gpu.linear_swiglu_f64acc(x, layer["wg"], layer["wu"], st["act"],
-                                     norm_w=layer["mlp_norm"], eps=eps)
-            gpu.linear_f64acc(st["act"], layer["wd"], x, resid=x)
+                                     norm_w=layer["mlp_norm"], eps=eps, prefetch=layer["wd"])
+            gpu.linear_f64acc(st["act"], layer["wd"], x, resid=x, prefetch=nxt)
         gpu.linear_f64acc(x, self.lm_head, st["logits"], norm_w=self.final_norm, eps=eps)
         gpu.greedy_advance(st["logits"], self.tok_emb, x, st["tokens"], st["history"],
                            st["step"], st["positions"], st["lens"], st["done"])

@@ -97,7 +97,9 @@ enum crucible_tuning_key {
                                               (a static longest-first list of the row tiles that
                                               hold rows): 0 off (default), 1 one workgroup per
                                               resident slot, n >= 2 a grid of n workgroups */
-    CRUCIBLE_TUNE_COUNT = 12
+    CRUCIBLE_TUNE_LINEAR_PREFETCH = 12,    /* the _prefetch projections' next-kernel prefetch:
+                                              1 on (default), 0 off */
+    CRUCIBLE_TUNE_COUNT = 13
 };
 int crucible_attn_set_tuning(int key, int value);
 /* Current value of a key (-1: automatic, or an unknown key). */
@@ -405,6 +407,28 @@ int crucible_linear_swiglu_f64acc(const float* x, int64_t ldx, const float* norm
                                   const void* w_gate, const void* w_up, int64_t hidden,
                                   int64_t k_in, float* out, int64_t ldo, int64_t rows,
                                   crucible_stream_t stream);
+
+/* The two products above, with a prefetch of the next kernel's read-only operands: the
+ * prefetch_bytes bytes at prefetch (typically the next projection's weights) are read, one
+ * word per 64-byte line, by the product's workgroups right after they have issued their own
+ * loads, so that the next kernel finds them in the last-level cache instead of waiting a
+ * cold HBM round trip. The outputs are those of the plain entry points, bit for bit; only
+ * the decode-sized tilings (rows below the prompt-sized GEMM's threshold) issue it, and at
+ * most 128 KB a workgroup. prefetch may be NULL with prefetch_bytes 0; otherwise it must be
+ * 4-byte aligned and prefetch_bytes a non-negative multiple of 64; its memory must stay
+ * allocated until the launch completes. CRUCIBLE_TUNE_LINEAR_PREFETCH = 0 turns the
+ * prefetch off. No counterpart in the reference: its decode step launches the same kernels
+ * back to back, each waiting for its weights (gpu_model.rs:1393-1605). */
+int crucible_linear_f64acc_prefetch(const float* x, int64_t ldx, const float* norm_w, float eps,
+                                    const void* w, int64_t n_out, int64_t k_in,
+                                    const float* resid, float* out, int64_t ldo, int64_t rows,
+                                    const void* prefetch, int64_t prefetch_bytes,
+                                    crucible_stream_t stream);
+int crucible_linear_swiglu_f64acc_prefetch(const float* x, int64_t ldx, const float* norm_w,
+                                           float eps, const void* w_gate, const void* w_up,
+                                           int64_t hidden, int64_t k_in, float* out,
+                                           int64_t ldo, int64_t rows, const void* prefetch,
+                                           int64_t prefetch_bytes, crucible_stream_t stream);
 
 /* RMSNorm of each row (ops.rs:39-52; replaces rmsnorm_batch_f32, kernels.cu:968-996). */
 int crucible_rmsnorm_rows(const float* x, int64_t ldx, const float* w, float eps, float* out,

@@ -147,6 +147,14 @@ std::vector<Entry> entries() {
         return crucible_linear_swiglu_f64acc(FF, a[0], FF, 1e-5f, F, F, a[1], a[2], FW, a[3],
                                              a[4], nullptr);
     }});
+    e.push_back({"linear_f64acc_prefetch", {768, 1152, 768, 1152, 16, 1 << 20}, [](V a) {
+        return crucible_linear_f64acc_prefetch(FF, a[0], FF, 1e-5f, F, a[1], a[2], nullptr, FW,
+                                               a[3], a[4], F, a[5], nullptr);
+    }});
+    e.push_back({"linear_swiglu_f64acc_prefetch", {768, 3072, 768, 3072, 16, 1 << 20}, [](V a) {
+        return crucible_linear_swiglu_f64acc_prefetch(FF, a[0], FF, 1e-5f, F, F, a[1], a[2], FW,
+                                                      a[3], a[4], F, a[5], nullptr);
+    }});
     e.push_back({"rmsnorm_rows", {768, 768, 16, 768}, [](V a) {
         return crucible_rmsnorm_rows(FF, a[0], FF, 1e-5f, FW, a[1], a[2], a[3], nullptr);
     }});
@@ -258,6 +266,19 @@ void explicit_cases() {
     expect("linear misaligned x",
            crucible_linear_f64acc(reinterpret_cast<const float*>(0x1004), 128, nullptr, 1e-6f, F,
                                   64, 128, nullptr, FW, 64, 4, nullptr),
+           CRUCIBLE_ERR_INVALID);
+    expect("linear prefetch not whole 64-byte lines",
+           crucible_linear_f64acc_prefetch(FF, 128, nullptr, 1e-6f, F, 64, 128, nullptr, FW, 64, 4,
+                                           F, 100, nullptr),
+           CRUCIBLE_ERR_INVALID);
+    expect("linear prefetch misaligned",
+           crucible_linear_swiglu_f64acc_prefetch(FF, 128, nullptr, 1e-6f, F, F, 64, 128, FW, 64,
+                                                  4, reinterpret_cast<const void*>(0x1002), 64,
+                                                  nullptr),
+           CRUCIBLE_ERR_INVALID);
+    expect("linear prefetch bytes without a buffer",
+           crucible_linear_f64acc_prefetch(FF, 128, nullptr, 1e-6f, F, 64, 128, nullptr, FW, 64, 4,
+                                           nullptr, 64, nullptr),
            CRUCIBLE_ERR_INVALID);
     expect("rope odd head_dim",
            crucible_rope_split_qkv(FF, 1152, FW, FW, FW, FF, FF, FI, 16, 12, 3, 63, 1024, nullptr),

@@ -117,6 +117,46 @@ def test_swiglu_matches_reference_ops(gpu, dev, tune, rows, hidden, k_in, tile):
     assert np.all(np.abs(got - want) <= 8 * 2.0 ** -24 * np.abs(want) + 1e-30)
 
 
+# the decode step's four projections at batch 16, and ragged shapes
+PREFETCH_SHAPES = [("qkv", 16, 1280, 768, True, False), ("o", 16, 768, 768, False, True),
+                   ("down", 16, 768, 2048, False, True), ("ragged", 5, 200, 2048, True, False),
+                   ("small", 7, 203, 160, False, True)]
+
+
+@pytest.mark.parametrize("tile", ["auto", "4", "16"])
+@pytest.mark.parametrize("pf_bytes", [100, 2 << 20, 64 << 20])
+def test_prefetch_variants_write_the_plain_products(gpu, dev, tune, tile, pf_bytes):
+    """The _prefetch entry points, with a region of one line, of a projection's weights and
+    of more than the grid fetches (128 KB a workgroup), write the plain entry points' bits;
+    the region is read only. The tuning key's off setting does the same."""
+    if tile != "auto":
+        tune(linear_tile=tile)
+    rng = np.random.default_rng(pf_bytes % 1000 + len(tile))
+    region = torch.from_numpy(rng.integers(0, 255, pf_bytes, dtype=np.uint8)).to(dev)
+    region_before = region.clone()
+    for name, rows, n_out, k_in, norm, resid in PREFETCH_SHAPES:
+        x = torch.from_numpy(rng.standard_normal((rows, k_in), dtype=np.float32)).to(dev)
+        w = torch.from_numpy(_mat(rng, (n_out, k_in), 0.02)).to(dev)
+        nw = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(k_in)).astype(np.float32)).to(dev)
+        r = torch.from_numpy(rng.standard_normal((rows, n_out), dtype=np.float32)).to(dev)
+        kw = dict(norm_w=nw if norm else None, eps=float(EPS))
+        want = r.clone()
+        gpu.linear_f64acc(x, w, want, resid=want if resid else None, **kw)
+        for setting in (None, 0):
+            tune(linear_prefetch=setting)
+            got = r.clone()
+            gpu.linear_f64acc(x, w, got, resid=got if resid else None, prefetch=region, **kw)
+            assert torch.equal(got, want), (name, setting)
+        tune(linear_prefetch=None)
+        wg = torch.from_numpy(_mat(rng, (n_out, k_in), 0.05)).to(dev)
+        want = torch.full((rows, n_out), np.nan, device=dev)
+        gpu.linear_swiglu_f64acc(x, w, wg, want, **kw)
+        got = torch.full_like(want, np.nan)
+        gpu.linear_swiglu_f64acc(x, w, wg, got, prefetch=region, **kw)
+        assert torch.equal(got, want), (name, "swiglu")
+    assert torch.equal(region, region_before)
+
+
 def test_rmsnorm_rows(gpu, dev):
     rng = np.random.default_rng(3)
     x = (rng.standard_normal((7, 768), dtype=np.float32) * 3).astype(np.float32)

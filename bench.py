@@ -789,7 +789,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the attention path shards by sequence or KV head, see DESIGN.md)",
+              "(a multi-GPU run would shard the attention path by sequence or KV head)",
               file=sys.stderr)
         sys.exit(2)
     import numpy as np  # noqa: F401

@@ -257,7 +257,7 @@ int crucible_attention_decode_paged_append_noalloc(
 
 /* The same fused step fed straight from the fused q/k/v projection, with the RoPE of
  * the reference's decode step (rope_rows before the K append and on q, gpu_model.rs:1424-1444;
- * RopeTable::apply, ops.rs:124-135) applied in the same launch (§8f rank 2). Row b of qkv
+ * RopeTable::apply, ops.rs:124-135) applied in the same launch. Row b of qkv
  * (f32, row stride qkv_row_stride, a multiple of 4) holds q (n_head*head_dim), k (kv_dim),
  * v (kv_dim). q and k are rotated at positions[b] with rope_cos/rope_sin
  * ([rope_max_pos][head_dim/2] f32, 16-byte aligned, rope_max_pos >= max_seq; both NULL: no

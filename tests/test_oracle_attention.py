@@ -78,7 +78,7 @@ def test_closed_forms():
 
 
 def test_reference_order_f32_agrees_with_f64():
-    """model.rs-order f32 attention vs the f64 definition (SURVEY build-plan gate 1e-5)."""
+    """model.rs-order f32 attention vs the f64 definition, within 1e-5."""
     rng = np.random.default_rng(11)
     n_head, n_kv, hd, S = 12, 3, 64, 1024
     q = rng.standard_normal((4, n_head * hd)).astype(np.float32)
